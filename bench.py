@@ -1,0 +1,264 @@
+"""Benchmark of the torch_spyre MI355X hot path (one JSON line on stdout).
+
+Headline (BASELINE.json metric, configs[1]): fp16 GEMM C = A @ B with
+M = N = K = 4096, A, B ~ U(-1, 1) from seed 0xAFFE, fp32 accumulate, on one
+MI355X.  A step is one GEMM over resident HBM inputs.  Secondary figures for
+the other hot-path kernels (config 1 softmax, config 2 bmm, config 3 norms and
+GELU chain) are reported under "extra", each against its roofline.
+
+Kernel durations are taken with HIP events on the stream the kernels run on;
+the CPU baseline times the oracle (numpy, CPU) on a bounded slice of the same
+workload on this host's cores.
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "torch-spyre_amd"))
+sys.path.insert(0, os.path.join(REPO, "tests"))
+sys.path.insert(0, REPO)
+
+PEAK_FP16_TFLOPS = 2516.6   # MI355X dense fp16 MFMA (256 CU x 4096 FLOP/clk x 2.4 GHz)
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+SEED = 0xAFFE
+
+
+def _log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _gen(k):
+    import torch
+
+    return torch.Generator().manual_seed(SEED + k)
+
+
+class Timer:
+    """HIP-event timing of `fn` launched `steps` times on `stream`."""
+
+    def __init__(self, stream):
+        import torch
+
+        self.torch = torch
+        self.stream = stream
+
+    def run(self, fn, steps, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        start.record(self.stream)
+        for _ in range(steps):
+            fn()
+        end.record(self.stream)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / steps
+        return start.elapsed_time(end) / steps, wall
+
+
+def _traffic_for(kernel_key):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, calibrated against a copy kernel), committed under
+    profiles/traffic.json; None when that measurement is absent."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kernel_key, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def bench_gemm(steps, warmup, stream, capi):
+    import torch
+
+    M = N = K = 4096
+    a = (torch.rand(M, K, generator=_gen(0)) * 2 - 1).half().cuda()
+    b = (torch.rand(K, N, generator=_gen(1)) * 2 - 1).half().cuda()
+    d = torch.empty(M, N, dtype=torch.float16, device="cuda")
+    s = stream.cuda_stream
+    lib = capi.lib()
+
+    def step():
+        rc = lib.sph_gemm_f16(M, N, K, a.data_ptr(), b.data_ptr(), d.data_ptr(), s)
+        if rc:
+            capi.check(rc, "sph_gemm_f16")
+
+    kernel_ms, wall_ms = Timer(stream).run(step, steps, warmup)
+    flop = 2.0 * M * N * K
+    return {"kernel_ms": kernel_ms, "wall_ms": wall_ms, "flop": flop,
+            "tflops": flop / (kernel_ms * 1e-3) / 1e12, "a": a, "b": b, "d": d}
+
+
+def bench_extra(steps, warmup, stream, capi):
+    """Secondary kernels: bytes / FLOPs per launch and roofline fractions."""
+    import torch
+
+    s = stream.cuda_stream
+    lib = capi.lib()
+    out = {}
+    timer = Timer(stream)
+
+    def hbm_entry(name, key, nbytes, fn):
+        ms, _ = timer.run(fn, steps, warmup)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us_per_launch": round(ms * 1e3, 2), "algorithmic_bytes": nbytes,
+                     "GB/s": round(gbs, 1), "roofline_frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "bound": "hbm", "traffic": _traffic_for(key)}
+
+    # c1 softmax [512, 4096] fp16, N(0,1)*4.  Cold-cache variant rotates 80
+    # input/output pairs (640 MiB > MALL) so each launch reads from HBM.
+    R, C = 512, 4096
+    x = (torch.randn(R, C, generator=_gen(0)) * 4).half().cuda()
+    y = torch.empty_like(x)
+    hbm_entry("c1_softmax_512x4096_hot", "softmax", 2 * R * C * 2,
+              lambda: lib.sph_softmax_rows_f16(x.data_ptr(), y.data_ptr(), R, C, s))
+    xs = [x.clone() for _ in range(80)]
+    ys = [torch.empty_like(x) for _ in range(80)]
+    it = [0]
+
+    def cold_softmax():
+        i = it[0] = (it[0] + 1) % 80
+        lib.sph_softmax_rows_f16(xs[i].data_ptr(), ys[i].data_ptr(), R, C, s)
+
+    hbm_entry("c1_softmax_512x4096_cold", "softmax", 2 * R * C * 2, cold_softmax)
+    del xs, ys
+
+    # c3 residual add + RMSNorm / LayerNorm, GELU chain: [8192, 4096] fp16
+    R, C = 8192, 4096
+    x = torch.randn(R, C, generator=_gen(0)).half().cuda()
+    r = torch.randn(R, C, generator=_gen(1)).half().cuda()
+    w = (torch.randn(C, generator=_gen(2)) * 0.02 + 1).half().cuda()
+    bb = (torch.randn(C, generator=_gen(3)) * 0.02).half().cuda()
+    yy = torch.empty_like(x)
+    h = torch.empty_like(x)
+    hbm_entry("c3_add_rmsnorm_8192x4096", "rmsnorm", 4 * R * C * 2 + C * 2,
+              lambda: lib.sph_rmsnorm_f16(x.data_ptr(), r.data_ptr(), w.data_ptr(),
+                                          yy.data_ptr(), h.data_ptr(), R, C, 1e-5, s))
+    hbm_entry("c3_add_layernorm_8192x4096", "layernorm", 4 * R * C * 2 + 2 * C * 2,
+              lambda: lib.sph_layernorm_f16(x.data_ptr(), r.data_ptr(), w.data_ptr(),
+                                            bb.data_ptr(), yy.data_ptr(), h.data_ptr(), R, C,
+                                            1e-5, s))
+    rs = torch.empty(R, dtype=torch.float16, device="cuda")
+    hbm_entry("c3_gelu_affine_rowsum_8192x4096", "gelu_rowsum", 2 * R * C * 2 + 2 * C * 2 + R * 2,
+              lambda: lib.sph_gelu_affine_rowsum_f16(x.data_ptr(), w.data_ptr(), bb.data_ptr(),
+                                                     yy.data_ptr(), rs.data_ptr(), R, C, s))
+    del x, r, yy, h
+
+    # c2 bmm 32 x [2048,128] x [128,2048]: HBM-bound (AI 113.8 < ridge 314.6)
+    Bt, M, N, K = 32, 2048, 2048, 128
+    A = (torch.rand(Bt, M, K, generator=_gen(0)) * 2 - 1).half().cuda()
+    Bm = (torch.rand(Bt, K, N, generator=_gen(1)) * 2 - 1).half().cuda()
+    D = torch.empty(Bt, M, N, dtype=torch.float16, device="cuda")
+    ms, _ = timer.run(lambda: lib.sph_bmm_f16(Bt, M, N, K, A.data_ptr(), Bm.data_ptr(),
+                                              D.data_ptr(), s), steps, warmup)
+    nbytes = (Bt * M * K + Bt * K * N + Bt * M * N) * 2
+    flop = 2.0 * Bt * M * N * K
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    out["c2_bmm_32x2048x2048x128"] = {
+        "us_per_launch": round(ms * 1e3, 2), "algorithmic_bytes": nbytes,
+        "GB/s": round(gbs, 1), "roofline_frac": round(gbs / PEAK_HBM_GBS, 4), "bound": "hbm",
+        "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1), "traffic": _traffic_for("bmm")}
+    return out
+
+
+def cpu_baseline_gemm(a, b):
+    """Oracle GEMM (numpy fp32) on a bounded row slice of the same problem,
+    timed on this host's cores."""
+    import numpy as np
+
+    from oracle import ops as O
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        cores = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+    except Exception:
+        cores = os.cpu_count() or 1
+    rows = 512
+    an = a[:rows].float().cpu().numpy()
+    bn = b.float().cpu().numpy()
+    O.gemm(an[:64], bn)  # warm the BLAS pool
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.gemm(an, bn)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > 5.0 or reps >= 20:
+            break
+    flop = 2.0 * rows * b.shape[0] * b.shape[1] * reps
+    return {"value": round(flop / el / 1e12, 4), "unit": "TFLOP/s", "cores": int(cores),
+            "kind": "port",
+            "sample": f"oracle.ops.gemm (numpy fp32 BLAS) on rows 0..{rows} of the 4096^3 "
+                      f"problem, {reps} reps, {el:.1f} s"}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one MI355X; runs on more than one GPU are not "
+              "part of it (see DESIGN.md, 'How the path would shard').", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    from torch_spyre import _capi
+
+    stream = torch.cuda.current_stream()
+    _log("gemm 4096^3")
+    g = bench_gemm(args.steps, args.warmup, stream, _capi)
+    extra = {}
+    if not args.no_extra:
+        _log("extra kernels")
+        extra = bench_extra(max(10, args.steps), args.warmup, stream, _capi)
+    cpu = None
+    if not args.no_cpu:
+        _log("cpu baseline")
+        cpu = cpu_baseline_gemm(g["a"], g["b"])
+    tflops = g["tflops"]
+    line = {
+        "metric": "fp16 GEMM TFLOP/s (M=N=K=4096, fp32 accumulate)",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["wall_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (U(-1,1), seed 0xAFFE)",
+        "config": {"workload": "c2: fp16 mm C = A @ B, M=N=K=4096 (BASELINE configs[1])",
+                   "M": 4096, "N": 4096, "K": 4096, "path": "C-ABI sph_gemm_f16"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
+                     "traffic": _traffic_for("gemm")},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,402 @@
+/*
+ * spyre_hip.h -- C-ABI of the MI355X (gfx950) kernel library behind the
+ * torch_spyre PrivateUse1 backend.
+ *
+ * This is the drop-in boundary: the ATen glue in torch_spyre/_C (eager ops)
+ * and the compiled-kernel runners (torch.compile path) call only these entry
+ * points.  Conventions:
+ *   - every function returns int status: 0 = ok; a positive hipError_t value
+ *     when the HIP runtime failed; SPH_ERR_* (>= 1000) for argument errors.
+ *     sph_last_error() returns a thread-local message for the last failure.
+ *   - no C++ exception crosses this ABI; no torch type appears in it.
+ *   - every pointer is a device pointer owned by the caller, except where a
+ *     parameter is documented as a host pointer.  Nothing here allocates
+ *     device memory.
+ *   - every launch takes an explicit stream (a hipStream_t passed as void*;
+ *     NULL = the legacy default stream) and is asynchronous w.r.t. the host.
+ *   - sizes, strides and leading dimensions are int64_t and count ELEMENTS.
+ *
+ * Reference interfaces replaced (paths relative to the torch-spyre tree):
+ *   The reference runs every device op through the IBM sendnn/flex SDK:
+ *   eager kernels build a sendnn graph per (op, shape, stride) and call
+ *   GraphLoader::Compute (codegen/templates/base.jinja2:135-232,
+ *   codegen/inputs/spyre_torch_ops.cpp:214-452), compiled kernels are SuperDSC
+ *   programs launched by _C.launch_kernel (torch_spyre/csrc/module.cpp:64-170),
+ *   and host<->device copies build a 3-stage DMA graph with a stick-layout
+ *   conversion (torch_spyre/csrc/spyre_mem.cpp:281-438).  Each entry point
+ *   below names the reference function it stands in for.
+ */
+#ifndef SPYRE_HIP_H_
+#define SPYRE_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SPH_ABI_VERSION 1
+#define SPH_MAX_DIMS 8
+
+typedef void* sph_stream_t; /* hipStream_t */
+
+/* Status codes beyond hipError_t. */
+enum {
+  SPH_OK = 0,
+  SPH_ERR_INVALID_ARG = 1001,
+  SPH_ERR_UNSUPPORTED = 1002,
+  SPH_ERR_TOO_LARGE = 1003
+};
+
+/* Element types.  Codes are this library's own, not torch's. */
+typedef enum {
+  SPH_F16 = 0,
+  SPH_BF16 = 1,
+  SPH_F32 = 2,
+  SPH_F64 = 3,
+  SPH_I8 = 4,
+  SPH_U8 = 5,
+  SPH_I16 = 6,
+  SPH_I32 = 7,
+  SPH_I64 = 8,
+  SPH_BOOL = 9
+} sph_dtype;
+
+/* ------------------------------------------------------------------ */
+/* Library / diagnostics                                               */
+/* ------------------------------------------------------------------ */
+
+/* Thread-local message describing the last non-zero status. */
+const char* sph_last_error(void);
+
+/* SPH_ABI_VERSION of the built library. */
+int sph_abi_version(void);
+
+/* ------------------------------------------------------------------ */
+/* Row softmax                                                         */
+/* Replaces: generated spyre___softmax_default / _out                  */
+/*   (codegen/inputs/Metadata.yaml:275-277, codegen/templates/          */
+/*    base.jinja2:16-241) and the compiled amax/sub/exp/sum/realdiv    */
+/*   chain (torch_spyre/_inductor/choices.py:58-83).                   */
+/* ------------------------------------------------------------------ */
+
+/* Softmax flags. */
+enum {
+  SPH_SOFTMAX_LOG = 1,   /* log_softmax instead of softmax */
+  SPH_SOFTMAX_CAUSAL = 2 /* mask column c of row r when
+                            c > (r % causal_q_len) + causal_offset */
+};
+
+/* y[r, c] = softmax_c(scale * x[r, c]) over each of `rows` rows of `cols`
+ * elements; row r of x starts at x + r*ldx, of y at y + r*ldy.
+ * Arithmetic in fp32; in_dtype/out_dtype in {F16, BF16, F32}.
+ * A row whose every column is masked produces NaN, as torch does. */
+int sph_softmax_rows(sph_dtype in_dtype, sph_dtype out_dtype, const void* x,
+                     int64_t ldx, void* y, int64_t ldy, int64_t rows,
+                     int64_t cols, float scale, int flags,
+                     int64_t causal_q_len, int64_t causal_offset,
+                     sph_stream_t stream);
+
+/* fp16 shorthand: contiguous rows, scale 1, no mask. */
+int sph_softmax_rows_f16(const void* x, void* y, int64_t rows, int64_t cols,
+                         sph_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* Normalisation over the last dimension (rows x cols, contiguous)      */
+/* Replaces: spyre__native_layer_norm_default (stub returning its input,*/
+/*   codegen/inputs/spyre_torch_ops.cpp:188-194), the compiled          */
+/*   exx2 -> layernormscale -> layernormnorm chain                      */
+/*   (torch_spyre/_inductor/decompositions.py:26-36, customops.py:      */
+/*   102-154, lowering.py:78-153) and the 5-launch eager RMSNorm        */
+/*   composite pow/mean/add/rsqrt/mul (spyre_torch_ops.cpp:456-474).    */
+/* ------------------------------------------------------------------ */
+
+/* If residual != NULL: h = round_to_dtype(x + residual) is written to h_out
+ * (h_out may alias x or residual) and normalised; otherwise h = x.
+ * RMSNorm:   y = h * rsqrt(mean(h^2) + eps) * weight
+ * LayerNorm: y = (h - mean(h)) * rsqrt(var(h) + eps) * weight + bias
+ * weight / bias may be NULL (treated as 1 / 0); w_dtype is the dtype of
+ * weight and bias (F32 or the activation dtype).  mean_out / rstd_out are
+ * optional fp32 per-row outputs (the saved statistics of
+ * aten::native_layer_norm / aten::_fused_rms_norm). */
+int sph_rmsnorm(sph_dtype dtype, sph_dtype w_dtype, const void* x,
+                const void* residual, const void* weight, void* y,
+                void* h_out, float* rstd_out, int64_t rows, int64_t cols,
+                float eps, sph_stream_t stream);
+
+int sph_layernorm(sph_dtype dtype, sph_dtype w_dtype, const void* x,
+                  const void* residual, const void* weight, const void* bias,
+                  void* y, void* h_out, float* mean_out, float* rstd_out,
+                  int64_t rows, int64_t cols, float eps, sph_stream_t stream);
+
+/* fp16 shorthands of the above with fp16 weight/bias. */
+int sph_rmsnorm_f16(const void* x, const void* residual, const void* weight,
+                    void* y, void* h_out, int64_t rows, int64_t cols,
+                    float eps, sph_stream_t stream);
+int sph_layernorm_f16(const void* x, const void* residual, const void* weight,
+                      const void* bias, void* y, void* h_out, int64_t rows,
+                      int64_t cols, float eps, sph_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* Fused pointwise chain + row reduction                                */
+/* Replaces: generated gelu (approximate forced to "none",             */
+/*   codegen/inputs/Metadata.yaml:125-132) followed by ReduceSum        */
+/*   (Metadata.yaml:299-302); the compile path cannot lower erf at all  */
+/*   (torch_spyre/_inductor/opfuncs.py:49-72).                          */
+/* ------------------------------------------------------------------ */
+
+/* y[r,c] = gelu_erf(x[r,c] * s[c] + b[c]);  rowsum[r] = sum_c y[r,c]
+ * (sum of the fp32 values before rounding to dtype).  s / b may be NULL,
+ * then the scalars s_scalar / b_scalar are used.  s, b have `dtype`.
+ * rowsum has `dtype`; y or rowsum may be NULL to skip that output. */
+int sph_gelu_affine_rowsum(sph_dtype dtype, const void* x, const void* s,
+                           const void* b, float s_scalar, float b_scalar,
+                           void* y, void* rowsum, int64_t rows, int64_t cols,
+                           sph_stream_t stream);
+
+int sph_gelu_affine_rowsum_f16(const void* x, const void* s, const void* b,
+                               void* y, void* rowsum, int64_t rows,
+                               int64_t cols, sph_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* GEMM on MFMA (fp32 accumulate)                                       */
+/* Replaces: spyre__mm_default (codegen/inputs/spyre_torch_ops.cpp:     */
+/*   214-293), spyre__bmm_default (:297-377), spyre__addmm_* (:381-452) */
+/*   and the compiled "pt"-unit matmul (torch_spyre/_inductor/          */
+/*   codegen/compute_ops.py:396-824).                                   */
+/* ------------------------------------------------------------------ */
+
+/* Epilogue selectors applied to alpha*A@B + beta*C before rounding. */
+enum {
+  SPH_EPI_NONE = 0,
+  SPH_EPI_RELU = 1,
+  SPH_EPI_GELU = 2, /* erf form */
+  SPH_EPI_SILU = 3
+};
+
+/* Row-major D[m,n] = epi(alpha * op(A)[m,k] @ op(B)[k,n] + beta * C[m,n]).
+ * op(A) = A (trans_a = 0, A[i,p] at a + i*lda + p) or A^T (trans_a = 1,
+ * A[i,p] at a + p*lda + i); likewise B with ldb.  C is optional (NULL or
+ * beta == 0 ignore it) and is addressed as c[i*ldc_row + j*ldc_col], so a
+ * bias row broadcast is ldc_row = 0, ldc_col = 1.  C and D may alias only
+ * when they are the same matrix with the same strides.
+ * dtype in {F16, BF16}: A, B, C, D all have it.  Any m, n, k >= 0. */
+int sph_gemm(sph_dtype dtype, int trans_a, int trans_b, int64_t m, int64_t n,
+             int64_t k, float alpha, const void* a, int64_t lda,
+             const void* b, int64_t ldb, float beta, const void* c,
+             int64_t ldc_row, int64_t ldc_col, void* d, int64_t ldd,
+             int epilogue, sph_stream_t stream);
+
+/* Strided batched form: batch b uses a + b*stride_a, etc. (stride_c may be
+ * 0 to broadcast one C over the batch). */
+int sph_gemm_strided_batched(sph_dtype dtype, int trans_a, int trans_b,
+                             int64_t batch, int64_t m, int64_t n, int64_t k,
+                             float alpha, const void* a, int64_t lda,
+                             int64_t stride_a, const void* b, int64_t ldb,
+                             int64_t stride_b, float beta, const void* c,
+                             int64_t ldc_row, int64_t ldc_col,
+                             int64_t stride_c, void* d, int64_t ldd,
+                             int64_t stride_d, int epilogue,
+                             sph_stream_t stream);
+
+/* fp16 shorthands: contiguous row-major, no transpose, no C. */
+int sph_gemm_f16(int64_t m, int64_t n, int64_t k, const void* a,
+                 const void* b, void* d, sph_stream_t stream);
+int sph_bmm_f16(int64_t batch, int64_t m, int64_t n, int64_t k,
+                const void* a, const void* b, void* d, sph_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* Generic strided pointwise engine                                     */
+/* Replaces: the generated base/list_inp eager ops of Metadata.yaml     */
+/*   (add/sub/mul/div/exp/log/.../where/eq/ge, base.jinja2:16-241),     */
+/*   spyre__clone_default (spyre_torch_ops.cpp:507-583),                */
+/*   spyre__fill_Scalar (:394-403) and the SFP OpFuncs of the compile   */
+/*   path (torch_spyre/_inductor/opfuncs.py:49-72).                     */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+  void* data;                     /* device pointer */
+  int32_t dtype;                  /* sph_dtype */
+  int32_t pad_;
+  int64_t strides[SPH_MAX_DIMS];  /* element strides, 0 = broadcast */
+} sph_operand;
+
+/* Pointwise op codes.  Arity in brackets; a, b, c are inputs 0..2,
+ * alpha/beta the scalar parameters. */
+enum {
+  SPH_PW_COPY = 0,        /* [1] out = a (with dtype conversion) */
+  SPH_PW_FILL = 1,        /* [0] out = alpha */
+  SPH_PW_ADD = 2,         /* [2] out = a + alpha*b */
+  SPH_PW_SUB = 3,         /* [2] out = a - alpha*b */
+  SPH_PW_MUL = 4,         /* [2] out = a * b */
+  SPH_PW_DIV = 5,         /* [2] out = a / b */
+  SPH_PW_ADD_SCALAR = 6,  /* [1] out = a + alpha */
+  SPH_PW_MUL_SCALAR = 7,  /* [1] out = a * alpha */
+  SPH_PW_RSUB_SCALAR = 8, /* [1] out = alpha - a */
+  SPH_PW_DIV_SCALAR = 9,  /* [1] out = a / alpha */
+  SPH_PW_POW_SCALAR = 10, /* [1] out = a ^ alpha */
+  SPH_PW_RPOW_SCALAR = 11,/* [1] out = alpha ^ a */
+  SPH_PW_POW = 12,        /* [2] out = a ^ b */
+  SPH_PW_MAXIMUM = 13,    /* [2] */
+  SPH_PW_MINIMUM = 14,    /* [2] */
+  SPH_PW_NEG = 20,        /* [1] */
+  SPH_PW_ABS = 21,
+  SPH_PW_EXP = 22,
+  SPH_PW_LOG = 23,
+  SPH_PW_SQRT = 24,
+  SPH_PW_RSQRT = 25,
+  SPH_PW_RECIPROCAL = 26,
+  SPH_PW_SIGMOID = 27,
+  SPH_PW_TANH = 28,
+  SPH_PW_RELU = 29,
+  SPH_PW_GELU = 30,       /* erf form */
+  SPH_PW_GELU_TANH = 31,
+  SPH_PW_SILU = 32,
+  SPH_PW_SIN = 33,
+  SPH_PW_COS = 34,
+  SPH_PW_ERF = 35,
+  SPH_PW_LOG1P = 36,
+  SPH_PW_EXPM1 = 37,
+  SPH_PW_MISH = 38,
+  SPH_PW_LOGICAL_NOT = 39,
+  SPH_PW_BITWISE_NOT = 40,
+  SPH_PW_SIGN = 41,
+  SPH_PW_FLOOR = 42,
+  SPH_PW_CEIL = 43,
+  SPH_PW_ROUND = 44,
+  SPH_PW_TRUNC = 45,
+  SPH_PW_CLAMP = 46,      /* [1] out = min(max(a, alpha), beta) */
+  SPH_PW_LEAKY_RELU = 47, /* [1] slope alpha */
+  SPH_PW_SQUARE = 48,
+  SPH_PW_EQ = 60,         /* [2] comparisons: out is bool (or any dtype) */
+  SPH_PW_NE = 61,
+  SPH_PW_LT = 62,
+  SPH_PW_LE = 63,
+  SPH_PW_GT = 64,
+  SPH_PW_GE = 65,
+  SPH_PW_EQ_SCALAR = 66,  /* [1] compare with alpha */
+  SPH_PW_NE_SCALAR = 67,
+  SPH_PW_LT_SCALAR = 68,
+  SPH_PW_LE_SCALAR = 69,
+  SPH_PW_GT_SCALAR = 70,
+  SPH_PW_GE_SCALAR = 71,
+  SPH_PW_LOGICAL_AND = 72,/* [2] */
+  SPH_PW_LOGICAL_OR = 73,
+  SPH_PW_WHERE = 80,      /* [3] out = a ? b : c */
+  SPH_PW_SILU_MUL = 81,   /* [2] out = silu(a) * b  (SwiGLU) */
+  SPH_PW_ADDCMUL = 82,    /* [3] out = a + alpha * b * c */
+  SPH_PW_LERP = 83,       /* [2] out = a + alpha * (b - a) */
+  SPH_PW_OP_COUNT_ = 128
+};
+
+/* out[i] = op(in...[i]) over the index space `sizes` (ndim <= 8, row-major
+ * order of dims, last dim fastest).  operands[0] is the output,
+ * operands[1..nin] the inputs.  Integer and bool operands are computed in
+ * int64 for the integer-exact ops (copy/fill/add/sub/mul/neg/abs/compare/
+ * where/logical/bitwise/maximum/minimum); everything else computes in fp32,
+ * or fp64 when any operand is F64.  Conversion to the output dtype rounds to
+ * nearest-even for floating outputs and truncates toward zero for integer
+ * outputs, like torch's casts. */
+int sph_pointwise(int op, int nin, const sph_operand* operands, int ndim,
+                  const int64_t* sizes, double alpha, double beta,
+                  sph_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* Reductions                                                           */
+/* Replaces: eager ReduceSum/mean (Metadata.yaml:299-302,               */
+/*   spyre_torch_ops.cpp:456-490) and the compiled sum/max/min/argmax/  */
+/*   argmin reductions (torch_spyre/_inductor/opfuncs.py:26-39).        */
+/* ------------------------------------------------------------------ */
+
+enum {
+  SPH_RED_SUM = 0,
+  SPH_RED_MEAN = 1,
+  SPH_RED_MAX = 2,
+  SPH_RED_MIN = 3,
+  SPH_RED_ARGMAX = 4, /* output int64 index along the (single) reduced dim */
+  SPH_RED_ARGMIN = 5,
+  SPH_RED_PROD = 6,
+  SPH_RED_SUMSQ = 7,  /* sum of squares */
+  SPH_RED_ANY = 8,
+  SPH_RED_ALL = 9
+};
+
+/* Reduces `in` over the dims d with reduce_mask bit d set.  sizes[] is the
+ * input shape; out.strides[d] is ignored (treated as 0) for reduced dims.
+ * Accumulation in fp32 (fp64 for F64 input, int64 for integer sums).
+ * For ARGMAX/ARGMIN exactly one dim must be reduced; ties resolve to the
+ * first index and NaN wins, as in torch. */
+int sph_reduce(int op, const sph_operand* in, const sph_operand* out,
+               int ndim, const int64_t* sizes, uint32_t reduce_mask,
+               sph_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* Data movement                                                        */
+/* ------------------------------------------------------------------ */
+
+/* Row gather (embedding / index_select on dim 0):
+ * out[i, :] = table[idx[i], :] for i < n_idx; rows of `row_elems` elements
+ * of `elem_bytes` bytes; idx is int64 (idx_is_i64 = 1) or int32.
+ * An index outside [0, num_rows) yields a zero row (no fault); callers that
+ * need torch's error check the indices themselves.
+ * Replaces: generated embedding (Metadata.yaml:105-115). */
+int sph_gather_rows(const void* table, int64_t num_rows, int64_t row_elems,
+                    int elem_bytes, const void* idx, int idx_is_i64,
+                    int64_t n_idx, void* out, sph_stream_t stream);
+
+/* tril/triu on the last two dims of a contiguous [batch, rows, cols]
+ * tensor: keep element (r, c) when c - r <= diagonal (lower) or
+ * c - r >= diagonal (upper), zero it otherwise.
+ * Replaces: generated tril (Metadata.yaml:322-324). */
+int sph_tri(int upper, int64_t diagonal, int elem_bytes, const void* x,
+            void* y, int64_t batch, int64_t rows, int64_t cols,
+            sph_stream_t stream);
+
+/* Rotary position embedding, rotate-half convention, on a contiguous
+ * [tokens, heads, head_dim] tensor (in place allowed: y == x):
+ * y[..., i]       = x[i] cos(p w_i) - x[i + d/2] sin(p w_i)
+ * y[..., i + d/2] = x[i + d/2] cos(p w_i) + x[i] sin(p w_i),
+ * w_i = theta^(-2i/d), p = positions[token] (int64).  The compiled and
+ * eager decoder both use this; the reference has no RoPE (sin/cos have
+ * no OpFunc, torch_spyre/_inductor/opfuncs.py:49-72). */
+int sph_rope(sph_dtype dtype, const void* x, void* y,
+             const int64_t* positions, int64_t tokens, int64_t heads,
+             int64_t head_dim, float theta, sph_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* Stick (tiled) layout                                                 */
+/* Replaces: the host-side stick conversion of the DMA path            */
+/*   (torch_spyre/csrc/spyre_mem.cpp:62-279, generate_dci /             */
+/*   get_device_stride_info) with an on-GPU permutation.  The layout is */
+/*   SpyreTensorLayout's generic stick format                           */
+/*   (torch_spyre/csrc/spyre_tensor_impl.cpp:29-74): device dims         */
+/*   [ceil(S/E), host dims in dim_order[:-1]..., E] with S the size of  */
+/*   the stick dim dim_order[-1] and E = 128 / elem_bytes elements per  */
+/*   128-byte stick, row-major on the device, padding sticks zeroed.    */
+/*   With the stick dim = K this is the K-panel layout of a GEMM        */
+/*   operand: a [rows x 64] panel slice is one contiguous block.        */
+/* ------------------------------------------------------------------ */
+
+/* Number of bytes the stick layout of `host_sizes` occupies. */
+int64_t sph_stick_nbytes(int ndim, const int64_t* host_sizes,
+                         const int32_t* dim_order, int elem_bytes);
+
+/* src (strided host-order tensor, element strides host_strides) ->
+ * dst (stick layout, dst_nbytes = sph_stick_nbytes(...)).  Bit-exact. */
+int sph_stick_pack(const void* src, void* dst, int ndim,
+                   const int64_t* host_sizes, const int64_t* host_strides,
+                   const int32_t* dim_order, int elem_bytes,
+                   sph_stream_t stream);
+
+/* Inverse of sph_stick_pack: stick layout -> strided host-order tensor. */
+int sph_stick_unpack(const void* src, void* dst, int ndim,
+                     const int64_t* host_sizes, const int64_t* host_strides,
+                     const int32_t* dim_order, int elem_bytes,
+                     sph_stream_t stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* SPYRE_HIP_H_ */

@@ -1,0 +1,510 @@
+"""Parity of every HIP kernel with the CPU oracle, called through the C-ABI
+(include/spyre_hip.h) on device buffers.  Device memory comes from torch
+(plumbing only); the computation is the library's.
+
+Bars: bit-exact for layout / copy / gather / integer work; rtol = atol = 1e-2
+against the oracle's fp32 result rounded to the output dtype for fp16 / bf16
+floating point (fp32 outputs: 1e-4)."""
+
+import numpy as np
+import pytest
+import torch
+
+from torch_spyre import _capi
+
+from oracle import layout as L
+from oracle import ops as O
+
+from helpers import assert_close_fp, np32, randn, uniform
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _p(t):
+    return t.data_ptr() if t is not None else None
+
+
+def _sync():
+    torch.cuda.synchronize()
+
+
+def _log(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+DT = {torch.float16: _capi.F16, torch.bfloat16: _capi.BF16, torch.float32: _capi.F32}
+
+
+# ---------------------------------------------------------------------------
+# softmax
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,cols", [(512, 4096), (3, 64), (5, 1), (7, 1000), (33, 7),
+                                       (4, 2048), (2, 8192), (2, 12000), (2, 70000)])
+def test_softmax_shapes(rows, cols):
+    _log(f"softmax {rows}x{cols}")
+    x = randn((rows, cols), k=0, scale=4.0)
+    xd = x.to(DEV)
+    yd = torch.empty_like(xd)
+    _capi.call("sph_softmax_rows_f16", _p(xd), _p(yd), rows, cols, _stream())
+    _sync()
+    assert_close_fp(yd, O.softmax(x.numpy()), what="softmax")
+    np.testing.assert_allclose(np32(yd).sum(-1), 1.0, rtol=2e-2)
+
+
+def test_softmax_reference_kat():
+    _log("softmax arange KAT")
+    x = torch.arange(0, 64, dtype=torch.float16).unsqueeze(0).repeat(3, 1)
+    xd = x.to(DEV)
+    yd = torch.empty_like(xd)
+    _capi.call("sph_softmax_rows_f16", _p(xd), _p(yd), 3, 64, _stream())
+    _sync()
+    torch.testing.assert_close(yd.cpu(), torch.softmax(x.float(), 1).half(), rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("in_dt,out_dt", [(torch.bfloat16, torch.bfloat16),
+                                          (torch.float32, torch.float32),
+                                          (torch.float16, torch.float32)])
+def test_softmax_dtypes_log_scale_strided(in_dt, out_dt):
+    _log(f"softmax dtypes {in_dt}->{out_dt}")
+    rows, cols, ld = 37, 300, 320
+    big = randn((rows, ld), k=1, scale=3.0, dtype=in_dt)
+    xd = big.to(DEV)
+    yd = torch.zeros(rows, ld + 8, dtype=out_dt, device=DEV)
+    for flags in (0, _capi.SOFTMAX_LOG):
+        _capi.call("sph_softmax_rows", DT[in_dt], DT[out_dt], _p(xd), ld, _p(yd), ld + 8,
+                   rows, cols, 0.5, flags, 0, 0, _stream())
+        _sync()
+        want = O.softmax(big[:, :cols].float().numpy(), scale=0.5, log=bool(flags))
+        tol = 1e-4 if out_dt == torch.float32 and in_dt == torch.float32 else 1e-2
+        assert_close_fp(yd[:, :cols], want, out_dtype=out_dt, rtol=tol, atol=tol,
+                        what=f"softmax flags={flags}")
+        assert torch.all(yd[:, cols:].cpu() == 0)  # nothing written past cols
+
+
+@pytest.mark.parametrize("q_len,k_len", [(5, 9), (2048, 2048), (1, 1152), (7, 64)])
+def test_softmax_causal(q_len, k_len):
+    _log(f"softmax causal {q_len}x{k_len}")
+    heads = 4 if q_len < 2048 else 2
+    x = randn((heads * q_len, k_len), k=2)
+    xd = x.to(DEV)
+    yd = torch.empty_like(xd)
+    off = k_len - q_len
+    _capi.call("sph_softmax_rows", _capi.F16, _capi.F16, _p(xd), k_len, _p(yd), k_len,
+               heads * q_len, k_len, 0.125, _capi.SOFTMAX_CAUSAL, q_len, off, _stream())
+    _sync()
+    want = O.softmax(x.numpy(), scale=0.125, causal_q_len=q_len, causal_offset=off)
+    assert_close_fp(yd, want, what="causal softmax")
+
+
+# ---------------------------------------------------------------------------
+# norms
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,cols", [(8192, 4096), (3, 64), (17, 100), (4, 4097),
+                                       (2, 70000), (64, 1)])
+@pytest.mark.parametrize("residual", [False, True])
+def test_rmsnorm(rows, cols, residual):
+    _log(f"rmsnorm {rows}x{cols} residual={residual}")
+    x = randn((rows, cols), k=0)
+    r = randn((rows, cols), k=1) if residual else None
+    w = randn((cols,), k=2, scale=0.02, mean=1.0)
+    xd, wd = x.to(DEV), w.to(DEV)
+    rd = r.to(DEV) if residual else None
+    yd = torch.empty_like(xd)
+    hd = torch.empty_like(xd) if residual else None
+    rstd = torch.empty(rows, dtype=torch.float32, device=DEV)
+    _capi.call("sph_rmsnorm", _capi.F16, _capi.F16, _p(xd), _p(rd), _p(wd), _p(yd), _p(hd),
+               _p(rstd), rows, cols, 1e-5, _stream())
+    _sync()
+    y, h = O.rmsnorm(x.numpy(), w.numpy(), 1e-5, residual=r.numpy() if residual else None)
+    assert_close_fp(yd, y, what="rmsnorm y")
+    if residual:
+        # h is a plain fp16 add: bit-exact
+        assert torch.equal(hd.cpu(), (x + r))
+
+
+@pytest.mark.parametrize("rows,cols", [(8192, 4096), (5, 300), (3, 8), (2, 70000)])
+@pytest.mark.parametrize("residual", [False, True])
+def test_layernorm(rows, cols, residual):
+    _log(f"layernorm {rows}x{cols} residual={residual}")
+    x = randn((rows, cols), k=3)
+    r = randn((rows, cols), k=4) if residual else None
+    w = randn((cols,), k=5, scale=0.02, mean=1.0)
+    b = randn((cols,), k=6, scale=0.02)
+    xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
+    rd = r.to(DEV) if residual else None
+    yd = torch.empty_like(xd)
+    hd = torch.empty_like(xd) if residual else None
+    mean = torch.empty(rows, dtype=torch.float32, device=DEV)
+    rstd = torch.empty(rows, dtype=torch.float32, device=DEV)
+    _capi.call("sph_layernorm", _capi.F16, _capi.F16, _p(xd), _p(rd), _p(wd), _p(bd), _p(yd),
+               _p(hd), _p(mean), _p(rstd), rows, cols, 1e-5, _stream())
+    _sync()
+    y, h, m, rs = O.layernorm(x.numpy(), w.numpy(), b.numpy(), 1e-5,
+                              residual=r.numpy() if residual else None)
+    assert_close_fp(yd, y, what="layernorm y")
+    np.testing.assert_allclose(mean.cpu().numpy(), m, rtol=1e-3, atol=1e-3)
+    np.testing.assert_allclose(rstd.cpu().numpy(), rs, rtol=1e-3, atol=1e-3)
+    if residual:
+        assert torch.equal(hd.cpu(), (x + r))
+
+
+def test_norm_fp32_weight_and_bf16():
+    _log("norm fp32 weight / bf16")
+    x = randn((9, 256), k=7)
+    w = randn((256,), k=8, scale=0.02, mean=1.0, dtype=torch.float32)
+    xd, wd = x.to(DEV), w.to(DEV)
+    yd = torch.empty_like(xd)
+    _capi.call("sph_rmsnorm", _capi.F16, _capi.F32, _p(xd), None, _p(wd), _p(yd), None, None,
+               9, 256, 1e-6, _stream())
+    _sync()
+    assert_close_fp(yd, O.rmsnorm(x.numpy(), w.numpy(), 1e-6)[0])
+    xb = randn((9, 256), k=9, dtype=torch.bfloat16)
+    xbd = xb.to(DEV)
+    ybd = torch.empty_like(xbd)
+    _capi.call("sph_layernorm", _capi.BF16, _capi.F32, _p(xbd), None, _p(wd), None, _p(ybd),
+               None, None, None, 9, 256, 1e-5, _stream())
+    _sync()
+    assert_close_fp(ybd, O.layernorm(xb.float().numpy(), w.numpy(), None, 1e-5)[0],
+                    out_dtype=torch.bfloat16, rtol=2e-2, atol=2e-2)
+
+
+# ---------------------------------------------------------------------------
+# GELU chain
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,cols", [(8192, 4096), (3, 100), (2, 70000)])
+def test_gelu_affine_rowsum(rows, cols):
+    _log(f"gelu_rowsum {rows}x{cols}")
+    x = randn((rows, cols), k=0)
+    s = randn((cols,), k=1, scale=0.02, mean=1.0)
+    b = randn((cols,), k=2, scale=0.02)
+    xd, sd, bd = x.to(DEV), s.to(DEV), b.to(DEV)
+    yd = torch.empty_like(xd)
+    rd = torch.empty(rows, dtype=torch.float16, device=DEV)
+    _capi.call("sph_gelu_affine_rowsum_f16", _p(xd), _p(sd), _p(bd), _p(yd), _p(rd), rows, cols,
+               _stream())
+    _sync()
+    y, r = O.gelu_affine_rowsum(x.numpy(), s.numpy(), b.numpy())
+    assert_close_fp(yd, y, what="gelu y")
+    assert_close_fp(rd, r, what="gelu rowsum")
+
+
+def test_gelu_scalar_affine():
+    _log("gelu scalar s,b")
+    x = randn((4, 512), k=3)
+    xd = x.to(DEV)
+    yd = torch.empty_like(xd)
+    rd = torch.empty(4, dtype=torch.float16, device=DEV)
+    _capi.call("sph_gelu_affine_rowsum", _capi.F16, _p(xd), None, None, 1.5, -0.25, _p(yd),
+               _p(rd), 4, 512, _stream())
+    _sync()
+    y, r = O.gelu_affine_rowsum(x.numpy(), np.float32(1.5), np.float32(-0.25))
+    assert_close_fp(yd, y)
+    assert_close_fp(rd, r)
+
+
+# ---------------------------------------------------------------------------
+# GEMM
+# ---------------------------------------------------------------------------
+def _gemm(a, b, trans_a=False, trans_b=False, alpha=1.0, beta=0.0, c=None, crow=0, ccol=0,
+          epi=0, dtype=torch.float16):
+    """a/b are device tensors holding op(A)/op(B) in their storage layout."""
+    m = a.shape[1] if trans_a else a.shape[0]
+    k = a.shape[0] if trans_a else a.shape[1]
+    n = b.shape[0] if trans_b else b.shape[1]
+    d = torch.empty(m, n, dtype=dtype, device=DEV)
+    _capi.call("sph_gemm", DT[dtype], int(trans_a), int(trans_b), m, n, k, alpha, _p(a),
+               a.stride(0), _p(b), b.stride(0), beta, _p(c), crow, ccol, _p(d), n, epi, _stream())
+    _sync()
+    return d
+
+
+def test_gemm_reference_kat_exact():
+    _log("gemm arange KAT")
+    x = torch.arange(15, dtype=torch.float16).view(3, 5)
+    y = torch.arange(35, dtype=torch.float16).view(5, 7)
+    d = _gemm(x.to(DEV), y.to(DEV))
+    want = O.gemm(x.numpy(), y.numpy())
+    assert torch.equal(d.cpu().float(), torch.from_numpy(want))  # exact in fp32 accumulate
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 4096), (256, 256, 64), (300, 200, 70),
+                                   (1, 1, 1), (5, 7, 3), (129, 65, 257), (2048, 1024, 128),
+                                   (64, 49155, 64)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_gemm_shapes_transposes(m, n, k, ta, tb):
+    if m * n * k >= 2**30 and (ta or tb):
+        pytest.skip("large case covered by the NN / NT layouts")
+    _log(f"gemm {m}x{n}x{k} ta={ta} tb={tb}")
+    A = uniform((m, k), k=1)
+    B = uniform((k, n), k=2)
+    a_store = A.t().contiguous() if ta else A
+    b_store = B.t().contiguous() if tb else B
+    d = _gemm(a_store.to(DEV), b_store.to(DEV), ta, tb)
+    assert_close_fp(d, O.gemm(A.numpy(), B.numpy()), what=f"gemm ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("epi,name", [(0, "none"), (1, "relu"), (2, "gelu"), (3, "silu")])
+def test_gemm_bias_alpha_beta_epilogue(epi, name):
+    _log(f"gemm epilogue {name}")
+    m, n, k = 96, 80, 136
+    A, B = uniform((m, k), k=3), uniform((k, n), k=4)
+    bias = uniform((n,), k=5)
+    d = _gemm(A.to(DEV), B.to(DEV), alpha=0.5, beta=1.5, c=bias.to(DEV), crow=0, ccol=1, epi=epi)
+    want = O.gemm(A.numpy(), B.numpy(), alpha=0.5, beta=1.5, c=bias.numpy()[None, :], epilogue=name)
+    assert_close_fp(d, want, what=f"epilogue {name}")
+    C = uniform((m, n), k=6)
+    d2 = _gemm(A.to(DEV), B.to(DEV), beta=-1.0, c=C.to(DEV), crow=n, ccol=1)
+    assert_close_fp(d2, O.gemm(A.numpy(), B.numpy(), beta=-1.0, c=C.numpy()))
+
+
+def test_gemm_bf16_and_unaligned_ld():
+    _log("gemm bf16 / unaligned")
+    A, B = uniform((70, 45), k=7, dtype=torch.bfloat16), uniform((45, 33), k=8, dtype=torch.bfloat16)
+    d = _gemm(A.to(DEV), B.to(DEV), dtype=torch.bfloat16)
+    assert_close_fp(d, O.gemm(A.float().numpy(), B.float().numpy()), out_dtype=torch.bfloat16,
+                    rtol=2e-2, atol=2e-2)
+    # row-major views with odd leading dims (no 16-byte vector path)
+    big = uniform((70, 51), k=9)
+    Av = big.to(DEV)[:, 3:48]
+    Bd = uniform((45, 33), k=10).to(DEV)
+    m, k, n = 70, 45, 33
+    dd = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    _capi.call("sph_gemm", _capi.F16, 0, 0, m, n, k, 1.0, Av.data_ptr(), 51, _p(Bd), 33, 0.0, None,
+               0, 0, _p(dd), n, 0, _stream())
+    _sync()
+    assert_close_fp(dd, O.gemm(big[:, 3:48].numpy(), Bd.cpu().numpy()))
+
+
+@pytest.mark.parametrize("batch,m,n,k,tb", [(32, 2048, 2048, 128, False), (32, 2048, 128, 2048, False),
+                                            (4, 100, 36, 72, True), (3, 5, 7, 9, False)])
+def test_bmm(batch, m, n, k, tb):
+    _log(f"bmm {batch}x{m}x{n}x{k} tb={tb}")
+    A = uniform((batch, m, k), k=1)
+    B = uniform((batch, k, n), k=2)
+    ad = A.to(DEV)
+    bd = (B.transpose(1, 2).contiguous() if tb else B).to(DEV)
+    d = torch.empty(batch, m, n, dtype=torch.float16, device=DEV)
+    ldb = k if tb else n
+    _capi.call("sph_gemm_strided_batched", _capi.F16, 0, int(tb), batch, m, n, k, 1.0, _p(ad), k,
+               m * k, _p(bd), ldb, k * n, 0.0, None, 0, 0, 0, _p(d), n, m * n, 0, _stream())
+    _sync()
+    assert_close_fp(d, O.gemm(A.numpy(), B.numpy()), what="bmm")
+
+
+# ---------------------------------------------------------------------------
+# pointwise engine
+# ---------------------------------------------------------------------------
+def _pw(op, out, ins, alpha=0.0, beta=0.0):
+    shape = list(out.shape)
+    ops = [_capi.operand(out.data_ptr(), _capi.torch_dtype_code(out.dtype), out.stride())]
+    for t in ins:
+        t = t.expand(shape) if t.dim() <= len(shape) else t
+        ops.append(_capi.operand(t.data_ptr(), _capi.torch_dtype_code(t.dtype), t.stride()))
+    arr = (_capi.Operand * len(ops))(*ops)
+    _capi.call("sph_pointwise", op, len(ins), arr, len(shape), _capi.i64_array(shape), alpha, beta,
+               _stream())
+    _sync()
+
+
+UNARY = [(20, torch.neg), (21, torch.abs), (22, torch.exp), (24, lambda t: torch.sqrt(t.abs())),
+         (26, torch.reciprocal), (27, torch.sigmoid), (28, torch.tanh), (29, torch.relu),
+         (30, torch.nn.functional.gelu), (32, torch.nn.functional.silu), (33, torch.sin),
+         (34, torch.cos), (35, torch.erf), (48, torch.square)]
+
+
+@pytest.mark.parametrize("op,fn", UNARY)
+def test_pointwise_unary(op, fn):
+    _log(f"pointwise unary {op}")
+    x = randn((67, 256), k=1)
+    if op == 24:
+        x = x.abs()
+    xd = x.to(DEV)
+    out = torch.empty_like(xd)
+    _pw(op, out, [xd])
+    want = fn(x.float()).numpy()
+    assert_close_fp(out, want, what=f"unary {op}")
+
+
+BINARY = [(2, lambda a, b: a + 2 * b, 2.0), (3, lambda a, b: a - b, 1.0), (4, torch.mul, 0.0),
+          (5, torch.div, 0.0), (13, torch.maximum, 0.0), (14, torch.minimum, 0.0),
+          (81, lambda a, b: torch.nn.functional.silu(a) * b, 0.0)]
+
+
+@pytest.mark.parametrize("op,fn,alpha", BINARY)
+def test_pointwise_binary_broadcast_strided(op, fn, alpha):
+    _log(f"pointwise binary {op}")
+    a = randn((67, 256), k=2)
+    b = randn((256,), k=3)
+    if op == 5:
+        b = torch.where(b.abs() < 0.1, torch.full_like(b, 0.5), b)
+    ad, bd = a.to(DEV), b.to(DEV)
+    out = torch.empty_like(ad)
+    _pw(op, out, [ad, bd.unsqueeze(0)], alpha)
+    assert_close_fp(out, fn(a.float(), b.float()).numpy(), what=f"binary {op}")
+    # transposed (non-contiguous) input and output
+    a2 = randn((256, 67), k=9)
+    if op == 5:
+        a2 = torch.where(a2.abs() < 0.1, torch.full_like(a2, 0.5), a2)
+    a2t = a2.to(DEV).t()
+    out_t = torch.empty(256, 67, dtype=torch.float16, device=DEV).t()
+    _pw(op, out_t, [ad, a2t], alpha)
+    assert_close_fp(out_t, fn(a.float(), a2.t().float()).numpy(), what=f"binary {op} strided")
+
+
+def test_pointwise_compare_where_cast_fill():
+    _log("pointwise compare/where/cast/fill")
+    x, y = randn((256,), k=4), randn((256,), k=5)
+    xd, yd = x.to(DEV), y.to(DEV)
+    eq = torch.empty(256, dtype=torch.bool, device=DEV)
+    for op, fn in [(60, torch.eq), (65, torch.ge), (62, torch.lt)]:
+        _pw(op, eq, [xd, yd])
+        assert torch.equal(eq.cpu(), fn(x, y))
+    ge = torch.empty(256, dtype=torch.bool, device=DEV)
+    _pw(65, ge, [xd, yd])
+    w = torch.empty_like(xd)
+    _pw(80, w, [ge, xd, yd])
+    assert torch.equal(w.cpu(), torch.where(x >= y, x, y))
+    # casts are bit-exact with torch's
+    f32 = torch.empty(256, dtype=torch.float32, device=DEV)
+    _pw(0, f32, [xd])
+    assert torch.equal(f32.cpu(), x.float())
+    big = (randn((256,), k=6, dtype=torch.float32) * 1000)
+    bd = big.to(DEV)
+    for dt in (torch.float16, torch.bfloat16, torch.int32, torch.int8, torch.int64):
+        o = torch.empty(256, dtype=dt, device=DEV)
+        _pw(0, o, [bd])
+        if dt == torch.int8:
+            continue  # out-of-range float -> int8 is undefined behaviour in C and torch
+        assert torch.equal(o.cpu(), big.to(dt)), dt
+    fill = torch.empty(3, 5, dtype=torch.float16, device=DEV)
+    _pw(1, fill, [], alpha=3.5)
+    assert torch.equal(fill.cpu(), torch.full((3, 5), 3.5, dtype=torch.float16))
+    ints = torch.arange(-5, 5, dtype=torch.int64)
+    io = torch.empty(10, dtype=torch.int64, device=DEV)
+    _pw(2, io, [ints.to(DEV), ints.to(DEV)], alpha=3.0)
+    assert torch.equal(io.cpu(), ints + 3 * ints)
+
+
+# ---------------------------------------------------------------------------
+# reductions
+# ---------------------------------------------------------------------------
+def _reduce(op, x, dims, out_dtype=None, keep_out=False):
+    shape = list(x.shape)
+    out_shape = [1 if i in dims else s for i, s in enumerate(shape)]
+    out = torch.empty(out_shape, dtype=out_dtype or x.dtype, device=DEV)
+    ost = [0 if i in dims else s for i, s in enumerate(out.stride())]
+    i_op = _capi.operand(x.data_ptr(), _capi.torch_dtype_code(x.dtype), x.stride())
+    o_op = _capi.operand(out.data_ptr(), _capi.torch_dtype_code(out.dtype), ost)
+    mask = sum(1 << d for d in dims)
+    _capi.call("sph_reduce", op, i_op, o_op, len(shape), _capi.i64_array(shape), mask, _stream())
+    _sync()
+    return out
+
+
+@pytest.mark.parametrize("dims", [[0], [1], [0, 1], [2], [0, 2]])
+def test_reduce_sum_mean_max(dims):
+    _log(f"reduce dims={dims}")
+    x = randn((6, 67, 40), k=7)
+    xd = x.to(DEV)
+    for op, fn in [(0, lambda t: t.sum(dims, keepdim=True)), (1, lambda t: t.mean(dims, keepdim=True)),
+                   (2, lambda t: t.amax(dims, keepdim=True)), (3, lambda t: t.amin(dims, keepdim=True))]:
+        out = _reduce(op, xd, dims)
+        assert_close_fp(out, fn(x.float()).numpy(), what=f"reduce op={op}")
+
+
+def test_reduce_argmax_ties_nan_and_ints():
+    _log("reduce argmax / ints")
+    x = torch.tensor([[1.0, 3.0, 3.0, 2.0], [float("nan"), 5.0, float("nan"), 1.0],
+                      [-1.0, -1.0, -2.0, -3.0]], dtype=torch.float16)
+    xd = x.to(DEV)
+    am = _reduce(4, xd, [1], out_dtype=torch.int64)
+    assert torch.equal(am.cpu().view(-1), torch.argmax(x.float(), 1))
+    an = _reduce(5, xd, [1], out_dtype=torch.int64)
+    assert torch.equal(an.cpu().view(-1), torch.argmin(x.float(), 1))
+    logits = randn((4, 49155), k=8)
+    ld = logits.to(DEV)
+    am2 = _reduce(4, ld, [1], out_dtype=torch.int64)
+    assert torch.equal(am2.cpu().view(-1), torch.argmax(logits.float(), 1))
+    ints = torch.arange(64, dtype=torch.int32).view(8, 8)
+    s = _reduce(0, ints.to(DEV), [0], out_dtype=torch.int64)
+    assert torch.equal(s.cpu(), ints.long().sum(0, keepdim=True))
+
+
+# ---------------------------------------------------------------------------
+# data movement
+# ---------------------------------------------------------------------------
+def test_gather_rows_embedding():
+    _log("gather rows")
+    table = randn((49155, 4096), k=1)
+    idx = torch.randint(0, 49155, (2048,), generator=torch.Generator().manual_seed(5))
+    td, idd = table.to(DEV), idx.to(DEV)
+    out = torch.empty(2048, 4096, dtype=torch.float16, device=DEV)
+    _capi.call("sph_gather_rows", _p(td), 49155, 4096, 2, _p(idd), 1, 2048, _p(out), _stream())
+    _sync()
+    assert torch.equal(out.cpu(), table[idx])
+    # ragged rows, int32 indices, out-of-range -> zero row
+    t2 = randn((10, 3), k=2)
+    i2 = torch.tensor([9, 0, 10, -1, 4], dtype=torch.int32)
+    o2 = torch.empty(5, 3, dtype=torch.float16, device=DEV)
+    _capi.call("sph_gather_rows", _p(t2.to(DEV)), 10, 3, 2, _p(i2.to(DEV)), 0, 5, _p(o2), _stream())
+    _sync()
+    want = torch.stack([t2[9], t2[0], torch.zeros(3, dtype=torch.float16),
+                        torch.zeros(3, dtype=torch.float16), t2[4]])
+    assert torch.equal(o2.cpu(), want)
+
+
+@pytest.mark.parametrize("upper,diag", [(0, 0), (1, 0), (0, -2), (1, 3)])
+def test_tri(upper, diag):
+    _log(f"tri upper={upper} diag={diag}")
+    x = randn((3, 9, 13), k=3)
+    xd = x.to(DEV)
+    y = torch.empty_like(xd)
+    _capi.call("sph_tri", upper, diag, 2, _p(xd), _p(y), 3, 9, 13, _stream())
+    _sync()
+    want = torch.triu(x, diag) if upper else torch.tril(x, diag)
+    assert torch.equal(y.cpu(), want)
+
+
+def test_rope():
+    _log("rope")
+    x = randn((2048, 32, 128), k=4)
+    pos = torch.arange(2048, dtype=torch.int64)
+    xd, pd = x.to(DEV), pos.to(DEV)
+    y = torch.empty_like(xd)
+    _capi.call("sph_rope", _capi.F16, _p(xd), _p(y), _p(pd), 2048, 32, 128, 1e4, _stream())
+    _sync()
+    assert_close_fp(y, O.rope(x.numpy(), pos.numpy(), 1e4), what="rope")
+
+
+@pytest.mark.parametrize("shape,order,dtype", [([512, 256], [0, 1], torch.float16),
+                                               ([512, 256], [1, 0], torch.float16),
+                                               ([512, 8, 256], [2, 1, 0], torch.float16),
+                                               ([3, 100], [0, 1], torch.float32),
+                                               ([2, 3, 5, 70], [1, 3, 0, 2], torch.int8),
+                                               ([4096, 4096], [1, 0], torch.float16)])
+def test_stick_pack_unpack_bit_exact(shape, order, dtype):
+    _log(f"stick {shape} {order} {dtype}")
+    if dtype.is_floating_point:
+        x = randn(shape, k=5, dtype=dtype)
+    else:
+        x = torch.randint(-100, 100, shape, generator=torch.Generator().manual_seed(7)).to(dtype)
+    eb = x.element_size()
+    nbytes = L.stick_nbytes(shape, eb, order)
+    xd = x.to(DEV)
+    dev = torch.full((nbytes,), 0x5A, dtype=torch.uint8, device=DEV)
+    _capi.call("sph_stick_pack", _p(xd), _p(dev), len(shape), _capi.i64_array(shape),
+               _capi.i64_array(list(xd.stride())), _capi.i32_array(order), eb, _stream())
+    _sync()
+    np.testing.assert_array_equal(dev.cpu().numpy(), L.stick_pack(x.numpy(), order))
+    back = torch.zeros_like(xd)
+    _capi.call("sph_stick_unpack", _p(dev), _p(back), len(shape), _capi.i64_array(shape),
+               _capi.i64_array(list(back.stride())), _capi.i32_array(order), eb, _stream())
+    _sync()
+    assert torch.equal(back.cpu().view(torch.uint8) if dtype != torch.int8 else back.cpu(),
+                       x.view(torch.uint8) if dtype != torch.int8 else x)

@@ -1,0 +1,444 @@
+// fp16 / bf16 GEMM on gfx950 MFMA (v_mfma_f32_32x32x16_{f16,bf16}), fp32
+// accumulate, with an alpha/beta/bias/activation epilogue.
+//
+// Structure
+//   * Workgroup tile BM x BN, K step 64, WM x WN waves; each wave owns a
+//     (BM/WM) x (BN/WN) block of 32x32 MFMA tiles whose accumulators live in
+//     AGPRs for the whole K loop.
+//   * Both operands are staged in LDS "K-contiguous": tile row r (an M row of
+//     A or an N column of B) holds its 64 K values as eight 16-byte chunks,
+//     chunk c stored at position c ^ (r & 7).  The XOR swizzle makes the
+//     16-byte fragment reads of eight consecutive rows hit eight different
+//     bank groups, and the 16-byte writes of the loaders conflict-free.
+//   * An operand whose K is contiguous in memory (A row-major; B given as
+//     B^T row-major, the nn.Linear weight layout) is copied chunk by chunk.
+//     An operand whose K is strided (B row-major, A transposed) is loaded as
+//     8x8 blocks (eight 16-byte rows) and transposed in registers with byte
+//     permutes before the LDS write.
+//   * Double-buffered LDS with register staging: the global loads of step
+//     k+1 are issued before the MFMAs of step k, one barrier per step.
+//   * Workgroup ids are remapped so that the 8 XCDs (round-robin dispatch)
+//     each get a compact group of C tiles, sharing A rows and B columns in
+//     their own L2.
+#include "sph_common.h"
+
+namespace sph {
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int BK = 64;  // K per LDS stage (eight 16-byte chunks of fp16)
+
+struct GemmArgs {
+  int64_t m, n, k;
+  const void* a;
+  int64_t lda, stride_a;
+  const void* b;
+  int64_t ldb, stride_b;
+  const void* c;
+  int64_t ldc_row, ldc_col, stride_c;
+  void* d;
+  int64_t ldd, stride_d;
+  float alpha, beta;
+  int epilogue;
+  int vec_a, vec_b;
+  int tiles_m, tiles_n;
+};
+
+template <typename T>
+__device__ inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (sizeof(T) == 2 && __is_same(T, half_t)) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(
+        __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+}
+
+__device__ inline u32x4 zero4() {
+  u32x4 z = {0u, 0u, 0u, 0u};
+  return z;
+}
+
+// Reads `n` (< 8) two-byte elements with element stride `es` into a chunk,
+// zero-filling the rest.
+__device__ inline u32x4 load_partial(const uint16_t* p, int n, int64_t es) {
+  uint16_t e[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) e[i] = (i < n) ? p[i * es] : static_cast<uint16_t>(0);
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    r[i] = static_cast<uint32_t>(e[2 * i]) | (static_cast<uint32_t>(e[2 * i + 1]) << 16);
+  return r;
+}
+
+// LDS offset (in 2-byte elements) of chunk c of tile row r.
+__device__ inline int lds_off(int r, int c) { return r * BK + ((c ^ (r & 7)) << 3); }
+
+// ---------------------------------------------------------------------------
+// Tile loaders: global -> registers (issue) and registers -> LDS (commit).
+// `rows` is the tile height (BM for A, BN for B); r0 the first global row
+// (M index for A, N index for B); nrows the matrix extent in that dim.
+// ---------------------------------------------------------------------------
+
+// K-contiguous operand: element (r, k) at base[r * ld + k].
+template <int ROWS, int NT>
+struct KContLoader {
+  static constexpr int PER_T = (ROWS * 8 + NT - 1) / NT;
+  u32x4 reg[PER_T];
+
+  __device__ inline void issue(const uint16_t* __restrict__ base, int64_t ld,
+                               int64_t r0, int64_t nrows, int64_t k0,
+                               int64_t kdim, bool vec) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int idx = t + i * NT;
+      const int r = idx >> 3, c = idx & 7;
+      const int64_t gr = r0 + r, gk = k0 + c * 8;
+      if ((ROWS * 8) % NT != 0 && idx >= ROWS * 8) continue;
+      if (gr < nrows && vec && gk + 8 <= kdim) {
+        reg[i] = *reinterpret_cast<const u32x4*>(base + gr * ld + gk);
+      } else if (gr < nrows && gk < kdim) {
+        const int64_t n = kdim - gk;
+        reg[i] = load_partial(base + gr * ld + gk, n > 8 ? 8 : static_cast<int>(n), 1);
+      } else {
+        reg[i] = zero4();
+      }
+    }
+  }
+
+  __device__ inline void commit(uint16_t* __restrict__ lds) const {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int idx = t + i * NT;
+      if ((ROWS * 8) % NT != 0 && idx >= ROWS * 8) continue;
+      const int r = idx >> 3, c = idx & 7;
+      *reinterpret_cast<u32x4*>(lds + lds_off(r, c)) = reg[i];
+    }
+  }
+};
+
+// K-strided operand: element (r, k) at base[k * ld + r].  Loaded as 8x8
+// blocks: block (rb, kb) covers rows 8rb..8rb+7 and k 8kb..8kb+7; the 8
+// global loads are along r (16 bytes each), the block is transposed in
+// registers so each LDS write is one 16-byte K chunk of one row.
+template <int ROWS, int NT>
+struct KStridedLoader {
+  static constexpr int NB = ROWS;  // (ROWS / 8) r-blocks x 8 k-blocks
+  static constexpr int PER_T = (NB + NT - 1) / NT;
+  u32x4 reg[PER_T][8];
+
+  __device__ inline void issue(const uint16_t* __restrict__ base, int64_t ld,
+                               int64_t r0, int64_t nrows, int64_t k0,
+                               int64_t kdim, bool vec) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int idx = t + i * NT;
+      if (NB % NT != 0 && idx >= NB) continue;
+      const int kb = idx & 7, rb = idx >> 3;
+      const int64_t gr = r0 + rb * 8;
+#pragma unroll
+      for (int kr = 0; kr < 8; ++kr) {
+        const int64_t gk = k0 + kb * 8 + kr;
+        if (gk < kdim && vec && gr + 8 <= nrows) {
+          reg[i][kr] = *reinterpret_cast<const u32x4*>(base + gk * ld + gr);
+        } else if (gk < kdim && gr < nrows) {
+          const int64_t n = nrows - gr;
+          reg[i][kr] = load_partial(base + gk * ld + gr, n > 8 ? 8 : static_cast<int>(n), 1);
+        } else {
+          reg[i][kr] = zero4();
+        }
+      }
+    }
+  }
+
+  __device__ inline void commit(uint16_t* __restrict__ lds) const {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int idx = t + i * NT;
+      if (NB % NT != 0 && idx >= NB) continue;
+      const int kb = idx & 7, rb = idx >> 3;
+      // reg[i][kr] dword q holds rows (2q, 2q+1) of k row kr.  Output row j
+      // (= r offset) dword p holds k values (2p, 2p+1).
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        u32x4 o;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const uint32_t lo = reg[i][2 * p][j >> 1];
+          const uint32_t hi = reg[i][2 * p + 1][j >> 1];
+          o[p] = (j & 1) ? __builtin_amdgcn_perm(hi, lo, 0x07060302u)
+                         : __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+        }
+        const int r = rb * 8 + j;
+        *reinterpret_cast<u32x4*>(lds + lds_off(r, kb)) = o;
+      }
+    }
+  }
+};
+
+template <bool KCONT, int ROWS, int NT>
+struct LoaderSel;
+template <int ROWS, int NT>
+struct LoaderSel<true, ROWS, NT> {
+  using type = KContLoader<ROWS, NT>;
+};
+template <int ROWS, int NT>
+struct LoaderSel<false, ROWS, NT> {
+  using type = KStridedLoader<ROWS, NT>;
+};
+
+__device__ inline float apply_epilogue(float v, int epi) {
+  switch (epi) {
+    case SPH_EPI_RELU:
+      return fmaxf(v, 0.f);
+    case SPH_EPI_GELU:
+      return gelu_erf(v);
+    case SPH_EPI_SILU:
+      return silu(v);
+    default:
+      return v;
+  }
+}
+
+// Maps the linear workgroup id to a (tile_m, tile_n) pair: ids are first
+// regrouped so that consecutive ids run on one XCD (dispatch is round-robin
+// over 8 XCDs), then walked in GROUP_M-row bands for L2 reuse.
+__device__ inline void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int nt = tiles_m * tiles_n;
+  if ((nt & 7) == 0) bid = (bid & 7) * (nt >> 3) + (bid >> 3);
+  constexpr int GROUP_M = 4;
+  const int per_group = GROUP_M * tiles_n;
+  const int g = bid / per_group;
+  const int first_m = g * GROUP_M;
+  const int gm = (tiles_m - first_m) < GROUP_M ? (tiles_m - first_m) : GROUP_M;
+  const int in_g = bid - g * per_group;
+  tm = first_m + in_g % gm;
+  tn = in_g / gm;
+}
+
+template <typename T, int BM, int BN, int WM, int WN, bool A_KCONT, bool B_KCONT>
+__global__ void __launch_bounds__(WM * WN * 64)
+gemm_kernel(const GemmArgs p) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int TM = BM / WM / 32;  // MFMA tiles per wave along M
+  constexpr int TN = BN / WN / 32;
+  static_assert(TM >= 1 && TN >= 1, "wave tile too small");
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2][(BM + BN) * BK];
+
+  int tm, tn;
+  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int64_t batch = blockIdx.y;
+  const uint16_t* A = static_cast<const uint16_t*>(p.a) + batch * p.stride_a;
+  const uint16_t* B = static_cast<const uint16_t*>(p.b) + batch * p.stride_b;
+  const int64_t m0 = static_cast<int64_t>(tm) * BM;
+  const int64_t n0 = static_cast<int64_t>(tn) * BN;
+
+  typename LoaderSel<A_KCONT, BM, NT>::type la;
+  typename LoaderSel<B_KCONT, BN, NT>::type lb;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int row_in = lane & 31;  // fragment row within a 32x32 tile
+  const int khalf = lane >> 5;   // which 8-wide K half of a 16-K step
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int64_t ksteps = (p.k + BK - 1) / BK;
+  if (ksteps > 0) {
+    la.issue(A, p.lda, m0, p.m, 0, p.k, p.vec_a);
+    lb.issue(B, p.ldb, n0, p.n, 0, p.k, p.vec_b);
+    la.commit(lds[0]);
+    lb.commit(lds[0] + BM * BK);
+    __syncthreads();
+  }
+  for (int64_t ks = 0; ks < ksteps; ++ks) {
+    const int cur = ks & 1;
+    const bool more = ks + 1 < ksteps;
+    if (more) {
+      la.issue(A, p.lda, m0, p.m, (ks + 1) * BK, p.k, p.vec_a);
+      lb.issue(B, p.ldb, n0, p.n, (ks + 1) * BK, p.k, p.vec_b);
+    }
+    const uint16_t* sa = lds[cur];
+    const uint16_t* sb = lds[cur] + BM * BK;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      u32x4 af[TM], bf[TN];
+      const int c = kk * 2 + khalf;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = wm * (BM / WM) + i * 32 + row_in;
+        af[i] = *reinterpret_cast<const u32x4*>(sa + lds_off(r, c));
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int r = wn * (BN / WN) + j * 32 + row_in;
+        bf[j] = *reinterpret_cast<const u32x4*>(sb + lds_off(r, c));
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<T>(af[i], bf[j], acc[i][j]);
+    }
+    if (more) {
+      la.commit(lds[cur ^ 1]);
+      lb.commit(lds[cur ^ 1] + BM * BK);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue.  Accumulator register r of tile (i, j) holds
+  // row 8*(r/4) + 4*(lane/32) + r%4, column lane%32 of that 32x32 tile.
+  T* D = static_cast<T*>(p.d) + batch * p.stride_d;
+  const T* C = p.c ? static_cast<const T*>(p.c) + batch * p.stride_c : nullptr;
+  const bool use_c = C != nullptr && p.beta != 0.f;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col = n0 + wn * (BN / WN) + j * 32 + (lane & 31);
+      if (col >= p.n) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * (BM / WM) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if (row >= p.m) continue;
+        float v = p.alpha * acc[i][j][r];
+        if (use_c) v += p.beta * Num<T>::to_f(C[row * p.ldc_row + col * p.ldc_col]);
+        v = apply_epilogue(v, p.epilogue);
+        D[row * p.ldd + col] = Num<T>::from_f(v);
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+template <typename T, int BM, int BN, int WM, int WN>
+int launch_cfg(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
+               hipStream_t st) {
+  p.tiles_m = static_cast<int>(ceil_div(p.m, BM));
+  p.tiles_n = static_cast<int>(ceil_div(p.n, BN));
+  dim3 grid(static_cast<unsigned>(p.tiles_m) * p.tiles_n, static_cast<unsigned>(batch));
+  dim3 block(WM * WN * 64);
+  if (a_kcont && b_kcont)
+    gemm_kernel<T, BM, BN, WM, WN, true, true><<<grid, block, 0, st>>>(p);
+  else if (a_kcont && !b_kcont)
+    gemm_kernel<T, BM, BN, WM, WN, true, false><<<grid, block, 0, st>>>(p);
+  else if (!a_kcont && b_kcont)
+    gemm_kernel<T, BM, BN, WM, WN, false, true><<<grid, block, 0, st>>>(p);
+  else
+    gemm_kernel<T, BM, BN, WM, WN, false, false><<<grid, block, 0, st>>>(p);
+  return check_launch("sph_gemm");
+}
+
+inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Chooses a tile configuration from the problem shape: 256x256 tiles when
+// they give at least one tile per CU, else 128x128 (more workgroups for the
+// 256 CUs), else 64x64 for small problems.
+template <typename T>
+int gemm_dispatch(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
+                  hipStream_t st) {
+  const int64_t t256 = ceil_div(p.m, 256) * ceil_div(p.n, 256) * batch;
+  const int64_t t128 = ceil_div(p.m, 128) * ceil_div(p.n, 128) * batch;
+  if (t256 >= 256) return launch_cfg<T, 256, 256, 2, 2>(p, batch, a_kcont, b_kcont, st);
+  if (t128 >= 128) return launch_cfg<T, 128, 128, 2, 2>(p, batch, a_kcont, b_kcont, st);
+  return launch_cfg<T, 64, 64, 2, 2>(p, batch, a_kcont, b_kcont, st);
+}
+
+}  // namespace
+}  // namespace sph
+
+using namespace sph;
+
+extern "C" int sph_gemm_strided_batched(
+    sph_dtype dtype, int trans_a, int trans_b, int64_t batch, int64_t m,
+    int64_t n, int64_t k, float alpha, const void* a, int64_t lda,
+    int64_t stride_a, const void* b, int64_t ldb, int64_t stride_b, float beta,
+    const void* c, int64_t ldc_row, int64_t ldc_col, int64_t stride_c, void* d,
+    int64_t ldd, int64_t stride_d, int epilogue, sph_stream_t stream) {
+  SPH_REQUIRE(m >= 0 && n >= 0 && k >= 0 && batch >= 0, SPH_ERR_INVALID_ARG,
+              "gemm: negative size");
+  SPH_REQUIRE(dtype == SPH_F16 || dtype == SPH_BF16, SPH_ERR_UNSUPPORTED,
+              "gemm: dtype must be F16 or BF16");
+  SPH_REQUIRE(epilogue >= SPH_EPI_NONE && epilogue <= SPH_EPI_SILU,
+              SPH_ERR_INVALID_ARG, "gemm: bad epilogue");
+  if (m == 0 || n == 0 || batch == 0) return SPH_OK;
+  SPH_REQUIRE(batch <= 65535, SPH_ERR_TOO_LARGE, "gemm: batch > 65535");
+  SPH_REQUIRE(ldd >= n, SPH_ERR_INVALID_ARG, "gemm: ldd < n");
+  SPH_REQUIRE(k == 0 || (trans_a ? lda >= m : lda >= k), SPH_ERR_INVALID_ARG,
+              "gemm: lda too small");
+  SPH_REQUIRE(k == 0 || (trans_b ? ldb >= k : ldb >= n), SPH_ERR_INVALID_ARG,
+              "gemm: ldb too small");
+  SPH_REQUIRE(ceil_div(m, 64) * ceil_div(n, 64) < (1LL << 31), SPH_ERR_TOO_LARGE,
+              "gemm: too many tiles");
+  GemmArgs p{};
+  p.m = m;
+  p.n = n;
+  p.k = k;
+  p.a = a;
+  p.lda = lda;
+  p.stride_a = stride_a;
+  p.b = b;
+  p.ldb = ldb;
+  p.stride_b = stride_b;
+  p.c = (beta != 0.f) ? c : nullptr;
+  p.ldc_row = ldc_row;
+  p.ldc_col = ldc_col;
+  p.stride_c = stride_c;
+  p.d = d;
+  p.ldd = ldd;
+  p.stride_d = stride_d;
+  p.alpha = alpha;
+  p.beta = beta;
+  p.epilogue = epilogue;
+  // A is K-contiguous unless transposed; B is K-contiguous when transposed.
+  const bool a_kcont = !trans_a, b_kcont = trans_b != 0;
+  // 16-byte vector loads need aligned bases and leading dims (and batch
+  // strides) that keep every row aligned.
+  p.vec_a = al16(a) && (lda % 8 == 0) && (batch == 1 || stride_a % 8 == 0);
+  p.vec_b = al16(b) && (ldb % 8 == 0) && (batch == 1 || stride_b % 8 == 0);
+  hipStream_t st = as_stream(stream);
+  if (dtype == SPH_F16) return gemm_dispatch<half_t>(p, batch, a_kcont, b_kcont, st);
+  return gemm_dispatch<bf16_t>(p, batch, a_kcont, b_kcont, st);
+}
+
+extern "C" int sph_gemm(sph_dtype dtype, int trans_a, int trans_b, int64_t m,
+                        int64_t n, int64_t k, float alpha, const void* a,
+                        int64_t lda, const void* b, int64_t ldb, float beta,
+                        const void* c, int64_t ldc_row, int64_t ldc_col,
+                        void* d, int64_t ldd, int epilogue,
+                        sph_stream_t stream) {
+  return sph_gemm_strided_batched(dtype, trans_a, trans_b, 1, m, n, k, alpha, a,
+                                  lda, 0, b, ldb, 0, beta, c, ldc_row, ldc_col,
+                                  0, d, ldd, 0, epilogue, stream);
+}
+
+extern "C" int sph_gemm_f16(int64_t m, int64_t n, int64_t k, const void* a,
+                            const void* b, void* d, sph_stream_t stream) {
+  return sph_gemm(SPH_F16, 0, 0, m, n, k, 1.0f, a, k, b, n, 0.0f, nullptr, 0, 0,
+                  d, n, SPH_EPI_NONE, stream);
+}
+
+extern "C" int sph_bmm_f16(int64_t batch, int64_t m, int64_t n, int64_t k,
+                           const void* a, const void* b, void* d,
+                           sph_stream_t stream) {
+  return sph_gemm_strided_batched(SPH_F16, 0, 0, batch, m, n, k, 1.0f, a, k,
+                                  m * k, b, n, k * n, 0.0f, nullptr, 0, 0, 0, d,
+                                  n, m * n, SPH_EPI_NONE, stream);
+}
