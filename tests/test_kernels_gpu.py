@@ -452,7 +452,10 @@ def test_gather_rows_embedding():
     t2 = randn((10, 3), k=2)
     i2 = torch.tensor([9, 0, 10, -1, 4], dtype=torch.int32)
     o2 = torch.empty(5, 3, dtype=torch.float16, device=DEV)
-    _capi.call("sph_gather_rows", _p(t2.to(DEV)), 10, 3, 2, _p(i2.to(DEV)), 0, 5, _p(o2), _stream())
+    # keep the device copies referenced until the kernel has run: a dropped
+    # temporary's block is reused by the next allocation
+    t2d, i2d = t2.to(DEV), i2.to(DEV)
+    _capi.call("sph_gather_rows", _p(t2d), 10, 3, 2, _p(i2d), 0, 5, _p(o2), _stream())
     _sync()
     want = torch.stack([t2[9], t2[0], torch.zeros(3, dtype=torch.float16),
                         torch.zeros(3, dtype=torch.float16), t2[4]])
