@@ -3,20 +3,26 @@
 //
 // Structure
 //   * Workgroup tile BM x BN, K step 64, WM x WN waves; each wave owns a
-//     (BM/WM) x (BN/WN) block of 32x32 MFMA tiles whose accumulators live in
-//     AGPRs for the whole K loop.
+//     (BM/WM) x (BN/WN) block of 32x32 MFMA tiles whose fp32 accumulators
+//     stay in registers for the whole K loop.  Whole 256x256 tiles use 8
+//     waves (two per SIMD, so latency hides across waves).
 //   * Both operands are staged in LDS "K-contiguous": tile row r (an M row of
 //     A or an N column of B) holds its 64 K values as eight 16-byte chunks,
-//     chunk c stored at position c ^ (r & 7).  The XOR swizzle makes the
-//     16-byte fragment reads of eight consecutive rows hit eight different
-//     bank groups, and the 16-byte writes of the loaders conflict-free.
+//     chunk c stored at slot c ^ ((r >> 1) & 7), which makes the 16-byte
+//     fragment reads and the loaders' 16-byte writes free of bank conflicts
+//     on gfx950's 64-bank LDS.
 //   * An operand whose K is contiguous in memory (A row-major; B given as
 //     B^T row-major, the nn.Linear weight layout) is copied chunk by chunk.
 //     An operand whose K is strided (B row-major, A transposed) is loaded as
 //     8x8 blocks (eight 16-byte rows) and transposed in registers with byte
 //     permutes before the LDS write.
-//   * Double-buffered LDS with register staging: the global loads of step
-//     k+1 are issued before the MFMAs of step k, one barrier per step.
+//   * Whole tiles (FULL) run a three-deep pipeline without bounds checks:
+//     K tile k is multiplied from one LDS buffer while tile k+1 moves from
+//     registers to the other buffer and tile k+2 is loaded from memory.
+//     Partial tiles use bounds-checked loaders and a two-deep pipeline.
+//   * The epilogue stages each 32-row slab of results in LDS and writes D
+//     as whole rows with 16-byte stores; activation and the C term are
+//     resolved once per slab, not per element.
 //   * Workgroup ids are remapped so that the 8 XCDs (round-robin dispatch)
 //     each get a compact group of C tiles, sharing A rows and B columns in
 //     their own L2.
@@ -43,7 +49,7 @@ struct GemmArgs {
   int64_t ldd, stride_d;
   float alpha, beta;
   int epilogue;
-  int vec_a, vec_b;
+  int vec_a, vec_b, vec_d;
   int tiles_m, tiles_n;
 };
 
@@ -76,8 +82,13 @@ __device__ inline u32x4 load_partial(const uint16_t* p, int n, int64_t es) {
   return r;
 }
 
-// LDS offset (in 2-byte elements) of chunk c of tile row r.
-__device__ inline int lds_off(int r, int c) { return r * BK + ((c ^ (r & 7)) << 3); }
+// LDS offset (in 2-byte elements) of chunk c of tile row r.  gfx950's LDS
+// serves 16 lanes of a 16-byte access per cycle from 64 four-byte banks
+// (a 256-byte window): a 128-byte tile row covers one half of the window
+// (even rows the low half, odd rows the high half), so the eight rows of
+// each parity among 16 consecutive rows must use eight different 16-byte
+// slots, which c ^ ((r >> 1) & 7) guarantees for every fixed c.
+__device__ inline int lds_off(int r, int c) { return r * BK + ((c ^ ((r >> 1) & 7)) << 3); }
 
 // ---------------------------------------------------------------------------
 // Tile loaders: global -> registers (issue) and registers -> LDS (commit).
@@ -89,8 +100,11 @@ __device__ inline int lds_off(int r, int c) { return r * BK + ((c ^ (r & 7)) << 
 template <int ROWS, int NT>
 struct KContLoader {
   static constexpr int PER_T = (ROWS * 8 + NT - 1) / NT;
+  static constexpr int NLOADS = PER_T;  // global loads per issue
   u32x4 reg[PER_T];
 
+  // FULL: the whole tile is in bounds and 16-byte aligned (no checks).
+  template <bool FULL>
   __device__ inline void issue(const uint16_t* __restrict__ base, int64_t ld,
                                int64_t r0, int64_t nrows, int64_t k0,
                                int64_t kdim, bool vec) {
@@ -101,7 +115,7 @@ struct KContLoader {
       const int r = idx >> 3, c = idx & 7;
       const int64_t gr = r0 + r, gk = k0 + c * 8;
       if ((ROWS * 8) % NT != 0 && idx >= ROWS * 8) continue;
-      if (gr < nrows && vec && gk + 8 <= kdim) {
+      if (FULL || (gr < nrows && vec && gk + 8 <= kdim)) {
         reg[i] = *reinterpret_cast<const u32x4*>(base + gr * ld + gk);
       } else if (gr < nrows && gk < kdim) {
         const int64_t n = kdim - gk;
@@ -132,8 +146,10 @@ template <int ROWS, int NT>
 struct KStridedLoader {
   static constexpr int NB = ROWS;  // (ROWS / 8) r-blocks x 8 k-blocks
   static constexpr int PER_T = (NB + NT - 1) / NT;
+  static constexpr int NLOADS = PER_T * 8;
   u32x4 reg[PER_T][8];
 
+  template <bool FULL>
   __device__ inline void issue(const uint16_t* __restrict__ base, int64_t ld,
                                int64_t r0, int64_t nrows, int64_t k0,
                                int64_t kdim, bool vec) {
@@ -147,7 +163,7 @@ struct KStridedLoader {
 #pragma unroll
       for (int kr = 0; kr < 8; ++kr) {
         const int64_t gk = k0 + kb * 8 + kr;
-        if (gk < kdim && vec && gr + 8 <= nrows) {
+        if (FULL || (gk < kdim && vec && gr + 8 <= nrows)) {
           reg[i][kr] = *reinterpret_cast<const u32x4*>(base + gk * ld + gr);
         } else if (gk < kdim && gr < nrows) {
           const int64_t n = nrows - gr;
@@ -167,18 +183,22 @@ struct KStridedLoader {
       if (NB % NT != 0 && idx >= NB) continue;
       const int kb = idx & 7, rb = idx >> 3;
       // reg[i][kr] dword q holds rows (2q, 2q+1) of k row kr.  Output row j
-      // (= r offset) dword p holds k values (2p, 2p+1).
+      // (= r offset) dword p holds k values (2p, 2p+1).  Lanes of odd r
+      // blocks write rows in the order 1,0,3,2,... so that the 16 lanes of
+      // one LDS write cycle (two r blocks) cover rows of both parities.
+      const int flip = rb & 1;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
+        const int jj = j ^ flip;
+        const uint32_t sel = (jj & 1) ? 0x07060302u : 0x05040100u;
         u32x4 o;
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
           const uint32_t lo = reg[i][2 * p][j >> 1];
           const uint32_t hi = reg[i][2 * p + 1][j >> 1];
-          o[p] = (j & 1) ? __builtin_amdgcn_perm(hi, lo, 0x07060302u)
-                         : __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+          o[p] = __builtin_amdgcn_perm(hi, lo, sel);
         }
-        const int r = rb * 8 + j;
+        const int r = rb * 8 + jj;
         *reinterpret_cast<u32x4*>(lds + lds_off(r, kb)) = o;
       }
     }
@@ -196,18 +216,6 @@ struct LoaderSel<false, ROWS, NT> {
   using type = KStridedLoader<ROWS, NT>;
 };
 
-__device__ inline float apply_epilogue(float v, int epi) {
-  switch (epi) {
-    case SPH_EPI_RELU:
-      return fmaxf(v, 0.f);
-    case SPH_EPI_GELU:
-      return gelu_erf(v);
-    case SPH_EPI_SILU:
-      return silu(v);
-    default:
-      return v;
-  }
-}
 
 // Maps the linear workgroup id to a (tile_m, tile_n) pair: ids are first
 // regrouped so that consecutive ids run on one XCD (dispatch is round-robin
@@ -225,14 +233,110 @@ __device__ inline void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& 
   tn = in_g / gm;
 }
 
-template <typename T, int BM, int BN, int WM, int WN, bool A_KCONT, bool B_KCONT>
+// Writes one 32 x WTN slab of fp32 results (LDS, row pitch EPITCH floats)
+// to D rows row0.., columns col0.. as D = epi(alpha * slab + beta * C).
+// Lane l handles columns 8*(l % (WTN/8)) .. +7 of rows l / (WTN/8) + k*RPP.
+// The activation and the C term are resolved outside the row loop.
+template <typename T, int EPI, bool USE_C, int WTN, int EPITCH>
+__device__ inline void store_slab_impl(const GemmArgs& p, const float* slab, T* D,
+                                       const T* C, int64_t row0, int64_t col0,
+                                       int lane) {
+  constexpr int LPR = WTN / 8;   // lanes per row
+  constexpr int RPP = 64 / LPR;  // rows per pass
+  const int er = lane / LPR, ec = (lane % LPR) * 8;
+  const int64_t col = col0 + ec;
+  if (col >= p.n) return;
+  const bool full_cols = p.vec_d && col + 8 <= p.n;
+  const int ncols = p.n - col >= 8 ? 8 : static_cast<int>(p.n - col);
+  // Lanes whose 8-column group has bit 3 set read the two 16-byte halves
+  // in the opposite order, so each LDS read cycle touches 64 distinct banks.
+  const int sw = (lane >> 3) & 1;
+#pragma unroll 1
+  for (int rr = er; rr < 32; rr += RPP) {
+    const int64_t row = row0 + rr;
+    if (row >= p.m) break;
+    const u32x4* sp = reinterpret_cast<const u32x4*>(slab + rr * EPITCH + ec);
+    const u32x4 h0 = sp[sw], h1 = sp[sw ^ 1];
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = __builtin_bit_cast(float, sw ? h1[e] : h0[e]);
+      v[e + 4] = __builtin_bit_cast(float, sw ? h0[e] : h1[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float x = p.alpha * v[e];
+      if constexpr (USE_C) {
+        if (e < ncols) x += p.beta * Num<T>::to_f(C[row * p.ldc_row + (col + e) * p.ldc_col]);
+      }
+      if constexpr (EPI == SPH_EPI_RELU) x = fmaxf(x, 0.f);
+      if constexpr (EPI == SPH_EPI_GELU) x = gelu_erf(x);
+      if constexpr (EPI == SPH_EPI_SILU) x = silu(x);
+      v[e] = x;
+    }
+    T* dp = D + row * p.ldd + col;
+    if (full_cols)
+      store8<T>(dp, v);
+    else
+      store8_partial<T>(dp, ncols, v);
+  }
+}
+
+template <typename T, int WTN, int EPITCH>
+__device__ inline void store_slab(const GemmArgs& p, const float* slab, T* D, const T* C,
+                                  int64_t row0, int64_t col0, int lane) {
+  const bool use_c = C != nullptr && p.beta != 0.f;
+#define SPH_EPI_CASE(E)                                                            \
+  if (use_c)                                                                       \
+    store_slab_impl<T, E, true, WTN, EPITCH>(p, slab, D, C, row0, col0, lane);     \
+  else                                                                             \
+    store_slab_impl<T, E, false, WTN, EPITCH>(p, slab, D, C, row0, col0, lane);
+  switch (p.epilogue) {
+    case SPH_EPI_RELU:
+      SPH_EPI_CASE(SPH_EPI_RELU);
+      break;
+    case SPH_EPI_GELU:
+      SPH_EPI_CASE(SPH_EPI_GELU);
+      break;
+    case SPH_EPI_SILU:
+      SPH_EPI_CASE(SPH_EPI_SILU);
+      break;
+    default:
+      SPH_EPI_CASE(SPH_EPI_NONE);
+  }
+#undef SPH_EPI_CASE
+}
+
+// Reads the MFMA fragments of K sub-step kk (16 K values) for this wave.
+template <int TM, int TN, int WTM, int WTN>
+__device__ inline void load_frags(const uint16_t* __restrict__ sa,
+                                  const uint16_t* __restrict__ sb, int wm,
+                                  int wn, int row_in, int khalf, int kk,
+                                  u32x4 (&af)[TM], u32x4 (&bf)[TN]) {
+  const int c = kk * 2 + khalf;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+    af[i] = *reinterpret_cast<const u32x4*>(sa + lds_off(wm * WTM + i * 32 + row_in, c));
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+    bf[j] = *reinterpret_cast<const u32x4*>(sb + lds_off(wn * WTN + j * 32 + row_in, c));
+}
+
+template <typename T, int BM, int BN, int WM, int WN, bool A_KCONT, bool B_KCONT,
+          bool FULL>
 __global__ void __launch_bounds__(WM * WN * 64)
 gemm_kernel(const GemmArgs p) {
   constexpr int NT = WM * WN * 64;
-  constexpr int TM = BM / WM / 32;  // MFMA tiles per wave along M
-  constexpr int TN = BN / WN / 32;
+  constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
+  constexpr int TM = WTM / 32;                 // 32x32 MFMA tiles per wave along M
+  constexpr int TN = WTN / 32;
+  constexpr int STAGE = (BM + BN) * BK;        // LDS elements per pipeline stage
+  // Epilogue staging: per wave one 32-row slab of fp32 accumulators, rows
+  // padded by 8 floats so the two half-waves' rows land on different banks.
+  constexpr int EPITCH = WTN + 8;
   static_assert(TM >= 1 && TN >= 1, "wave tile too small");
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2][(BM + BN) * BK];
+  static_assert(WM * WN * 32 * EPITCH * 4 <= 2 * STAGE * 2, "epilogue staging exceeds LDS");
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * STAGE];
 
   int tm, tn;
   tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
@@ -260,89 +364,168 @@ gemm_kernel(const GemmArgs p) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int64_t ksteps = (p.k + BK - 1) / BK;
-  if (ksteps > 0) {
-    la.issue(A, p.lda, m0, p.m, 0, p.k, p.vec_a);
-    lb.issue(B, p.ldb, n0, p.n, 0, p.k, p.vec_b);
-    la.commit(lds[0]);
-    lb.commit(lds[0] + BM * BK);
+  if constexpr (FULL) {
+    // Three-deep pipeline over K tiles: while the MFMAs consume tile ks
+    // from LDS buffer ks&1, tile ks+1 (loaded into registers during the
+    // previous step) is written to the other buffer, and tile ks+2 is
+    // loaded from global memory into the freed registers.  Global loads
+    // thus have a whole K step to land and the LDS writes never wait.
+    // The body is branch-free (one scheduling region): indices past the
+    // last tile are clamped, re-loading and re-writing the last tile into
+    // the idle buffer, which nothing reads afterwards.
+    const int64_t klast = (ksteps - 1) * BK;
+    la.template issue<true>(A, p.lda, m0, p.m, 0, p.k, true);
+    lb.template issue<true>(B, p.ldb, n0, p.n, 0, p.k, true);
+    la.commit(lds);
+    lb.commit(lds + BM * BK);
+    const int64_t k1 = BK < klast ? BK : klast;
+    la.template issue<true>(A, p.lda, m0, p.m, k1, p.k, true);
+    lb.template issue<true>(B, p.ldb, n0, p.n, k1, p.k, true);
     __syncthreads();
-  }
-  for (int64_t ks = 0; ks < ksteps; ++ks) {
-    const int cur = ks & 1;
-    const bool more = ks + 1 < ksteps;
-    if (more) {
-      la.issue(A, p.lda, m0, p.m, (ks + 1) * BK, p.k, p.vec_a);
-      lb.issue(B, p.ldb, n0, p.n, (ks + 1) * BK, p.k, p.vec_b);
-    }
-    const uint16_t* sa = lds[cur];
-    const uint16_t* sb = lds[cur] + BM * BK;
+    for (int64_t ks = 0; ks < ksteps; ++ks) {
+      const int cur = static_cast<int>(ks & 1);
+      const uint16_t* sa = lds + cur * STAGE;
+      const uint16_t* sb = sa + BM * BK;
+      u32x4 af[2][TM], bf[2][TN];
+      load_frags<TM, TN, WTM, WTN>(sa, sb, wm, wn, row_in, khalf, 0, af[0], bf[0]);
 #pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      u32x4 af[TM], bf[TN];
-      const int c = kk * 2 + khalf;
+      for (int kk = 0; kk < BK / 16; ++kk) {
+        if (kk + 1 < BK / 16)
+          load_frags<TM, TN, WTM, WTN>(sa, sb, wm, wn, row_in, khalf, kk + 1,
+                                       af[(kk + 1) & 1], bf[(kk + 1) & 1]);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int r = wm * (BM / WM) + i * 32 + row_in;
-        af[i] = *reinterpret_cast<const u32x4*>(sa + lds_off(r, c));
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = mfma32<T>(af[kk & 1][i], bf[kk & 1][j], acc[i][j]);
       }
+      la.commit(lds + (cur ^ 1) * STAGE);
+      lb.commit(lds + (cur ^ 1) * STAGE + BM * BK);
+      const int64_t k2 = (ks + 2) * BK < klast ? (ks + 2) * BK : klast;
+      la.template issue<true>(A, p.lda, m0, p.m, k2, p.k, true);
+      lb.template issue<true>(B, p.ldb, n0, p.n, k2, p.k, true);
+      // Instruction order for the scheduler (one wave per SIMD, so latency
+      // must be hidden inside the wave): fragment reads of sub-step 0;
+      // sub-steps 0-2 alternate MFMAs with the next sub-step's fragment
+      // reads; sub-step 3 interleaves each MFMA with the register
+      // transposes, LDS writes and global loads of the pipeline.
+      constexpr int NMF = TM * TN, NDS = TM + TN;
+      constexpr int NVM = decltype(la)::NLOADS + decltype(lb)::NLOADS;
+      constexpr int IO_PER = (NVM + NMF - 1) / NMF;  // one LDS write per global load
+      // Sub-step kk's MFMAs run only after all fragment reads of sub-step
+      // kk+1 were issued, so those reads overlap a whole sub-step of MFMAs.
+      // (With two or more waves per SIMD the hardware interleaves waves and
+      // the compiler's own order is kept.)
+      if constexpr (WM * WN == 4) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * NDS, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, NMF, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, NMF, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, NMF, 0);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int r = wn * (BN / WN) + j * 32 + row_in;
-        bf[j] = *reinterpret_cast<const u32x4*>(sb + lds_off(r, c));
+      for (int x = 0; x < NMF; ++x) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, IO_PER, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, IO_PER, 0);
       }
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<T>(af[i], bf[j], acc[i][j]);
+      }
+      __syncthreads();
     }
-    if (more) {
-      la.commit(lds[cur ^ 1]);
-      lb.commit(lds[cur ^ 1] + BM * BK);
+  } else {
+    if (ksteps > 0) {
+      la.template issue<false>(A, p.lda, m0, p.m, 0, p.k, p.vec_a);
+      lb.template issue<false>(B, p.ldb, n0, p.n, 0, p.k, p.vec_b);
+      la.commit(lds);
+      lb.commit(lds + BM * BK);
+      __syncthreads();
     }
-    __syncthreads();
+    for (int64_t ks = 0; ks < ksteps; ++ks) {
+      const int cur = static_cast<int>(ks & 1);
+      const bool more = ks + 1 < ksteps;
+      if (more) {
+        la.template issue<false>(A, p.lda, m0, p.m, (ks + 1) * BK, p.k, p.vec_a);
+        lb.template issue<false>(B, p.ldb, n0, p.n, (ks + 1) * BK, p.k, p.vec_b);
+      }
+      const uint16_t* sa = lds + cur * STAGE;
+      const uint16_t* sb = sa + BM * BK;
+      u32x4 af[2][TM], bf[2][TN];
+      load_frags<TM, TN, WTM, WTN>(sa, sb, wm, wn, row_in, khalf, 0, af[0], bf[0]);
+#pragma unroll
+      for (int kk = 0; kk < BK / 16; ++kk) {
+        if (kk + 1 < BK / 16)
+          load_frags<TM, TN, WTM, WTN>(sa, sb, wm, wn, row_in, khalf, kk + 1,
+                                       af[(kk + 1) & 1], bf[(kk + 1) & 1]);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = mfma32<T>(af[kk & 1][i], bf[kk & 1][j], acc[i][j]);
+      }
+      if (more) {
+        la.commit(lds + (cur ^ 1) * STAGE);
+        lb.commit(lds + (cur ^ 1) * STAGE + BM * BK);
+      }
+      __syncthreads();
+    }
   }
 
-  // Epilogue.  Accumulator register r of tile (i, j) holds
-  // row 8*(r/4) + 4*(lane/32) + r%4, column lane%32 of that 32x32 tile.
+  // Epilogue.  Accumulator register r of tile (i, j) holds row
+  // 8*(r/4) + 4*(lane/32) + r%4, column lane%32 of that 32x32 tile.  Each
+  // 32-row slab of the wave tile goes through LDS so that the output is
+  // written as whole rows with 16-byte stores.
   T* D = static_cast<T*>(p.d) + batch * p.stride_d;
   const T* C = p.c ? static_cast<const T*>(p.c) + batch * p.stride_c : nullptr;
-  const bool use_c = C != nullptr && p.beta != 0.f;
+  float* slab = reinterpret_cast<float*>(lds) + wave * (32 * EPITCH);
+  const int64_t row0 = m0 + wm * WTM;
+  const int64_t colw = n0 + wn * WTN;
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t col = n0 + wn * (BN / WN) + j * 32 + (lane & 31);
-      if (col >= p.n) continue;
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * (BM / WM) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        if (row >= p.m) continue;
-        float v = p.alpha * acc[i][j][r];
-        if (use_c) v += p.beta * Num<T>::to_f(C[row * p.ldc_row + col * p.ldc_col]);
-        v = apply_epilogue(v, p.epilogue);
-        D[row * p.ldd + col] = Num<T>::from_f(v);
-      }
-    }
+      for (int r = 0; r < 16; ++r)
+        slab[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * EPITCH + j * 32 + (lane & 31)] =
+            acc[i][j][r];
+    __syncthreads();
+    store_slab<T, WTN, EPITCH>(p, slab, D, C, row0 + i * 32, colw, lane);
+    __syncthreads();
+  }
 }
 
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-template <typename T, int BM, int BN, int WM, int WN>
+template <typename T, int BM, int BN, int WM, int WN, bool FULL>
+void launch_full(const GemmArgs& p, dim3 grid, dim3 block, bool a_kcont, bool b_kcont,
+                 hipStream_t st) {
+  if (a_kcont && b_kcont)
+    gemm_kernel<T, BM, BN, WM, WN, true, true, FULL><<<grid, block, 0, st>>>(p);
+  else if (a_kcont && !b_kcont)
+    gemm_kernel<T, BM, BN, WM, WN, true, false, FULL><<<grid, block, 0, st>>>(p);
+  else if (!a_kcont && b_kcont)
+    gemm_kernel<T, BM, BN, WM, WN, false, true, FULL><<<grid, block, 0, st>>>(p);
+  else
+    gemm_kernel<T, BM, BN, WM, WN, false, false, FULL><<<grid, block, 0, st>>>(p);
+}
+
+// Launches BM x BN tiles: whole tiles with the FULL kernel on WMF x WNF
+// waves, otherwise the checked kernel on WMP x WNP waves.
+template <typename T, int BM, int BN, int WMF, int WNF, int WMP, int WNP>
 int launch_cfg(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
                hipStream_t st) {
   p.tiles_m = static_cast<int>(ceil_div(p.m, BM));
   p.tiles_n = static_cast<int>(ceil_div(p.n, BN));
   dim3 grid(static_cast<unsigned>(p.tiles_m) * p.tiles_n, static_cast<unsigned>(batch));
-  dim3 block(WM * WN * 64);
-  if (a_kcont && b_kcont)
-    gemm_kernel<T, BM, BN, WM, WN, true, true><<<grid, block, 0, st>>>(p);
-  else if (a_kcont && !b_kcont)
-    gemm_kernel<T, BM, BN, WM, WN, true, false><<<grid, block, 0, st>>>(p);
-  else if (!a_kcont && b_kcont)
-    gemm_kernel<T, BM, BN, WM, WN, false, true><<<grid, block, 0, st>>>(p);
+  // Every tile whole and every operand row 16-byte aligned: no bounds or
+  // alignment checks in the K loop.
+  const bool full = p.m % BM == 0 && p.n % BN == 0 && p.k % BK == 0 && p.k > 0 &&
+                    p.vec_a && p.vec_b;
+  if (full)
+    launch_full<T, BM, BN, WMF, WNF, true>(p, grid, dim3(WMF * WNF * 64), a_kcont, b_kcont, st);
   else
-    gemm_kernel<T, BM, BN, WM, WN, false, false><<<grid, block, 0, st>>>(p);
+    launch_full<T, BM, BN, WMP, WNP, false>(p, grid, dim3(WMP * WNP * 64), a_kcont, b_kcont, st);
   return check_launch("sph_gemm");
 }
 
@@ -356,9 +539,13 @@ int gemm_dispatch(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
                   hipStream_t st) {
   const int64_t t256 = ceil_div(p.m, 256) * ceil_div(p.n, 256) * batch;
   const int64_t t128 = ceil_div(p.m, 128) * ceil_div(p.n, 128) * batch;
-  if (t256 >= 256) return launch_cfg<T, 256, 256, 2, 2>(p, batch, a_kcont, b_kcont, st);
-  if (t128 >= 128) return launch_cfg<T, 128, 128, 2, 2>(p, batch, a_kcont, b_kcont, st);
-  return launch_cfg<T, 64, 64, 2, 2>(p, batch, a_kcont, b_kcont, st);
+  // 256x256 whole tiles run 8 waves (128x64 each, two per SIMD, so one
+  // wave's LDS and global-load latency hides under the other's MFMAs);
+  // partial tiles keep 4 waves, whose bounds-checked loaders need the
+  // larger per-wave register budget.
+  if (t256 >= 256) return launch_cfg<T, 256, 256, 2, 4, 2, 2>(p, batch, a_kcont, b_kcont, st);
+  if (t128 >= 128) return launch_cfg<T, 128, 128, 2, 2, 2, 2>(p, batch, a_kcont, b_kcont, st);
+  return launch_cfg<T, 64, 64, 2, 2, 2, 2>(p, batch, a_kcont, b_kcont, st);
 }
 
 }  // namespace
@@ -413,6 +600,7 @@ extern "C" int sph_gemm_strided_batched(
   // strides) that keep every row aligned.
   p.vec_a = al16(a) && (lda % 8 == 0) && (batch == 1 || stride_a % 8 == 0);
   p.vec_b = al16(b) && (ldb % 8 == 0) && (batch == 1 || stride_b % 8 == 0);
+  p.vec_d = al16(d) && (ldd % 8 == 0) && (batch == 1 || stride_d % 8 == 0);
   hipStream_t st = as_stream(stream);
   if (dtype == SPH_F16) return gemm_dispatch<half_t>(p, batch, a_kcont, b_kcont, st);
   return gemm_dispatch<bf16_t>(p, batch, a_kcont, b_kcont, st);
