@@ -1,0 +1,102 @@
+// torch_spyre._C: the Python face of the spyre backend's native runtime.
+//
+// Reference: PYBIND11_MODULE(_C) in torch_spyre/csrc/module.cpp:174-204
+// (start_runtime, free_runtime, launch_kernel, SpyreTensorLayout with its
+// StickFormat enum, three constructors, five fields and __str__).  Loading
+// this module also registers the allocator, the device guard, the
+// PrivateUse1 hooks and every eager ATen kernel (static registrations in the
+// other translation units).
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+#include <torch/extension.h>
+
+#include "spyre_layout.h"
+#include "spyre_runtime.h"
+
+namespace py = pybind11;
+
+namespace spyre {
+// Compiled-kernel launcher (ops_launch.cpp).
+void launch_kernel(const std::string& spec, const std::vector<at::Tensor>& args);
+}  // namespace spyre
+
+PYBIND11_MODULE(_C, m) {
+  m.doc() = "torch_spyre native runtime for MI355X (gfx950)";
+
+  m.def("start_runtime", &spyre::start_runtime, "Probes the HIP devices (idempotent).");
+  m.def("free_runtime", &spyre::free_runtime,
+        "Releases cached device memory and the spyre streams.");
+  m.def("launch_kernel", &spyre::launch_kernel, py::arg("spec"), py::arg("args"),
+        "Runs a compiled kernel spec on tensors (the last argument is the output).");
+
+  m.def("device_count", []() { return spyre::device_count(); });
+  m.def("current_device", []() { return spyre::current_device(); });
+  m.def("set_device", [](int d) { spyre::set_device(d); });
+  m.def("synchronize", [](int d) {
+    py::gil_scoped_release nogil;
+    spyre::synchronize(d);
+  }, py::arg("device") = -1);
+  m.def("is_available", []() { return spyre::device_count() > 0; });
+  m.def("manual_seed", [](uint64_t seed, int device) { spyre::set_seed(device, seed); },
+        py::arg("seed"), py::arg("device") = -1);
+  m.def("manual_seed_all", [](uint64_t seed) { spyre::set_seed(-1, seed); });
+  m.def("initial_seed", [](int device) { return spyre::get_seed(device); },
+        py::arg("device") = -1);
+  m.def("_stream_handle", [](int device) {
+    return reinterpret_cast<uintptr_t>(spyre::stream(device));
+  }, py::arg("device") = -1, "hipStream_t (as an int) that spyre ops on `device` run on.");
+  m.def("memory_allocated", [](int d) { return spyre::memory_stats(d).allocated; },
+        py::arg("device") = -1);
+  m.def("memory_reserved", [](int d) { return spyre::memory_stats(d).reserved; },
+        py::arg("device") = -1);
+  m.def("max_memory_allocated", [](int d) { return spyre::memory_stats(d).peak_allocated; },
+        py::arg("device") = -1);
+  m.def("memory_stats", [](int d) {
+    auto s = spyre::memory_stats(d);
+    py::dict r;
+    r["allocated_bytes"] = s.allocated;
+    r["reserved_bytes"] = s.reserved;
+    r["peak_allocated_bytes"] = s.peak_allocated;
+    r["num_alloc_calls"] = s.num_alloc_calls;
+    r["num_device_mallocs"] = s.num_device_mallocs;
+    return r;
+  }, py::arg("device") = -1);
+  m.def("empty_cache", &spyre::empty_cache);
+  m.def("stick_alloc_nbytes", [](std::vector<int64_t> sizes, int64_t elem_bytes) {
+    return spyre::stick_alloc_nbytes(sizes, elem_bytes);
+  });
+  m.def("get_device_properties", [](int d) {
+    hipDeviceProp_t p{};
+    SPYRE_HIP_CHECK(hipGetDeviceProperties(&p, d < 0 ? spyre::current_device() : d));
+    py::dict r;
+    r["name"] = std::string(p.name);
+    r["gcnArchName"] = std::string(p.gcnArchName);
+    r["multi_processor_count"] = p.multiProcessorCount;
+    r["total_memory"] = static_cast<int64_t>(p.totalGlobalMem);
+    r["max_shared_memory_per_block"] = static_cast<int64_t>(p.sharedMemPerBlock);
+    r["clock_rate_khz"] = p.clockRate;
+    r["warp_size"] = p.warpSize;
+    return r;
+  }, py::arg("device") = -1);
+
+  using STL = spyre::SpyreTensorLayout;
+  py::class_<STL> cls(m, "SpyreTensorLayout");
+  py::enum_<STL::StickFormat>(cls, "StickFormat")
+      .value("Dense", STL::Dense)
+      .value("Sparse", STL::Sparse)
+      .value("SparseMulti", STL::SparseMulti);
+  cls.def_readwrite("device_size", &STL::device_size)
+      .def_readwrite("device_strides", &STL::device_strides)
+      .def_readwrite("dim_map", &STL::dim_map)
+      .def_readwrite("num_stick_dims", &STL::num_stick_dims)
+      .def_readwrite("format", &STL::format)
+      .def("__str__", [](const STL& l) { return l.toString(); })
+      .def("__repr__", [](const STL& l) { return l.toString(); })
+      .def(py::init<std::vector<int64_t>, c10::ScalarType>())
+      .def(py::init<std::vector<int64_t>, c10::ScalarType, std::vector<int32_t>,
+                    STL::StickFormat>(),
+           py::arg("host_size"), py::arg("dtype"), py::arg("dim_order"),
+           py::arg("format") = STL::Dense)
+      .def(py::init<std::vector<int64_t>, std::vector<int64_t>, std::vector<int32_t>, int32_t,
+                    STL::StickFormat>());
+}

@@ -1,0 +1,352 @@
+// HIP runtime state, HBM caching allocator and pinned host allocator of the
+// spyre backend.  See spyre_runtime.h.
+#include "spyre_runtime.h"
+
+#include <c10/core/CPUAllocator.h>
+#include <c10/core/DeviceType.h>
+#include <c10/util/Exception.h>
+
+#include <algorithm>
+#include <array>
+#include <atomic>
+#include <map>
+#include <mutex>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+namespace spyre {
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+std::once_flag g_start_once;
+std::atomic<bool> g_started{false};
+int g_device_count = 0;
+
+std::mutex g_stream_mu;
+std::array<hipStream_t, kMaxDevices> g_streams{};
+
+std::array<std::atomic<uint64_t>, kMaxDevices> g_seeds{};
+
+void do_start() {
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    n = 0;
+  }
+  g_device_count = std::min(n, kMaxDevices);
+  g_started = true;
+}
+
+}  // namespace
+
+void start_runtime() { std::call_once(g_start_once, do_start); }
+
+bool runtime_started() { return g_started.load(); }
+
+int device_count() {
+  start_runtime();
+  return g_device_count;
+}
+
+int current_device() {
+  int d = 0;
+  SPYRE_HIP_CHECK(hipGetDevice(&d));
+  return d;
+}
+
+void set_device(int device) {
+  TORCH_CHECK(device >= 0 && device < device_count(), "spyre: invalid device index ", device,
+              " (", device_count(), " device(s) visible)");
+  int cur = -1;
+  SPYRE_HIP_CHECK(hipGetDevice(&cur));
+  if (cur != device) SPYRE_HIP_CHECK(hipSetDevice(device));
+}
+
+hipStream_t stream(int device) {
+  if (device < 0) device = current_device();
+  TORCH_CHECK(device < device_count(), "spyre: invalid device index ", device);
+  hipStream_t s = g_streams[device];
+  if (s) return s;
+  std::lock_guard<std::mutex> lk(g_stream_mu);
+  if (!g_streams[device]) {
+    int cur = current_device();
+    if (cur != device) SPYRE_HIP_CHECK(hipSetDevice(device));
+    hipStream_t ns = nullptr;
+    SPYRE_HIP_CHECK(hipStreamCreateWithFlags(&ns, hipStreamNonBlocking));
+    g_streams[device] = ns;
+    if (cur != device) SPYRE_HIP_CHECK(hipSetDevice(cur));
+  }
+  return g_streams[device];
+}
+
+void synchronize(int device) {
+  if (device >= 0) {
+    if (g_streams[device]) SPYRE_HIP_CHECK(hipStreamSynchronize(g_streams[device]));
+    return;
+  }
+  for (int d = 0; d < device_count(); ++d)
+    if (g_streams[d]) SPYRE_HIP_CHECK(hipStreamSynchronize(g_streams[d]));
+}
+
+bool has_sph(at::ScalarType t) {
+  switch (t) {
+    case at::kHalf:
+    case at::kBFloat16:
+    case at::kFloat:
+    case at::kDouble:
+    case at::kChar:
+    case at::kByte:
+    case at::kShort:
+    case at::kInt:
+    case at::kLong:
+    case at::kBool:
+      return true;
+    default:
+      return false;
+  }
+}
+
+sph_dtype to_sph(at::ScalarType t) {
+  switch (t) {
+    case at::kHalf:
+      return SPH_F16;
+    case at::kBFloat16:
+      return SPH_BF16;
+    case at::kFloat:
+      return SPH_F32;
+    case at::kDouble:
+      return SPH_F64;
+    case at::kChar:
+      return SPH_I8;
+    case at::kByte:
+      return SPH_U8;
+    case at::kShort:
+      return SPH_I16;
+    case at::kInt:
+      return SPH_I32;
+    case at::kLong:
+      return SPH_I64;
+    case at::kBool:
+      return SPH_BOOL;
+    default:
+      TORCH_CHECK(false, "spyre: dtype ", t, " is not supported by the MI355X kernels");
+  }
+}
+
+int64_t stick_alloc_nbytes(c10::IntArrayRef sizes, int64_t elem_bytes) {
+  constexpr int64_t kStick = 128;
+  if (sizes.empty()) return kStick;
+  const int64_t per_stick = std::max<int64_t>(1, kStick / elem_bytes);
+  int64_t n = kStick * ((sizes.back() + per_stick - 1) / per_stick);
+  for (size_t i = 0; i + 1 < sizes.size(); ++i) n *= sizes[i];
+  return n;
+}
+
+void set_seed(int device, uint64_t seed) {
+  if (device < 0) {
+    for (auto& s : g_seeds) s = seed;
+  } else {
+    TORCH_CHECK(device < kMaxDevices, "spyre: invalid device index ", device);
+    g_seeds[device] = seed;
+  }
+}
+
+uint64_t get_seed(int device) { return g_seeds[device < 0 ? 0 : device].load(); }
+
+// ---------------------------------------------------------------------------
+// HBM caching allocator
+//
+// Blocks are rounded (512 B below 1 MiB, 2 MiB above) and cached per device
+// on free.  A freed block is handed out again only for work that is ordered
+// after its last use: every spyre kernel and copy of a device runs on that
+// device's single spyre stream, so stream order guarantees it.  On an
+// out-of-memory error the cache is released and hipMalloc retried.
+// ---------------------------------------------------------------------------
+namespace {
+
+struct Block {
+  void* ptr;
+  size_t size;
+  int device;
+};
+
+class CachingAllocator final : public c10::Allocator {
+ public:
+  at::DataPtr allocate(size_t nbytes) override {
+    start_runtime();
+    const int dev = current_device();
+    const c10::Device device(c10::DeviceType::PrivateUse1, static_cast<c10::DeviceIndex>(dev));
+    if (nbytes == 0) return {nullptr, nullptr, &noop_delete, device};
+    const size_t size = round_size(nbytes);
+    Block* b = nullptr;
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      auto& pool = free_[dev];
+      // Best fit, without handing a block more than twice the request.
+      auto it = pool.lower_bound(size);
+      if (it != pool.end() && it->first <= 2 * size) {
+        b = it->second;
+        pool.erase(it);
+      }
+      stats_[dev].num_alloc_calls++;
+    }
+    if (!b) b = fresh_block(dev, size);
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      auto& st = stats_[dev];
+      st.allocated += static_cast<int64_t>(b->size);
+      st.peak_allocated = std::max(st.peak_allocated, st.allocated);
+    }
+    return {b->ptr, b, &release, device};
+  }
+
+  at::DeleterFnPtr raw_deleter() const override { return nullptr; }
+
+  void copy_data(void* dest, const void* src, std::size_t count) const override {
+    if (count == 0) return;
+    hipStream_t s = stream(-1);
+    SPYRE_HIP_CHECK(hipMemcpyAsync(dest, src, count, hipMemcpyDeviceToDevice, s));
+  }
+
+  MemoryStats stats(int dev) {
+    std::lock_guard<std::mutex> lk(mu_);
+    return stats_[dev];
+  }
+
+  void empty_cache() {
+    synchronize(-1);
+    std::lock_guard<std::mutex> lk(mu_);
+    for (int d = 0; d < kMaxDevices; ++d) {
+      for (auto& kv : free_[d]) {
+        Block* b = kv.second;
+        (void)hipFree(b->ptr);
+        stats_[d].reserved -= static_cast<int64_t>(b->size);
+        delete b;
+      }
+      free_[d].clear();
+    }
+  }
+
+  static CachingAllocator& instance() {
+    static CachingAllocator* inst = new CachingAllocator();  // never destroyed
+    return *inst;
+  }
+
+ private:
+  static size_t round_size(size_t n) {
+    constexpr size_t kSmall = 512, kLarge = size_t(2) << 20, kSplit = size_t(1) << 20;
+    if (n < kSplit) return (n + kSmall - 1) / kSmall * kSmall;
+    return (n + kLarge - 1) / kLarge * kLarge;
+  }
+
+  Block* fresh_block(int dev, size_t size) {
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, size);
+    if (e == hipErrorOutOfMemory) {
+      (void)hipGetLastError();
+      empty_cache();
+      e = hipMalloc(&p, size);
+    }
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      MemoryStats st = stats(dev);
+      TORCH_CHECK(false, "spyre: out of device memory allocating ", size, " bytes on spyre:",
+                  dev, " (allocated ", st.allocated, ", reserved ", st.reserved, "): ",
+                  hipGetErrorString(e));
+    }
+    std::lock_guard<std::mutex> lk(mu_);
+    stats_[dev].reserved += static_cast<int64_t>(size);
+    stats_[dev].num_device_mallocs++;
+    return new Block{p, size, dev};
+  }
+
+  static void release(void* ctx) {
+    Block* b = static_cast<Block*>(ctx);
+    auto& self = instance();
+    std::lock_guard<std::mutex> lk(self.mu_);
+    self.stats_[b->device].allocated -= static_cast<int64_t>(b->size);
+    self.free_[b->device].emplace(b->size, b);
+  }
+
+  static void noop_delete(void*) {}
+
+  std::mutex mu_;
+  std::array<std::multimap<size_t, Block*>, kMaxDevices> free_;
+  std::array<MemoryStats, kMaxDevices> stats_{};
+};
+
+// Pinned host memory for copy staging (hipHostMalloc, never hipHostRegister).
+class PinnedAllocator final : public c10::Allocator {
+ public:
+  at::DataPtr allocate(size_t nbytes) override {
+    const c10::Device cpu(c10::DeviceType::CPU);
+    if (nbytes == 0) return {nullptr, nullptr, &free_pinned, cpu};
+    void* p = nullptr;
+    SPYRE_HIP_CHECK(hipHostMalloc(&p, nbytes, hipHostMallocDefault));
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      live_.insert(p);
+    }
+    return {p, p, &free_pinned, cpu};
+  }
+  at::DeleterFnPtr raw_deleter() const override { return &free_pinned; }
+  void copy_data(void* dest, const void* src, std::size_t count) const override {
+    std::memcpy(dest, src, count);
+  }
+  bool owns(const void* p) {
+    std::lock_guard<std::mutex> lk(mu_);
+    return live_.count(const_cast<void*>(p)) != 0;
+  }
+  static PinnedAllocator& instance() {
+    static PinnedAllocator* inst = new PinnedAllocator();
+    return *inst;
+  }
+
+ private:
+  static void free_pinned(void* p) {
+    if (!p) return;
+    {
+      auto& self = instance();
+      std::lock_guard<std::mutex> lk(self.mu_);
+      self.live_.erase(p);
+    }
+    (void)hipHostFree(p);
+  }
+  std::mutex mu_;
+  std::unordered_set<void*> live_;
+};
+
+}  // namespace
+
+c10::Allocator* device_allocator() { return &CachingAllocator::instance(); }
+c10::Allocator* pinned_allocator() { return &PinnedAllocator::instance(); }
+bool is_pinned_ptr(const void* p) { return PinnedAllocator::instance().owns(p); }
+
+MemoryStats memory_stats(int device) {
+  if (device < 0) device = current_device();
+  return CachingAllocator::instance().stats(device);
+}
+
+void empty_cache() { CachingAllocator::instance().empty_cache(); }
+
+void free_runtime() {
+  if (!runtime_started()) return;
+  empty_cache();
+  std::lock_guard<std::mutex> lk(g_stream_mu);
+  for (int d = 0; d < kMaxDevices; ++d) {
+    if (g_streams[d]) {
+      (void)hipStreamDestroy(g_streams[d]);
+      g_streams[d] = nullptr;
+    }
+  }
+}
+
+}  // namespace spyre
+
+// Registered for the PrivateUse1 device type when the extension loads
+// (reference: REGISTER_ALLOCATOR, torch_spyre/csrc/spyre_mem.cpp:554).
+REGISTER_ALLOCATOR(c10::DeviceType::PrivateUse1, &spyre::CachingAllocator::instance());

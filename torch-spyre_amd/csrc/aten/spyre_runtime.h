@@ -1,0 +1,83 @@
+// Device runtime of the "spyre" PrivateUse1 backend on MI355X: HIP device
+// selection, the per-device stream every spyre op is ordered on, the HBM
+// caching allocator, and the mapping from torch dtypes to the kernel
+// library's element types.
+//
+// Reference counterparts (torch-spyre tree): _startRuntime / GlobalRuntime
+// (torch_spyre/csrc/module.cpp:40-59, module.h:27-53), SpyreAllocator
+// (torch_spyre/csrc/spyre_mem.cpp:486-554) and the guard's device/stream
+// state (torch_spyre/csrc/spyre_hooks.cpp:54-256).
+#pragma once
+
+#include <ATen/ATen.h>
+#include <c10/core/Allocator.h>
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <string>
+
+#include "spyre_hip.h"
+
+namespace spyre {
+
+#define SPYRE_HIP_CHECK(expr)                                                   \
+  do {                                                                          \
+    hipError_t err_ = (expr);                                                   \
+    TORCH_CHECK(err_ == hipSuccess, "spyre: HIP error ", static_cast<int>(err_), \
+                " (", hipGetErrorString(err_), ") in ", #expr);                 \
+  } while (0)
+
+// Non-zero status of a C-ABI entry point -> RuntimeError with its message.
+#define SPYRE_SPH_CHECK(expr)                                                   \
+  do {                                                                          \
+    int rc_ = (expr);                                                           \
+    TORCH_CHECK(rc_ == 0, "spyre: ", #expr, " failed (status ", rc_, "): ",     \
+                sph_last_error());                                              \
+  } while (0)
+
+// Runtime start (idempotent, thread-safe): probes the HIP devices.
+void start_runtime();
+// Releases cached device memory and the per-device streams.
+void free_runtime();
+bool runtime_started();
+
+int device_count();
+int current_device();
+void set_device(int device);
+
+// The stream all spyre work on `device` is ordered on (-1: current device).
+// Created on first use with default priority.
+hipStream_t stream(int device = -1);
+// Blocks until all spyre work on `device` (-1: every device) has finished.
+void synchronize(int device = -1);
+
+// Kernel-library element type of a torch dtype; throws for unsupported ones.
+sph_dtype to_sph(at::ScalarType t);
+bool has_sph(at::ScalarType t);
+
+// The HBM caching allocator registered for PrivateUse1.
+c10::Allocator* device_allocator();
+// Pinned host memory (hipHostMalloc) for staging copies.
+c10::Allocator* pinned_allocator();
+bool is_pinned_ptr(const void* p);
+
+struct MemoryStats {
+  int64_t allocated = 0;      // bytes in live blocks
+  int64_t reserved = 0;       // bytes obtained from hipMalloc and not freed
+  int64_t peak_allocated = 0;
+  int64_t num_alloc_calls = 0;
+  int64_t num_device_mallocs = 0;
+};
+MemoryStats memory_stats(int device);
+void empty_cache();
+
+// Bytes the reference's stick-granular sizing gives a tensor of `sizes`
+// (torch_spyre/csrc/spyre_mem.cpp:598-611, with the stick count rounded up):
+// 128 bytes per 128-byte stick of the last dim, times the other dims; 128
+// bytes for a 0-d tensor.
+int64_t stick_alloc_nbytes(c10::IntArrayRef sizes, int64_t elem_bytes);
+
+void set_seed(int device, uint64_t seed);
+uint64_t get_seed(int device);
+
+}  // namespace spyre

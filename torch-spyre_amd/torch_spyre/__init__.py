@@ -124,6 +124,13 @@ def make_spyre_module() -> types.ModuleType:
     mod.set_device = impl.set_device
     mod.synchronize = impl.synchronize
     mod.is_initialized = impl.is_initialized
+    mod.memory_allocated = lambda device=None: impl._C.memory_allocated(
+        -1 if device is None else int(getattr(device, "index", device) or 0))
+    mod.memory_reserved = lambda device=None: impl._C.memory_reserved(
+        -1 if device is None else int(getattr(device, "index", device) or 0))
+    mod.max_memory_allocated = lambda device=None: impl._C.max_memory_allocated(
+        -1 if device is None else int(getattr(device, "index", device) or 0))
+    mod.empty_cache = lambda: impl._C.empty_cache()
     mod._lazy_init = impl._lazy_init
     mod._is_compiled = lambda: True
 
@@ -158,3 +165,9 @@ def _autoload():
     from torch_spyre._inductor import _autoload as ts_autoload
 
     ts_autoload()
+
+
+# Installed packages are registered by torch itself through the
+# `torch.backends` entry point at `import torch`; importing the package (the
+# in-tree case, with no entry point) registers it as well.
+_autoload()
