@@ -172,6 +172,48 @@ def bench_extra(steps, warmup, stream, capi):
     return out
 
 
+def bench_copy(steps, warmup, stream, capi):
+    """Plain device copy of a known size (512 MiB read + 512 MiB written):
+    the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    n = 256 * 1024 * 1024  # fp16 elements = 512 MiB
+    src = torch.empty(n, dtype=torch.float16, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    ops = (capi.Operand * 2)(capi.operand(dst.data_ptr(), capi.F16, [1]),
+                             capi.operand(src.data_ptr(), capi.F16, [1]))
+    sizes = capi.i64_array([n])
+    lib = capi.lib()
+    s = stream.cuda_stream
+
+    def step():
+        capi.check(lib.sph_pointwise(0, 1, ops, 1, sizes, 0.0, 0.0, s), "sph_pointwise copy")
+
+    ms, _ = Timer(stream).run(step, steps, warmup)
+    return {"us_per_launch": round(ms * 1e3, 2), "bytes": 2 * n * 2,
+            "GB/s": round(2 * n * 2 / (ms * 1e-3) / 1e9, 1)}
+
+
+def bench_eager_mm(steps, warmup):
+    """torch.mm on "spyre" tensors: the drop-in (PrivateUse1) path to the same
+    kernel, timed on the spyre stream."""
+    import torch
+
+    import torch_spyre  # noqa: F401
+
+    a = (torch.rand(4096, 4096, generator=_gen(0)) * 2 - 1).half().to("spyre")
+    b = (torch.rand(4096, 4096, generator=_gen(1)) * 2 - 1).half().to("spyre")
+    for _ in range(warmup):
+        torch.mm(a, b)
+    torch.spyre.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        torch.mm(a, b)
+    torch.spyre.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    return {"ms_per_call": round(ms, 4), "TFLOP/s": round(2 * 4096 ** 3 / (ms * 1e-3) / 1e12, 1)}
+
+
 def cpu_baseline_gemm(a, b):
     """Oracle GEMM (numpy fp32) on a bounded row slice of the same problem,
     timed on this host's cores."""
@@ -194,7 +236,7 @@ def cpu_baseline_gemm(a, b):
         O.gemm(an, bn)
         reps += 1
         el = time.perf_counter() - t0
-        if el > 5.0 or reps >= 20:
+        if el > 10.0:
             break
     flop = 2.0 * rows * b.shape[0] * b.shape[1] * reps
     return {"value": round(flop / el / 1e12, 4), "unit": "TFLOP/s", "cores": int(cores),
@@ -210,6 +252,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel", choices=["all", "gemm", "copy"], default="all",
+                    help="gemm / copy: run only that kernel (for rocprofv3 counter passes)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; runs on more than one GPU are not "
@@ -224,12 +268,19 @@ def main(argv=None):
     from torch_spyre import _capi
 
     stream = torch.cuda.current_stream()
+    if args.kernel == "copy":
+        print(json.dumps({"kernel": "copy", **bench_copy(args.steps, args.warmup, stream, _capi)}))
+        return 0
+    if args.kernel == "gemm":
+        args.no_extra = args.no_cpu = True
     _log("gemm 4096^3")
     g = bench_gemm(args.steps, args.warmup, stream, _capi)
     extra = {}
     if not args.no_extra:
         _log("extra kernels")
         extra = bench_extra(max(10, args.steps), args.warmup, stream, _capi)
+        _log("eager torch.mm on spyre tensors")
+        extra["c2_mm_4096_spyre_device_eager"] = bench_eager_mm(max(10, args.steps), args.warmup)
     cpu = None
     if not args.no_cpu:
         _log("cpu baseline")
