@@ -1,0 +1,112 @@
+"""The spyre torch.compile backend on the CPU host: Inductor lowers graphs
+over fake spyre tensors, SpyreKernel generates HIP for the fused groups,
+hiprtc compiles them for gfx950 and the code objects are registered with
+torch_spyre._C.  Nothing is launched (no GPU here); the GPU parity of the
+same kernels is in test_compile_gpu.py.
+
+Checks the structure the backend promises: one kernel per fused row
+reduction (softmax = max, sum and normalise phases in one kernel; LayerNorm
+= Welford + normalise; GELU chain + row-sum), matrix products as extern
+calls to the MFMA GEMM, per-argument extents for the launch-time bounds
+check, and the fusions the reference forbids (choices.py:58-83).
+"""
+
+import re
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import torch_spyre  # noqa: F401
+from torch_spyre.utils import device_interface as di
+
+
+@pytest.fixture
+def fake_device(monkeypatch):
+    # No GPU on this host: fake tensors need a device index and Inductor's
+    # heuristics need the device's properties (MI355X values).
+    monkeypatch.setattr(torch.spyre, "current_device", lambda: 0)
+    monkeypatch.setattr(di.SpyreInterface.Worker, "get_device_properties", staticmethod(
+        lambda device=None: di.SpyreDeviceProperties("spyre", 0, "AMD Instinct MI355X",
+                                                     "gfx950", 256, 288 << 30, 64)))
+    yield
+
+
+def _compile(fn, specs):
+    from torch._inductor import config
+    from torch._inductor.compile_fx import compile_fx
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    n = len(specs)
+    names = ", ".join(f"a{i}" for i in range(n))
+    ns = {}
+    exec(f"def forward(self, {names}):\n    return self.fn({names})\n", ns)
+    mod = type("M", (torch.nn.Module,), {"forward": ns["forward"]})()
+    mod.fn = fn
+    gm = torch.fx.symbolic_trace(mod)
+    with FakeTensorMode():
+        args = [torch.empty(s, dtype=d, device="spyre") for s, d in specs]
+    codes = []
+    from torch._inductor.graph import GraphLowering
+
+    orig = GraphLowering.compile_to_module
+
+    def capture(self):
+        mod = orig(self)
+        with open(mod.__file__) as f:
+            codes.append(f.read())
+        return mod
+
+    GraphLowering.compile_to_module = capture
+    try:
+        with config.patch({"fx_graph_cache": False}):
+            compile_fx(gm, args)
+    finally:
+        GraphLowering.compile_to_module = orig
+    return "\n".join(codes)
+
+
+def _kernels(code):
+    return re.findall(r"async_compile\.hip\('([^']+)'", code)
+
+
+def test_softmax_is_one_three_phase_kernel(fake_device):
+    code = _compile(lambda x: torch.softmax(x, -1), [((512, 4096), torch.float16)])
+    ks = _kernels(code)
+    assert len(ks) == 1, ks
+    assert code.count("block_reduce<spy::MaxF") == 1 and code.count("block_reduce<spy::SumF") == 1
+    assert code.count("for (int64_t r0_cnt") == 3
+    assert "extent=2097152" in code  # 512*4096 elements bound both arguments
+
+
+def test_layernorm_gelu_rmsnorm_fuse(fake_device):
+    code = _compile(lambda x, w, b: F.layer_norm(x, [4096], w, b, 1e-5),
+                    [((64, 4096), torch.float16), ((4096,), torch.float16), ((4096,), torch.float16)])
+    assert len(_kernels(code)) == 1 and "block_welford" in code
+    code = _compile(lambda x, s, b: (lambda y: (y, y.sum(-1)))(F.gelu(x * s + b)),
+                    [((64, 4096), torch.float16), ((4096,), torch.float16), ((4096,), torch.float16)])
+    assert len(_kernels(code)) == 1 and "erff" in code
+    code = _compile(lambda x, r, w: (lambda h: (h, torch.rms_norm(h, [4096], w, 1e-5)))(x + r),
+                    [((64, 4096), torch.float16), ((64, 4096), torch.float16), ((4096,), torch.float16)])
+    assert len(_kernels(code)) == 1
+
+
+def test_matmul_is_extern_mfma_call(fake_device):
+    code = _compile(lambda a, b: a @ b, [((256, 512), torch.float16), ((512, 384), torch.float16)])
+    assert "extern_kernels.mm(" in code and not _kernels(code)
+    code = _compile(lambda a, b: torch.softmax(torch.bmm(a, b), -1),
+                    [((4, 64, 32), torch.float16), ((4, 32, 64), torch.float16)])
+    assert "extern_kernels.bmm(" in code and len(_kernels(code)) == 1
+
+
+def test_pointwise_chain_fuses_into_one_kernel(fake_device):
+    code = _compile(lambda x, y: torch.sigmoid(x * 2 + y).relu() - 1,
+                    [((1000, 3), torch.float32), ((1000, 3), torch.float32)])
+    assert len(_kernels(code)) == 1
+    assert "if (xindex >= 3000LL) return;" in code
+
+
+def test_unsupported_dynamic_shapes_raise(fake_device):
+    from torch_spyre._inductor import Unsupported
+
+    assert issubclass(Unsupported, RuntimeError)

@@ -1,0 +1,121 @@
+"""torch.compile on "spyre" tensors (MI355X): the generated, hiprtc-compiled
+HIP kernels and the extern MFMA GEMM calls, checked against the numpy oracle
+and torch's CPU ops at rtol = atol = 1e-2 (fp16 outputs).
+
+The reference's compiled-path tests (tests/_inductor/test_building_blocks.py
+:33-89, test_inductor_ops.py) compare torch.compile on its device with the
+CPU; the cases here are the BASELINE configs' compiled flows: c1 softmax,
+c2 matmul / bmm, c3 norms and the GELU chain with a row-sum, plus the
+reference's building blocks (softplus, single-head attention).
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import torch_spyre  # noqa: F401
+
+from oracle import ops as O
+
+from helpers import assert_close_fp, randn, uniform
+
+pytestmark = pytest.mark.gpu
+
+DEV = "spyre"
+TOL = dict(rtol=1e-2, atol=1e-2)
+
+
+def _log(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+@pytest.fixture(autouse=True)
+def _fresh_dynamo():
+    torch._dynamo.reset()
+    yield
+
+
+def test_c1_softmax_compiled_vs_oracle():
+    _log("compiled softmax [512,4096]")
+    x = randn((512, 4096), k=0, scale=4.0)
+    f = torch.compile(lambda a: torch.softmax(a, dim=-1))
+    y = f(x.to(DEV))
+    assert_close_fp(y, O.softmax(x.numpy()), what="compiled softmax")
+    # same result as the eager spyre kernel, and repeatable
+    torch.testing.assert_close(f(x.to(DEV)).cpu(), y.cpu(), rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("dim", [0, 1, -1])
+def test_building_block_softmax_dims(dim):
+    # reference tests/_inductor/test_building_blocks.py:33-36
+    _log(f"compiled softmax [512,1024] dim={dim}")
+    x = randn((512, 1024), k=1)
+    y = torch.compile(lambda a: torch.softmax(a, dim=dim))(x.to(DEV))
+    torch.testing.assert_close(y.cpu(), torch.softmax(x.float(), dim=dim).half(), **TOL)
+
+
+def test_c3_norms_and_gelu_chain_compiled_vs_oracle():
+    _log("compiled c3 at [512,4096]")
+    R, C = 512, 4096
+    x, r = randn((R, C), k=0), randn((R, C), k=1)
+    w = randn((C,), k=2, scale=0.02, mean=1.0)
+    b = randn((C,), k=3, scale=0.02)
+    xd, rd, wd, bd = (t.to(DEV) for t in (x, r, w, b))
+
+    h, y = torch.compile(lambda a, c, g: (lambda s: (s, torch.rms_norm(s, [C], g, 1e-5)))(a + c))(
+        xd, rd, wd)
+    ey, eh = O.rmsnorm(x.numpy(), w.numpy(), 1e-5, residual=r.numpy())[:2]
+    assert_close_fp(h, eh, what="compiled residual add")
+    assert_close_fp(y, ey, what="compiled add+rmsnorm")
+
+    h2, y2 = torch.compile(
+        lambda a, c, g, e: (lambda s: (s, F.layer_norm(s, [C], g, e, 1e-5)))(a + c))(xd, rd, wd, bd)
+    ly, lh = O.layernorm(x.numpy(), w.numpy(), b.numpy(), 1e-5, residual=r.numpy())[:2]
+    assert_close_fp(h2, lh, what="compiled residual add (LN)")
+    assert_close_fp(y2, ly, what="compiled add+layernorm")
+
+    g, rs = torch.compile(lambda a, s, c: (lambda t: (t, t.sum(-1)))(F.gelu(a * s + c)))(xd, wd, bd)
+    eg, ers = O.gelu_affine_rowsum(x.numpy(), w.numpy(), b.numpy())
+    assert_close_fp(g, eg, what="compiled gelu chain")
+    # a row-sum of 4096 fp16 values: fp16 output rounding is ~0.1 at |sum|~300
+    np.testing.assert_allclose(rs.cpu().float().numpy(), ers, rtol=2e-2, atol=0.5)
+
+
+def test_c2_matmul_and_bmm_compiled():
+    _log("compiled mm / bmm")
+    A, B = uniform((1024, 2048), k=0), uniform((2048, 512), k=1)
+    C = torch.compile(lambda a, b: a @ b)(A.to(DEV), B.to(DEV))
+    assert_close_fp(C, O.gemm(A.numpy(), B.numpy()), what="compiled mm")
+    Q, K = uniform((8, 256, 128), k=2), uniform((8, 128, 256), k=3)
+    S = torch.compile(lambda q, k: torch.softmax(torch.bmm(q, k) * 0.088, dim=-1))(
+        Q.to(DEV), K.to(DEV))
+    ref = torch.softmax(torch.bmm(Q.float(), K.float()).half().float() * 0.088, -1).half()
+    torch.testing.assert_close(S.cpu(), ref, **TOL)
+
+
+def test_building_block_softplus_and_attention():
+    # reference tests/_inductor/test_building_blocks.py:38-89
+    _log("compiled softplus / single-head attention")
+    x = randn((512, 1024), k=4)
+    sp = torch.compile(lambda a: F.softplus(a))(x.to(DEV))
+    torch.testing.assert_close(sp.cpu(), F.softplus(x.float()).half(), **TOL)
+    q, k, v = randn((256, 128), k=5), randn((256, 128), k=6), randn((256, 128), k=7)
+
+    def attn(q, k, v):
+        s = q @ k.transpose(-2, -1) * (1.0 / 128 ** 0.5)
+        return torch.softmax(s, dim=-1) @ v
+
+    o = torch.compile(attn)(q.to(DEV), k.to(DEV), v.to(DEV))
+    ref = attn(q.float(), k.float(), v.float()).half()
+    torch.testing.assert_close(o.cpu(), ref, rtol=2e-2, atol=2e-2)
+
+
+def test_pointwise_chain_and_broadcast_compiled():
+    _log("compiled pointwise chain")
+    x = randn((333, 77), k=8, dtype=torch.float32)
+    y = randn((77,), k=9, dtype=torch.float32)
+    f = torch.compile(lambda a, b: (torch.sigmoid(a * 2 + b).relu() - 1) * torch.tanh(a))
+    torch.testing.assert_close(f(x.to(DEV), y.to(DEV)).cpu(),
+                               (torch.sigmoid(x * 2 + y).relu() - 1) * torch.tanh(x),
+                               rtol=1e-5, atol=1e-5)

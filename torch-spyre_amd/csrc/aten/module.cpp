@@ -16,8 +16,10 @@
 namespace py = pybind11;
 
 namespace spyre {
-// Compiled-kernel launcher (ops_launch.cpp).
-void launch_kernel(const std::string& spec, const std::vector<at::Tensor>& args);
+// Compiled-kernel loader / launcher (ops_launch.cpp).
+int64_t load_kernel(const std::string& code_object, const std::string& name);
+void launch_kernel(int64_t handle, const std::vector<at::Tensor>& args, int64_t grid,
+                   int64_t block, const std::vector<int64_t>& extents);
 }  // namespace spyre
 
 PYBIND11_MODULE(_C, m) {
@@ -26,8 +28,14 @@ PYBIND11_MODULE(_C, m) {
   m.def("start_runtime", &spyre::start_runtime, "Probes the HIP devices (idempotent).");
   m.def("free_runtime", &spyre::free_runtime,
         "Releases cached device memory and the spyre streams.");
-  m.def("launch_kernel", &spyre::launch_kernel, py::arg("spec"), py::arg("args"),
-        "Runs a compiled kernel spec on tensors (the last argument is the output).");
+  m.def("load_kernel", [](py::bytes code, const std::string& name) {
+    return spyre::load_kernel(std::string(code), name);
+  }, py::arg("code_object"), py::arg("name"),
+        "Registers a gfx950 code object (loaded into each device on first launch).");
+  m.def("launch_kernel", &spyre::launch_kernel, py::arg("handle"), py::arg("args"),
+        py::arg("grid"), py::arg("block"), py::arg("extents"),
+        "Launches a loaded kernel on the spyre stream of the arguments' device; "
+        "extents[i] >= 0 bounds the elements argument i may address.");
 
   m.def("device_count", []() { return spyre::device_count(); });
   m.def("current_device", []() { return spyre::current_device(); });

@@ -1,0 +1,256 @@
+// Device runtime of the kernels the spyre Inductor backend generates
+// (compiled with hiprtc for gfx950 at torch.compile time).
+//
+// Generated kernels are one of two hand-written templates, instantiated with
+// the fused loop body Inductor produced:
+//   * pointwise: one thread per output element, 1-D grid over xnumel;
+//   * row reduction: one workgroup per output row; the threads stride over
+//     the reduction index (coalesced), accumulate in fp32, and combine with
+//     the wave64 / LDS block reductions below.  Several reductions of the
+//     same row run in sequence inside one kernel (softmax, norms).
+// All arithmetic is fp32 (fp16 / bf16 values are widened on load and
+// rounded once on store), like torch's CPU kernels.
+#pragma once
+
+typedef long long int64_t;
+typedef int int32_t;
+typedef unsigned int uint32_t;
+typedef unsigned short uint16_t;
+typedef signed char int8_t;
+typedef unsigned char uint8_t;
+
+struct bfloat16 {
+  uint16_t bits;
+};
+
+namespace spy {
+
+constexpr int kWave = 64;
+
+// ---- conversions ----------------------------------------------------------
+__device__ inline float to_f(float v) { return v; }
+__device__ inline float to_f(_Float16 v) { return static_cast<float>(v); }
+__device__ inline float to_f(double v) { return static_cast<float>(v); }
+__device__ inline float to_f(bfloat16 v) { return __uint_as_float(static_cast<uint32_t>(v.bits) << 16); }
+__device__ inline float to_f(bool v) { return v ? 1.f : 0.f; }
+__device__ inline float to_f(int8_t v) { return static_cast<float>(v); }
+__device__ inline float to_f(uint8_t v) { return static_cast<float>(v); }
+__device__ inline float to_f(int32_t v) { return static_cast<float>(v); }
+__device__ inline float to_f(int64_t v) { return static_cast<float>(v); }
+
+// Store-side conversion of a computed value (fp32, bool or integer) to the
+// buffer's dtype: floats round to nearest even, integers truncate toward
+// zero, bool tests != 0 -- torch's cast semantics.
+template <typename T>
+struct Cvt {
+  template <typename V>
+  __device__ static inline T from(V v) { return static_cast<T>(v); }
+};
+template <>
+struct Cvt<_Float16> {
+  template <typename V>
+  __device__ static inline _Float16 from(V v) { return static_cast<_Float16>(static_cast<float>(v)); }
+};
+template <>
+struct Cvt<bfloat16> {
+  template <typename V>
+  __device__ static inline bfloat16 from(V v) {
+    uint32_t u = __float_as_uint(static_cast<float>(v));
+    bfloat16 r;
+    if ((u & 0x7fffffffu) > 0x7f800000u) {  // NaN stays quiet
+      r.bits = static_cast<uint16_t>((u >> 16) | 0x40u);
+      return r;
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    r.bits = static_cast<uint16_t>(u >> 16);
+    return r;
+  }
+};
+template <>
+struct Cvt<bool> {
+  template <typename V>
+  __device__ static inline bool from(V v) { return v != 0; }
+};
+
+template <typename T, typename V>
+__device__ inline T cvt(V v) {
+  return Cvt<T>::from(v);
+}
+
+// Rounds an fp32 value to the precision of a narrower dtype (to_dtype).
+__device__ inline float round_half(float v) { return static_cast<float>(static_cast<_Float16>(v)); }
+__device__ inline float round_bf16(float v) { return to_f(Cvt<bfloat16>::from(v)); }
+
+// ---- math -----------------------------------------------------------------
+__device__ inline float inf() { return __builtin_inff(); }
+__device__ inline float where(float c, float a, float b) { return c != 0.f ? a : b; }
+__device__ inline float maximum(float a, float b) {
+  return (a != a || b != b) ? __builtin_nanf("") : (a > b ? a : b);
+}
+__device__ inline float minimum(float a, float b) {
+  return (a != a || b != b) ? __builtin_nanf("") : (a < b ? a : b);
+}
+__device__ inline float relu(float x) { return x > 0.f ? x : 0.f; }
+__device__ inline float sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
+__device__ inline float rsqrt(float x) { return 1.f / sqrtf(x); }
+__device__ inline float sign(float x) { return static_cast<float>((x > 0.f) - (x < 0.f)); }
+__device__ inline float floordiv(float a, float b) { return floorf(a / b); }
+__device__ inline float truncdiv(float a, float b) { return truncf(a / b); }
+__device__ inline float remainder(float a, float b) {
+  float r = fmodf(a, b);
+  return (r != 0.f && ((r < 0.f) != (b < 0.f))) ? r + b : r;
+}
+__device__ inline float isnan_(float x) { return x != x ? 1.f : 0.f; }
+__device__ inline float isinf_(float x) { return (x == inf() || x == -inf()) ? 1.f : 0.f; }
+__device__ inline float round_even(float x) { return rintf(x); }
+
+// Integer index helpers used by printed index expressions.
+__device__ inline int64_t floordiv_i(int64_t a, int64_t b) {
+  int64_t q = a / b;
+  return (a % b != 0 && ((a < 0) != (b < 0))) ? q - 1 : q;
+}
+__device__ inline int64_t mod_i(int64_t a, int64_t b) {
+  int64_t r = a % b;
+  return (r != 0 && ((r < 0) != (b < 0))) ? r + b : r;
+}
+__device__ inline int64_t min_i(int64_t a, int64_t b) { return a < b ? a : b; }
+__device__ inline int64_t max_i(int64_t a, int64_t b) { return a > b ? a : b; }
+
+// ---- block reductions (wave64 butterflies + one LDS exchange) -------------
+struct SumF {
+  __device__ static inline float id() { return 0.f; }
+  __device__ static inline float op(float a, float b) { return a + b; }
+};
+struct ProdF {
+  __device__ static inline float id() { return 1.f; }
+  __device__ static inline float op(float a, float b) { return a * b; }
+};
+struct MaxF {
+  __device__ static inline float id() { return -inf(); }
+  __device__ static inline float op(float a, float b) { return maximum(a, b); }
+};
+struct MinF {
+  __device__ static inline float id() { return inf(); }
+  __device__ static inline float op(float a, float b) { return minimum(a, b); }
+};
+struct AnyF {
+  __device__ static inline float id() { return 0.f; }
+  __device__ static inline float op(float a, float b) { return (a != 0.f || b != 0.f) ? 1.f : 0.f; }
+};
+
+// Reduction over the BLOCK threads of the workgroup; every thread gets the
+// result.  `lds` holds BLOCK/64 floats; two barriers, so every thread of the
+// workgroup must call it.
+template <typename Op, int BLOCK>
+__device__ inline float block_reduce(float v, float* lds) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = Op::op(v, __shfl_xor(v, off, kWave));
+  if constexpr (BLOCK <= kWave) {
+    return v;
+  } else {
+    const int w = threadIdx.x / kWave;
+    if ((threadIdx.x % kWave) == 0) lds[w] = v;
+    __syncthreads();
+    float r = lds[0];
+#pragma unroll
+    for (int i = 1; i < BLOCK / kWave; ++i) r = Op::op(r, lds[i]);
+    __syncthreads();
+    return r;
+  }
+}
+
+// (value, index) pairs for argmax / argmin; ties go to the lowest index and
+// NaN wins, as in torch.
+template <bool MAX>
+__device__ inline void arg_combine(float& v, int64_t& i, float v2, int64_t i2) {
+  const bool nan1 = v != v, nan2 = v2 != v2;
+  bool take;
+  if (nan1 || nan2) {
+    take = nan2 && (!nan1 || i2 < i);
+  } else {
+    take = MAX ? (v2 > v || (v2 == v && i2 < i)) : (v2 < v || (v2 == v && i2 < i));
+  }
+  if (take) {
+    v = v2;
+    i = i2;
+  }
+}
+
+template <bool MAX, int BLOCK>
+__device__ inline int64_t block_arg(float v, int64_t i, float* lds_v, int64_t* lds_i) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    float v2 = __shfl_xor(v, off, kWave);
+    int64_t i2 = __shfl_xor(i, off, kWave);
+    arg_combine<MAX>(v, i, v2, i2);
+  }
+  if constexpr (BLOCK > kWave) {
+    const int w = threadIdx.x / kWave;
+    if ((threadIdx.x % kWave) == 0) {
+      lds_v[w] = v;
+      lds_i[w] = i;
+    }
+    __syncthreads();
+    v = lds_v[0];
+    i = lds_i[0];
+#pragma unroll
+    for (int k = 1; k < BLOCK / kWave; ++k) arg_combine<MAX>(v, i, lds_v[k], lds_i[k]);
+    __syncthreads();
+  }
+  return i;
+}
+
+// Welford state (mean, m2, weight) and its combine (Chan et al. parallel
+// variance update).
+struct Welford {
+  float mean, m2, weight;
+};
+__device__ inline Welford welford_combine(Welford a, Welford b) {
+  if (b.weight == 0.f) return a;
+  if (a.weight == 0.f) return b;
+  const float w = a.weight + b.weight;
+  const float delta = b.mean - a.mean;
+  const float nb = b.weight / w;
+  Welford r;
+  r.mean = a.mean + delta * nb;
+  r.m2 = a.m2 + b.m2 + delta * delta * a.weight * nb;
+  r.weight = w;
+  return r;
+}
+__device__ inline Welford welford_add(Welford a, float x) {
+  Welford b;
+  b.mean = x;
+  b.m2 = 0.f;
+  b.weight = 1.f;
+  return welford_combine(a, b);
+}
+
+template <int BLOCK>
+__device__ inline Welford block_welford(Welford s, float* lds) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    Welford o;
+    o.mean = __shfl_xor(s.mean, off, kWave);
+    o.m2 = __shfl_xor(s.m2, off, kWave);
+    o.weight = __shfl_xor(s.weight, off, kWave);
+    s = welford_combine(s, o);
+  }
+  if constexpr (BLOCK > kWave) {
+    constexpr int NW = BLOCK / kWave;
+    const int w = threadIdx.x / kWave;
+    if ((threadIdx.x % kWave) == 0) {
+      lds[w] = s.mean;
+      lds[NW + w] = s.m2;
+      lds[2 * NW + w] = s.weight;
+    }
+    __syncthreads();
+    Welford r{lds[0], lds[NW], lds[2 * NW]};
+#pragma unroll
+    for (int k = 1; k < NW; ++k) r = welford_combine(r, Welford{lds[k], lds[NW + k], lds[2 * NW + k]});
+    __syncthreads();
+    s = r;
+  }
+  return s;
+}
+
+}  // namespace spy

@@ -1,0 +1,692 @@
+"""SpyreKernel: Inductor loop IR -> HIP source for gfx950.
+
+Reference: SpyreKernel (torch_spyre/_inductor/spyre_kernel.py:85-369), which
+records exactly ONE op per kernel (`record_compute_op` raises on a second,
+:107-114) and summarises it as a KernelSpec for the Spyre SuperDSC emitter.
+Here a kernel is a whole fused Inductor node group: every load, pointwise
+op, reduction and store of the group is emitted as HIP C++ into one of two
+hand-written templates (include/spyre_inductor_rt.h):
+
+  pointwise  one thread per element of the flattened x range;
+  reduction  one workgroup per x row; each reduction phase is a strided loop
+             over the row (coalesced, fp32 accumulators) closed by a block
+             reduction, and phases that depend on earlier reductions (softmax,
+             norms) follow in the same kernel.
+
+The kernel is compiled by hiprtc at compile time (runtime/async_compile.py)
+and launched by torch_spyre._C.launch_kernel.  Static shapes only: dynamic
+sizes raise Unsupported.
+"""
+
+from __future__ import annotations
+
+import itertools
+import math
+from typing import Any, Optional, Union
+
+import sympy
+import torch
+from sympy.printing.precedence import PRECEDENCE
+
+from torch._inductor.codegen.common import (
+    CSEVariable,
+    DeferredLine,
+    IndentedBuffer,
+    OpOverrides,
+)
+from torch._inductor.codegen.simd import IterationRangesEntry, SIMDKernel
+from torch._inductor.utils import get_bounds_index_expr
+from torch._inductor.virtualized import OpsWrapper, V, ops
+from torch.utils._sympy.printers import ExprPrinter
+from torch.utils._sympy.value_ranges import ValueRanges, bound_sympy
+
+from . import Unsupported
+
+DTYPE_TO_HIP = {
+    torch.float32: "float",
+    torch.float64: "double",
+    torch.float16: "_Float16",
+    torch.bfloat16: "bfloat16",
+    torch.bool: "bool",
+    torch.int8: "int8_t",
+    torch.uint8: "uint8_t",
+    torch.int32: "int32_t",
+    torch.int64: "int64_t",
+}
+
+# Values of these dtypes are widened to fp32 on load.
+_FLOAT_LOAD = {torch.float16, torch.bfloat16, torch.float32, torch.float64}
+
+MAX_BLOCK = 512
+
+
+def _next_pow2(n: int) -> int:
+    return 1 << max(0, (int(n) - 1).bit_length())
+
+
+def hip_value(val: Any) -> str:
+    if isinstance(val, bool):
+        return "true" if val else "false"
+    if isinstance(val, float):
+        if val == math.inf:
+            return "spy::inf()"
+        if val == -math.inf:
+            return "(-spy::inf())"
+        if val != val:
+            return '__builtin_nanf("")'
+        return f"{val!r}f"
+    if isinstance(val, int):
+        return f"static_cast<int64_t>({val}LL)"
+    return str(val)
+
+
+class HipExprPrinter(ExprPrinter):
+    """sympy index expressions -> int64 C++ expressions."""
+
+    def _print_Symbol(self, expr):
+        return str(expr)
+
+    def _print_Integer(self, expr):
+        return f"{int(expr)}LL"
+
+    def _print_FloorDiv(self, expr):
+        x, div = expr.args
+        return f"spy::floordiv_i({self.doprint(x)}, {self.doprint(div)})"
+
+    def _print_ModularIndexing(self, expr):
+        x, div, mod = expr.args
+        x = self.doprint(x)
+        if div != 1:
+            x = f"spy::floordiv_i({x}, {self.doprint(div)})"
+        return f"spy::mod_i({x}, {self.doprint(mod)})"
+
+    def _print_Mod(self, expr):
+        return f"spy::mod_i({self.doprint(expr.args[0])}, {self.doprint(expr.args[1])})"
+
+    def _print_PythonMod(self, expr):
+        return self._print_Mod(expr)
+
+    def _print_Min(self, expr):
+        args = [self.doprint(a) for a in expr.args]
+        out = args[0]
+        for a in args[1:]:
+            out = f"spy::min_i({out}, {a})"
+        return out
+
+    def _print_Max(self, expr):
+        args = [self.doprint(a) for a in expr.args]
+        out = args[0]
+        for a in args[1:]:
+            out = f"spy::max_i({out}, {a})"
+        return out
+
+    def _print_Where(self, expr):
+        c, p, q = (self.parenthesize(a, PRECEDENCE["Atom"] - 0.5) for a in expr.args)
+        return f"({c} ? {p} : {q})"
+
+    def _print_Pow(self, expr):
+        base, exp = expr.args
+        if exp.is_Integer and int(exp) >= 0:
+            b = self.parenthesize(base, PRECEDENCE["Mul"])
+            return "*".join([b] * int(exp)) if int(exp) > 0 else "1LL"
+        raise Unsupported(f"index expression {expr}")
+
+    def _print_PowByNatural(self, expr):
+        return self._print_Pow(sympy.Pow(*expr.args))
+
+    def _print_Abs(self, expr):
+        a = self.doprint(expr.args[0])
+        return f"(({a}) < 0 ? -({a}) : ({a}))"
+
+    def _print_ToFloat(self, expr):
+        return f"static_cast<float>({self.doprint(expr.args[0])})"
+
+    def _print_IntTrueDiv(self, expr):
+        a, b = expr.args
+        return f"(static_cast<float>({self.doprint(a)}) / static_cast<float>({self.doprint(b)}))"
+
+    def _print_FloorToInt(self, expr):
+        return f"static_cast<int64_t>(floorf({self.doprint(expr.args[0])}))"
+
+    def _print_TruncToInt(self, expr):
+        return f"static_cast<int64_t>(truncf({self.doprint(expr.args[0])}))"
+
+    def _print_Float(self, expr):
+        return f"{float(expr)!r}f"
+
+
+_printer = HipExprPrinter()
+
+
+class SpyreOverrides(OpOverrides):
+    """Pointwise ops as HIP C++ expressions on fp32 (or native int) values."""
+
+    @staticmethod
+    def to_dtype(x, dtype: torch.dtype, src_dtype: Optional[torch.dtype] = None,
+                 use_compute_types: bool = True):
+        if dtype == torch.float16:
+            return f"spy::round_half({x})"
+        if dtype == torch.bfloat16:
+            return f"spy::round_bf16({x})"
+        if dtype in (torch.float32, torch.float64):
+            return f"static_cast<float>({x})"
+        if dtype == torch.bool:
+            return f"(({x}) != 0)"
+        if dtype in DTYPE_TO_HIP:
+            return f"static_cast<{DTYPE_TO_HIP[dtype]}>({x})"
+        raise Unsupported(f"to_dtype {dtype}")
+
+    @staticmethod
+    def to_dtype_bitcast(x, dtype, src_dtype):
+        raise Unsupported("bitcast")
+
+    @staticmethod
+    def constant(val, dtype: torch.dtype):
+        if dtype.is_floating_point:
+            return hip_value(float(val))
+        if dtype == torch.bool:
+            return hip_value(bool(val))
+        return hip_value(int(val))
+
+    @staticmethod
+    def index_expr(expr: sympy.Expr, dtype: torch.dtype):
+        idx = V.kernel.index_to_str(V.kernel.prepare_indexing(expr))
+        var = V.kernel.cse.generate(V.kernel.compute, idx, bounds=get_bounds_index_expr(expr),
+                                    dtype=torch.int64)
+        return ops.to_dtype(var, dtype)
+
+    @staticmethod
+    def masked(mask, body, other):
+        with V.kernel.mask_loads(mask, other) as new_mask:
+            result = body()
+        if isinstance(result, tuple):
+            raise Unsupported("masked tuple")
+        other_s = hip_value(other) if not isinstance(other, CSEVariable) else str(other)
+        return f"(({new_mask}) ? ({result}) : ({other_s}))"
+
+    @staticmethod
+    def where(a, b, c):
+        return f"(({a}) ? ({b}) : ({c}))"
+
+    # comparisons / logic (C++ yields bool)
+    @staticmethod
+    def eq(a, b):
+        return f"({a} == {b})"
+
+    @staticmethod
+    def ne(a, b):
+        return f"({a} != {b})"
+
+    @staticmethod
+    def lt(a, b):
+        return f"({a} < {b})"
+
+    @staticmethod
+    def le(a, b):
+        return f"({a} <= {b})"
+
+    @staticmethod
+    def gt(a, b):
+        return f"({a} > {b})"
+
+    @staticmethod
+    def ge(a, b):
+        return f"({a} >= {b})"
+
+    @staticmethod
+    def logical_and(a, b):
+        return f"({a} && {b})"
+
+    @staticmethod
+    def logical_or(a, b):
+        return f"({a} || {b})"
+
+    @staticmethod
+    def logical_not(a):
+        return f"(!{a})"
+
+    @staticmethod
+    def logical_xor(a, b):
+        return f"(static_cast<bool>({a}) != static_cast<bool>({b}))"
+
+    @staticmethod
+    def bitwise_and(a, b):
+        return f"({a} & {b})"
+
+    @staticmethod
+    def bitwise_or(a, b):
+        return f"({a} | {b})"
+
+    @staticmethod
+    def bitwise_xor(a, b):
+        return f"({a} ^ {b})"
+
+    @staticmethod
+    def bitwise_not(a):
+        return f"(~{a})"
+
+    # arithmetic
+    @staticmethod
+    def neg(x):
+        return f"(-{x})"
+
+    @staticmethod
+    def reciprocal(x):
+        return f"(1.0f / {x})"
+
+    @staticmethod
+    def square(x):
+        return f"({x} * {x})"
+
+    @staticmethod
+    def floordiv(a, b):
+        return f"spy::floordiv({a}, {b})"
+
+    @staticmethod
+    def truncdiv(a, b):
+        return f"spy::truncdiv({a}, {b})"
+
+    @staticmethod
+    def remainder(a, b):
+        return f"spy::remainder({a}, {b})"
+
+    @staticmethod
+    def mod(a, b):
+        return f"spy::remainder({a}, {b})"
+
+    @staticmethod
+    def fmod(a, b):
+        return f"fmodf({a}, {b})"
+
+    @staticmethod
+    def pow(a, b):
+        return f"powf({a}, {b})"
+
+    @staticmethod
+    def maximum(a, b):
+        return f"spy::maximum({a}, {b})"
+
+    @staticmethod
+    def minimum(a, b):
+        return f"spy::minimum({a}, {b})"
+
+    @staticmethod
+    def abs(x):
+        return f"fabsf({x})"
+
+    @staticmethod
+    def relu(x):
+        return f"spy::relu({x})"
+
+    @staticmethod
+    def sigmoid(x):
+        return f"spy::sigmoid({x})"
+
+    @staticmethod
+    def rsqrt(x):
+        return f"spy::rsqrt({x})"
+
+    @staticmethod
+    def sign(x):
+        return f"spy::sign({x})"
+
+    @staticmethod
+    def round(x):
+        return f"rintf({x})"
+
+    @staticmethod
+    def isnan(x):
+        return f"({x} != {x})"
+
+    @staticmethod
+    def isinf(x):
+        return f"(spy::isinf_({x}) != 0.f)"
+
+    @staticmethod
+    def signbit(x):
+        return f"signbit({x})"
+
+    @staticmethod
+    def fma(a, b, c):
+        return f"fmaf({a}, {b}, {c})"
+
+
+def _unary_fn(fn: str):
+    return staticmethod(lambda x: f"{fn}({x})")
+
+
+for _name, _fn in {
+    "exp": "expf", "exp2": "exp2f", "expm1": "expm1f", "log": "logf", "log2": "log2f",
+    "log10": "log10f", "log1p": "log1pf", "sqrt": "sqrtf", "sin": "sinf", "cos": "cosf",
+    "tan": "tanf", "tanh": "tanhf", "asin": "asinf", "acos": "acosf", "atan": "atanf",
+    "sinh": "sinhf", "cosh": "coshf", "asinh": "asinhf", "acosh": "acoshf", "atanh": "atanhf",
+    "erf": "erff", "erfc": "erfcf", "floor": "floorf", "ceil": "ceilf", "trunc": "truncf",
+    "lgamma": "lgammaf",
+}.items():
+    setattr(SpyreOverrides, _name, _unary_fn(_fn))
+
+SpyreOverrides.atan2 = staticmethod(lambda a, b: f"atan2f({a}, {b})")
+SpyreOverrides.copysign = staticmethod(lambda a, b: f"copysignf({a}, {b})")
+SpyreOverrides.hypot = staticmethod(lambda a, b: f"hypotf({a}, {b})")
+
+
+class SpyreKernel(SIMDKernel):
+    """One generated HIP kernel (see module docstring)."""
+
+    overrides = SpyreOverrides  # type: ignore[assignment]
+    suffix = ";"
+    newvar_prefix = "auto "
+    kexpr = _printer.doprint
+
+    def __init__(self, tiling: dict[str, sympy.Expr], **kwargs: Any) -> None:
+        super().__init__(tiling, **kwargs)
+        self._acc_ids = itertools.count()
+        self._rloop_open = False
+        self._pending_accum = False
+        # outer buffer name -> max element extent (None = not checkable)
+        self._extents: dict[str, Optional[int]] = {}
+
+    # -- sizes ----------------------------------------------------------------
+    def _static(self, e) -> int:
+        if not isinstance(e, (int, sympy.Integer)):
+            raise Unsupported(f"dynamic size {e}")
+        return int(e)
+
+    def _xnumel(self) -> int:
+        n = 1
+        for t in self.range_trees:
+            if not t.is_reduction:
+                n *= self._static(t.numel)
+        return n
+
+    def _rnumel(self) -> int:
+        n = 1
+        for t in self.range_trees:
+            if t.is_reduction:
+                n *= self._static(t.numel)
+        return n
+
+    def _block(self) -> int:
+        if self.inside_reduction or self.features.is_reduction():
+            return min(MAX_BLOCK, max(64, _next_pow2(self._rnumel())))
+        return 256
+
+    def dtype_to_str(self, dtype: torch.dtype) -> str:
+        try:
+            return DTYPE_TO_HIP[dtype]
+        except KeyError:
+            raise Unsupported(f"dtype {dtype}")
+
+    def should_use_persistent_reduction(self) -> bool:
+        return False  # reductions are strided loops over the row
+
+    def should_use_cooperative_reduction(self) -> bool:
+        return False
+
+    # -- index ranges -----------------------------------------------------------
+    def _record_extent(self, name: str, index: sympy.Expr, masked: bool) -> None:
+        ext: Optional[int]
+        if masked:
+            ext = None
+        else:
+            ranges = {}
+            for sym, entry in self.range_tree_nodes.items():
+                ranges[sym] = ValueRanges(0, self._static(entry.length) - 1)
+            free = index.free_symbols
+            if any(s not in ranges for s in free):
+                ext = None  # indirect (gathered) index
+            else:
+                vr = bound_sympy(index, {s: ranges[s] for s in free})
+                lo, hi = vr.lower, vr.upper
+                if not (lo.is_number and hi.is_number) or lo < 0:
+                    raise Unsupported(f"cannot bound index {index}")
+                ext = int(hi) + 1
+        prev = self._extents.get(name, 0)
+        if prev is None or ext is None:
+            self._extents[name] = None
+        else:
+            self._extents[name] = max(prev, ext)
+
+    def _open_rloop(self) -> None:
+        if self._rloop_open:
+            return
+        r, b = self._rnumel(), self._block()
+        loops = (r + b - 1) // b
+        self.body.writeline(f"for (int64_t r0_cnt = 0; r0_cnt < {loops}LL; ++r0_cnt) {{")
+        with self.body.indent():
+            self.body.writeline(f"const int64_t r0_index = r0_cnt * {b}LL + threadIdx.x;")
+            if loops * b != r:
+                self.body.writeline(f"if (r0_index >= {r}LL) break;")
+        self._rloop_open = True
+
+    def codegen_iteration_ranges_entry(self, entry: IterationRangesEntry) -> None:
+        expr = self.kexpr(self.rename_indexing(entry.expr))
+        if entry.is_reduction:
+            self._open_rloop()
+            with self.body.indent():
+                self.body.writeline(f"const int64_t {entry.name} = {expr};")
+        else:
+            self.indexing_code.writeline(f"const int64_t {entry.name} = {expr};")
+
+    # -- memory -------------------------------------------------------------------
+    def load(self, name: str, index: sympy.Expr) -> CSEVariable:
+        var = self.args.input(name)
+        index = self.prepare_indexing(index)
+        dtype = V.graph.get_dtype(name)
+        self.dtype_to_str(dtype)
+        masked = bool(self._load_mask)
+        self._record_extent(name, index, masked)
+        line = f"{var}[{self.index_to_str(index)}]"
+        if dtype in _FLOAT_LOAD:
+            line = f"spy::to_f({line})"
+            out_dtype = torch.float32
+        else:
+            out_dtype = dtype
+        buf = self.loads
+        if masked:
+            other = self._load_other
+            other_s = hip_value(other) if other is not None else "0"
+            line = f"(({self._load_mask}) ? {line} : {other_s})"
+            buf = self.compute
+        elif self.is_indirect_indexing(index):
+            buf = self.compute
+        return self.cse.generate(buf, line, dtype=out_dtype)
+
+    def store(self, name: str, index: sympy.Expr, value: CSEVariable,
+              mode: Any = None) -> None:
+        if mode is not None:
+            raise Unsupported(f"store mode {mode}")
+        var = self.args.output(name)
+        index = self.prepare_indexing(index)
+        dtype = V.graph.get_dtype(name)
+        self._record_extent(name, index, False)
+        line = f"{var}[{self.index_to_str(index)}] = spy::cvt<{self.dtype_to_str(dtype)}>({value});"
+        if self.inside_reduction:
+            self.compute.writeline(DeferredLine(name, line))
+        else:
+            self.stores.writeline(DeferredLine(name, line))
+
+    def store_reduction(self, name: str, index: sympy.Expr, value: CSEVariable) -> None:
+        var = self.args.output(name)
+        index = self.prepare_indexing(index)
+        dtype = V.graph.get_dtype(name)
+        self._record_extent(name, index, False)
+        line = (f"if (threadIdx.x == 0) {var}[{self.index_to_str(index)}] = "
+                f"spy::cvt<{self.dtype_to_str(dtype)}>({value});")
+        self.stores.writeline(DeferredLine(name, line))
+
+    def check_bounds(self, expr: sympy.Expr, size: sympy.Expr, lower: bool, upper: bool) -> None:
+        # Indirect indices (gathers) are clamped into range instead of
+        # asserting: an out-of-range index reads row 0 rather than faulting.
+        if not (lower or upper):
+            return
+        if not isinstance(expr, sympy.Symbol):
+            raise Unsupported(f"bounds check on {expr}")
+        e = str(expr)
+        n = self.index_to_str(size)
+        self.compute.writeline(f"{e} = ({e} < 0 || {e} >= {n}) ? 0 : {e};")
+
+    # -- reductions ---------------------------------------------------------------
+    def _acc(self, decl: str) -> str:
+        name = f"acc{next(self._acc_ids)}"
+        self.indexing_code.writeline(decl.format(name=name))
+        return name
+
+    def reduction(self, dtype, src_dtype, reduction_type, value):
+        key = (src_dtype, reduction_type, value)
+        if key in self.cse.reduction_cache:
+            return self.cse.reduction_cache[key]
+        result = self._reduction(dtype, src_dtype, reduction_type, value)
+        self.cse.reduction_cache[key] = result  # type: ignore[assignment]
+        return result
+
+    def _reduction(self, dtype, src_dtype, reduction_type, value):
+        assert self.inside_reduction
+        if self._load_mask:
+            raise Unsupported("masked reduction")
+        b = self._block()
+        self._pending_accum = True
+        ops_map = {"sum": "SumF", "prod": "ProdF", "max": "MaxF", "min": "MinF", "any": "AnyF"}
+        if reduction_type in ops_map:
+            op = ops_map[reduction_type]
+            acc = self._acc(f"float {{name}} = spy::{op}::id();")
+            self.compute.writeline(f"{acc} = spy::{op}::op({acc}, static_cast<float>({value}));")
+            return self.cse.generate(
+                self.stores, f"spy::block_reduce<spy::{op}, {b}>({acc}, spy_lds)",
+                dtype=torch.float32)
+        if reduction_type in ("argmax", "argmin"):
+            is_max = "true" if reduction_type == "argmax" else "false"
+            init = "-spy::inf()" if reduction_type == "argmax" else "spy::inf()"
+            av = self._acc(f"float {{name}} = {init};")
+            ai = self._acc("int64_t {name} = 0x7fffffffffffffffLL;")
+            rvar = "r0_index"
+            self.compute.writeline(
+                f"spy::arg_combine<{is_max}>({av}, {ai}, static_cast<float>({value}), {rvar});")
+            return self.cse.generate(
+                self.stores, f"spy::block_arg<{is_max}, {b}>({av}, {ai}, spy_lds, spy_lds_i)",
+                dtype=torch.int64)
+        if reduction_type == "welford_reduce":
+            acc = self._acc("spy::Welford {name} = {{0.f, 0.f, 0.f}};")
+            self.compute.writeline(f"{acc} = spy::welford_add({acc}, static_cast<float>({value}));")
+            res = self.cse.generate(self.stores, f"spy::block_welford<{b}>({acc}, spy_lds)",
+                                    dtype=torch.float32)
+            return OpsWrapper._unwrap(
+                tuple(CSEVariable(f"{res}.{f}", ValueRanges.unknown(), torch.float32)
+                      for f in ("mean", "m2", "weight")))
+        if reduction_type == "welford_combine":
+            mean, m2, weight = value
+            acc = self._acc("spy::Welford {name} = {{0.f, 0.f, 0.f}};")
+            self.compute.writeline(
+                f"{acc} = spy::welford_combine({acc}, spy::Welford{{static_cast<float>({mean}), "
+                f"static_cast<float>({m2}), static_cast<float>({weight})}});")
+            res = self.cse.generate(self.stores, f"spy::block_welford<{b}>({acc}, spy_lds)",
+                                    dtype=torch.float32)
+            return OpsWrapper._unwrap(
+                tuple(CSEVariable(f"{res}.{f}", ValueRanges.unknown(), torch.float32)
+                      for f in ("mean", "m2", "weight")))
+        raise Unsupported(f"reduction {reduction_type}")
+
+    # -- assembly -----------------------------------------------------------------
+    def codegen_body(self) -> None:
+        if self._pending_accum and not self._rloop_open and self.inside_reduction:
+            self._open_rloop()
+        if self._rloop_open:
+            with self.body.indent():
+                self.body.splice(self.loads)
+                self.body.splice(self.compute)
+            self.body.writeline("}")
+            self._rloop_open = False
+            # values computed inside the loop die with it; reduction results
+            # (made after the loop) stay available to later phases
+            keep = set()
+            for item in self.cse.reduction_cache.values():
+                for v in (item if isinstance(item, tuple) else (item,)):
+                    keep.add(v)
+            from torch.utils._ordered_set import OrderedSet
+
+            self.cse.invalidate(OrderedSet(keep))
+            for entry in self.range_tree_nodes.values():
+                if entry.is_reduction:
+                    entry.cache_clear()
+        else:
+            self.body.splice(self.loads)
+            self.body.splice(self.compute)
+        self._pending_accum = False
+        self.body.splice(self.stores)
+        self.loads.clear()
+        self.compute.clear()
+        self.stores.clear()
+
+    def _kernel_args(self):
+        arg_defs, call_args, _, arg_types = self.args.python_argdefs()
+        if self.args.sizevars or self.args.workspace_args:
+            raise Unsupported("dynamic sizes / workspaces")
+        outputs = {inner for inner in self.args.output_buffers.values() if isinstance(inner, str)}
+        for inplaced in self.args.inplace_buffers.values():
+            if hasattr(inplaced, "inner_name"):
+                outputs.add(inplaced.inner_name)
+        return arg_defs, call_args, arg_types, outputs
+
+    def codegen_kernel(self, name: Optional[str] = None) -> str:
+        self.codegen_body()
+        is_red = self.features.is_reduction()
+        xnumel, rnumel = self._xnumel(), (self._rnumel() if is_red else 1)
+        block = self._block()
+        arg_defs, call_args, arg_types, outputs = self._kernel_args()
+        params = []
+        spec_args = []
+        for i, (ad, outer, dt) in enumerate(zip(arg_defs, call_args, arg_types)):
+            inner = str(ad.name) if hasattr(ad, "name") else str(ad)
+            ctype = self.dtype_to_str(dt)
+            if inner in outputs or inner.startswith("in_out_ptr"):
+                params.append(f"{ctype}* __restrict__ {inner}")
+                is_input = False
+            else:
+                params.append(f"const {ctype}* __restrict__ {inner}")
+                is_input = True
+            ext = self._extents.get(outer, 0)
+            spec_args.append(f"TensorArg(is_input={is_input}, arg_index={i}, "
+                             f"dtype={dt!r}, extent={ext!r})")
+        code = IndentedBuffer()
+        code.writeline('#include "spyre_inductor_rt.h"')
+        code.writeline(f'extern "C" __global__ void __launch_bounds__({block}) spyre_kernel(')
+        with code.indent():
+            code.writeline(",\n".join(params) if params else "")
+        code.writeline(") {")
+        with code.indent():
+            if is_red:
+                code.writeline(f"__shared__ float spy_lds[3 * {max(1, block // 64)}];")
+                code.writeline(f"__shared__ int64_t spy_lds_i[{max(1, block // 64)}];")
+                code.writeline("const int64_t xindex = blockIdx.x;")
+                grid = xnumel
+            else:
+                code.writeline(f"const int64_t xindex = static_cast<int64_t>(blockIdx.x) * {block}LL"
+                               " + threadIdx.x;")
+                code.writeline(f"if (xindex >= {xnumel}LL) return;")
+                grid = (xnumel + block - 1) // block
+            code.splice(self.indexing_code)
+            code.splice(self.body)
+        code.writeline("}")
+        src = code.getvalue()
+        if grid <= 0 or grid >= 2**31:
+            raise Unsupported(f"grid {grid}")
+        spec = IndentedBuffer()
+        spec.writeline("KernelSpec(")
+        with spec.indent():
+            spec.writeline(f"op={'reduction' if is_red else 'pointwise'!r},")
+            spec.writeline(f"is_reduction={is_red},")
+            spec.writeline(f"dimensions={[xnumel, rnumel] if is_red else [xnumel]!r},")
+            spec.writeline(f"grid={grid}, block={block},")
+            spec.writeline("args=[")
+            with spec.indent():
+                for a in spec_args:
+                    spec.writeline(a + ",")
+            spec.writeline("],")
+            spec.writeline(f"source={src!r},")
+        spec.writeline(")")
+        return spec.getvalue()
+
+    def call_kernel(self, name: str, node: Any = None, deallocate_ws: bool = True) -> None:
+        wrapper = V.graph.wrapper_code
+        _, call_args, _, _ = self.args.python_argdefs()
+        wrapper.writeline(f"{name}.run({', '.join(str(a) for a in call_args)})")
