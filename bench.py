@@ -194,6 +194,55 @@ def bench_copy(steps, warmup, stream, capi):
             "GB/s": round(2 * n * 2 / (ms * 1e-3) / 1e9, 1)}
 
 
+def _spyre_timer():
+    """Timer on the spyre stream (HIP events recorded on that stream)."""
+    import torch
+
+    from torch_spyre import _C
+
+    return Timer(torch.cuda.ExternalStream(_C._stream_handle(0)))
+
+
+def bench_spyre_paths(steps, warmup):
+    """The drop-in paths on "spyre" tensors: eager ATen kernels and
+    torch.compile-generated kernels for the c1 / c3 workloads."""
+    import torch
+    import torch.nn.functional as F
+
+    import torch_spyre  # noqa: F401
+
+    timer = _spyre_timer()
+    out = {}
+
+    def entry(name, nbytes, fn):
+        fn()
+        torch.spyre.synchronize()
+        ms, _ = timer.run(fn, steps, warmup)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us_per_call": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                     "roofline_frac": round(gbs / PEAK_HBM_GBS, 4)}
+
+    R, C = 512, 4096
+    x = (torch.randn(R, C, generator=_gen(0)) * 4).half().to("spyre")
+    sm = torch.compile(lambda a: torch.softmax(a, dim=-1))
+    entry("c1_softmax_eager_spyre", 2 * R * C * 2, lambda: torch.softmax(x, -1))
+    entry("c1_softmax_compiled_spyre", 2 * R * C * 2, lambda: sm(x))
+    R, C = 8192, 4096
+    x = torch.randn(R, C, generator=_gen(0)).half().to("spyre")
+    r = torch.randn(R, C, generator=_gen(1)).half().to("spyre")
+    w = (torch.randn(C, generator=_gen(2)) * 0.02 + 1).half().to("spyre")
+    b = (torch.randn(C, generator=_gen(3)) * 0.02).half().to("spyre")
+    rms = torch.compile(lambda a, c, g: (lambda s: (s, torch.rms_norm(s, [C], g, 1e-5)))(a + c))
+    ln = torch.compile(lambda a, c, g, e: (lambda s: (s, F.layer_norm(s, [C], g, e, 1e-5)))(a + c))
+    gl = torch.compile(lambda a, s, c: (lambda t: (t, t.sum(-1)))(F.gelu(a * s + c)))
+    entry("c3_add_rmsnorm_compiled_spyre", 4 * R * C * 2 + C * 2, lambda: rms(x, r, w))
+    entry("c3_add_layernorm_compiled_spyre", 4 * R * C * 2 + 2 * C * 2, lambda: ln(x, r, w, b))
+    entry("c3_gelu_rowsum_compiled_spyre", 2 * R * C * 2 + 2 * C * 2 + R * 2, lambda: gl(x, w, b))
+    entry("c3_rms_norm_eager_spyre", 2 * R * C * 2 + C * 2,
+          lambda: torch.rms_norm(x, [C], w, 1e-5))
+    return out
+
+
 def bench_eager_mm(steps, warmup):
     """torch.mm on "spyre" tensors: the drop-in (PrivateUse1) path to the same
     kernel, timed on the spyre stream."""
@@ -281,6 +330,8 @@ def main(argv=None):
         extra = bench_extra(max(10, args.steps), args.warmup, stream, _capi)
         _log("eager torch.mm on spyre tensors")
         extra["c2_mm_4096_spyre_device_eager"] = bench_eager_mm(max(10, args.steps), args.warmup)
+        _log("spyre device paths (eager + torch.compile)")
+        extra["spyre_device"] = bench_spyre_paths(max(10, args.steps), args.warmup)
     cpu = None
     if not args.no_cpu:
         _log("cpu baseline")
