@@ -8,10 +8,21 @@ torch.Generator().manual_seed(0xAFFE + k), then cast.
 
 from __future__ import annotations
 
+import json
+import os
+
 import numpy as np
 import torch
 
 SEED = 0xAFFE
+GOLDEN_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def golden(name: str):
+    """A section of tests/golden/reference_vectors.json (the reference
+    tests' known answers)."""
+    with open(os.path.join(GOLDEN_DIR, "reference_vectors.json")) as f:
+        return json.load(f)[name]
 
 
 def gen(k: int) -> torch.Generator:

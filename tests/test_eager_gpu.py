@@ -23,7 +23,7 @@ import torch_spyre  # noqa: F401  (registers the backend)
 
 from oracle import ops as O
 
-from helpers import assert_close_fp, randn, uniform
+from helpers import assert_close_fp, golden, randn, uniform
 
 pytestmark = pytest.mark.gpu
 
@@ -64,24 +64,27 @@ def test_ones_zeros_full():
     assert torch.ones(50, device=DEV, dtype=torch.float16).cpu().eq(1.0).all()
     assert torch.zeros(3, 7, device=DEV).cpu().eq(0).all()
     assert torch.full((4, 5), -2, device=DEV, dtype=torch.int32).cpu().eq(-2).all()
-    x = torch.tensor([1, -2, 3], dtype=torch.float16, device=DEV)
-    x.fill_(5.0)
-    assert torch.equal(x.cpu(), torch.tensor([5.0, 5.0, 5.0], dtype=torch.float16))
+    for c in golden("fill")["cases"]:
+        x = torch.tensor([1, -2, 3], dtype=torch.float16, device=DEV)
+        assert list(x.shape) == c["shape"]
+        x.fill_(c["value"])
+        assert torch.equal(x.cpu(), torch.tensor(c["out"], dtype=torch.float16))
 
 
 def test_str_and_repr_strings():
     _log("repr strings")
-    a = torch.tensor([1, 2], dtype=torch.float16).to(DEV)
-    assert _norm_dev(str(a)) == "tensor([1., 2.], dtype=torch.float16, device='spyre:0')"
-    b = torch.tensor([1.234242424234, 2], dtype=torch.float16).to(DEV)
-    assert _norm_dev(f"{b}") == "tensor([1.2344, 2.0000], dtype=torch.float16, device='spyre:0')"
+    for c in golden("repr")["cases"]:
+        a = torch.tensor(c["values"], dtype=torch.float16).to(DEV)
+        assert _norm_dev(str(a)) == c["text"]
+        assert _norm_dev(f"{a}") == c["text"]
     print(torch.ones((2, 3), device=DEV, dtype=torch.float16))
 
 
 def test_allocation_size_is_stick_granular():
     _log("allocation size")
-    x = torch.tensor([1, 2], dtype=torch.float16, device=DEV)
-    assert x.untyped_storage().nbytes() == 128
+    for c in golden("allocation")["cases"]:
+        x = torch.empty(c["host_size"], dtype=torch.float16, device=DEV)
+        assert x.untyped_storage().nbytes() == c["nbytes"]
     y = torch.empty(512, 4096, dtype=torch.float16, device=DEV)
     assert y.untyped_storage().nbytes() == 512 * 4096 * 2
     z = torch.empty(3, 65, dtype=torch.float16, device=DEV)  # 65 -> 2 sticks per row
@@ -193,11 +196,10 @@ def test_binary_kats():
     x = torch.tensor([1, 2, 3], dtype=torch.float16)
     y = torch.tensor([4, 5, 6], dtype=torch.float16)
     xd, yd = x.to(DEV), y.to(DEV)
-    _cmp(torch.add(xd, yd), x + y)
-    _cmp(torch.subtract(torch.tensor([10, 20, 3], dtype=torch.float16).to(DEV), yd),
-         torch.tensor([6, 15, -3], dtype=torch.float16))
-    _cmp(torch.mul(torch.tensor([1, 0, -3], dtype=torch.float16).to(DEV), yd),
-         torch.tensor([4, 0, -18], dtype=torch.float16))
+    ops = {"add": torch.add, "sub": torch.subtract, "mul": torch.mul}
+    for c in golden("binary")["cases"]:
+        a, b = (torch.tensor(c[k], dtype=torch.float16).to(DEV) for k in ("x", "y"))
+        assert torch.equal(ops[c["op"]](a, b).cpu(), torch.tensor(c["out"], dtype=torch.float16))
     _cmp(xd / yd, x / y)
     _cmp(xd + 5, x + 5)
     _cmp(2 - xd, 2 - x)
@@ -324,6 +326,8 @@ def test_mm_arange_kat_exact(ab):
     # fp32 accumulation of small integers is exact; the fp16 result is the
     # exact product rounded once
     assert torch.equal(z, (x.float() @ y.float()).half())
+    if ab == ("a", "b", "b", "c"):
+        assert torch.equal(z, torch.tensor(golden("mm_arange")["out"], dtype=torch.float16))
 
 
 def test_bmm_matmul_linear_addmm():

@@ -16,6 +16,8 @@ from torch_spyre._C import SpyreTensorLayout as STL
 
 from oracle import layout as L
 
+from helpers import golden
+
 
 def _check(stl, size, strides, dmap, fmt=STL.StickFormat.Dense):
     assert stl.device_size == size
@@ -29,16 +31,11 @@ def test_backend_registered():
     assert torch._C._get_privateuse1_backend_name() == "spyre"
 
 
-def test_generic_stick_golden():
-    _check(STL([128], torch.float16), [2, 64], [64, 1], [0, 0])
-    _check(STL([512, 256], torch.float16), [4, 512, 64], [32768, 64, 1], [1, 0, 1])
-    _check(STL([512, 8, 256], torch.float16), [4, 512, 8, 64], [262144, 512, 64, 1], [2, 0, 1, 2])
-
-
-def test_dim_order_golden():
-    _check(STL([512, 256], torch.float16, [1, 0]), [8, 256, 64], [16384, 64, 1], [0, 1, 0])
-    _check(STL([512, 8, 256], torch.float16, [2, 1, 0]), [8, 256, 8, 64], [131072, 512, 64, 1],
-           [0, 2, 1, 0])
+def test_layout_golden():
+    for c in golden("spyre_tensor_layout")["cases"]:
+        stl = (STL(c["host_size"], torch.float16) if c["dim_order"] is None
+               else STL(c["host_size"], torch.float16, c["dim_order"]))
+        _check(stl, c["device_size"], c["device_strides"], c["dim_map"])
 
 
 def test_explicit_and_sparse_constructors():
@@ -51,9 +48,8 @@ def test_explicit_and_sparse_constructors():
 
 
 def test_str_golden():
-    assert str(STL([512, 256], torch.float16)) == (
-        'SpyreTensorLayout(device_size=[4, 512, 64], device_strides=[32768, 64, 1], '
-        'dim_map =[1, 0, 1], num_stick_dims=1, format="Dense")')
+    g = golden("spyre_tensor_layout")["str"]
+    assert str(STL(g["host_size"], torch.float16)) == g["text"]
 
 
 @pytest.mark.parametrize("dtype,eb", [(torch.float16, 2), (torch.float32, 4), (torch.int8, 1),

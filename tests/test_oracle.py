@@ -18,19 +18,13 @@ import torch.nn.functional as F
 from oracle import layout as L
 from oracle import ops as O
 
-from helpers import randn, uniform
+from helpers import golden, randn, uniform
 
 # --------------------------------------------------------------------------
 # SpyreTensorLayout golden vectors: tests/tensor/test_tensor_layout.py:28-94
 # --------------------------------------------------------------------------
-GOLDEN_STL = [
-    # host_size, dim_order, device_size, device_strides, dim_map
-    ([128], None, [2, 64], [64, 1], [0, 0]),
-    ([512, 256], None, [4, 512, 64], [32768, 64, 1], [1, 0, 1]),
-    ([512, 8, 256], None, [4, 512, 8, 64], [262144, 512, 64, 1], [2, 0, 1, 2]),
-    ([512, 256], [1, 0], [8, 256, 64], [16384, 64, 1], [0, 1, 0]),
-    ([512, 8, 256], [2, 1, 0], [8, 256, 8, 64], [131072, 512, 64, 1], [0, 2, 1, 0]),
-]
+GOLDEN_STL = [(c["host_size"], c["dim_order"], c["device_size"], c["device_strides"], c["dim_map"])
+              for c in golden("spyre_tensor_layout")["cases"]]
 
 
 @pytest.mark.parametrize("host,order,dsize,dstrides,dmap", GOLDEN_STL)
@@ -42,10 +36,9 @@ def test_stl_golden(host, order, dsize, dstrides, dmap):
 
 
 def test_stl_str_golden():
-    ds, dst, dm = L.stl_init([512, 256], 2)
-    assert L.stl_to_string(ds, dst, dm) == (
-        'SpyreTensorLayout(device_size=[4, 512, 64], device_strides=[32768, 64, 1], '
-        'dim_map =[1, 0, 1], num_stick_dims=1, format="Dense")')
+    g = golden("spyre_tensor_layout")["str"]
+    ds, dst, dm = L.stl_init(g["host_size"], 2)
+    assert L.stl_to_string(ds, dst, dm) == g["text"]
 
 
 @pytest.mark.parametrize("eb", [1, 2, 4, 8])
@@ -67,7 +60,8 @@ def test_stl_closed_form(eb):
 # Allocation sizing: tests/test_spyre.py:171-176 (128 B for a 2-element fp16)
 # --------------------------------------------------------------------------
 def test_alloc_golden():
-    assert L.alloc_nbytes([2], 2) == 128
+    for c in golden("allocation")["cases"]:
+        assert L.alloc_nbytes(c["host_size"], c["elem_bytes"]) == c["nbytes"]
     assert L.alloc_nbytes([], 2) == 128
     assert L.alloc_nbytes([512, 4096], 2) == 512 * 4096 * 2
     assert L.alloc_nbytes([8192, 4096], 2) == 64 * 2**20

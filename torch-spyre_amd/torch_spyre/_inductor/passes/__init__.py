@@ -1,0 +1,34 @@
+"""Graph-pass hook of the spyre backend.
+
+Reference: torch_spyre/_inductor/passes/__init__.py:26-49, which installs a
+pre-grad list containing RemoveElementTypeConversions (every
+`convert_element_type` deleted, "all device ops are fp16") into Inductor's
+global config.  Here the passes run through the per-device custom pass of
+`register_backend_for_device`, i.e. only on post-grad graphs that hold spyre
+tensors, and no conversion is removed: kernels upcast to fp32 internally, so
+the conversions Inductor sees are the ones the program asked for.  The list
+is empty by default; a pass is any callable taking the GraphModule.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Callable, List, Optional
+
+import torch
+from torch._inductor.custom_graph_pass import CustomGraphModulePass, get_hash_for_files
+
+custom_post_passes: List[Callable[[torch.fx.GraphModule], None]] = []
+
+
+class CustomPostPasses(CustomGraphModulePass):
+    def __call__(self, gm: torch.fx.GraphModule) -> None:
+        for p in custom_post_passes:
+            p(gm)
+
+    def uuid(self) -> Optional[Any]:
+        files = {__file__}
+        for p in custom_post_passes:
+            f = getattr(p, "file", None)
+            if callable(f):
+                files.add(f())
+        return (get_hash_for_files(tuple(sorted(files))), tuple(repr(p) for p in custom_post_passes))
