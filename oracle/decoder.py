@@ -1,0 +1,149 @@
+"""numpy restatement of the decoder workload (configs c4 / c5).
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+The workload is defined by the benchmark configs, not by a reference file:
+RMSNorm (eps 1e-5) -> Q/K/V projections -> RoPE (theta 1e4, rotate-half) ->
+causal grouped-query attention (32 query heads over 8 KV heads, query head
+h reads KV head h // 4) -> output projection + residual -> RMSNorm ->
+SwiGLU MLP + residual; embedding gather in front, final RMSNorm and LM head
+behind.  Arithmetic is float32 with float32 accumulation; with act=np.float16
+intermediate values are rounded to fp16 where the device program holds an
+fp16 tensor.  `fused` selects which program: False = eager (every op's
+output is an fp16 tensor: RoPE rounds x*cos, rot*sin and their sum; the
+scores round after the bmm and again after the scale; SiLU rounds before
+the gate product), True = compiled (Inductor keeps values in registers
+inside each fused kernel: RoPE and SiLU*up round once, the scale is applied
+to the fp16 bmm output without another rounding).
+
+Pinned by tests/test_decoder.py against torch's CPU float32 ops with
+F.scaled_dot_product_attention (is_causal, enable_gqa) as an independent
+attention, causality (outputs at t do not change when later tokens do),
+RoPE's relative-position property and GQA == MHA with duplicated K/V heads.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from . import ops as O
+
+
+def _r(x, act):
+    x = np.asarray(x, dtype=np.float32)
+    return x if act is None else x.astype(act).astype(np.float32)
+
+
+def _linear(x, w, act):
+    return _r(np.matmul(x.astype(np.float32), np.asarray(w, np.float32).T), act)
+
+
+def _rmsnorm(x, w, eps, act):
+    x = np.asarray(x, np.float32)
+    ms = np.mean(x.astype(np.float64) ** 2, axis=-1, keepdims=True)
+    return _r(x / np.sqrt(ms + eps).astype(np.float32) * np.asarray(w, np.float32), act)
+
+
+def rope_tables(head_dim, positions, theta=1e4):
+    """cos / sin [len(positions), head_dim]: angle_i = pos * theta^(-2i/d)
+    in float32 (both halves equal), as the device tables are built."""
+    inv = (1.0 / (np.float32(theta) ** (np.arange(0, head_dim, 2, dtype=np.float32)
+                                         / np.float32(head_dim)))).astype(np.float32)
+    ang = np.asarray(positions, np.float32)[:, None] * inv[None, :]
+    ang = np.concatenate([ang, ang], axis=-1)
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def _rope(x, cos, sin, act, fused=False):
+    """x [B, S, H, D]; the rotate-half rotation of oracle.ops.rope."""
+    half = x.shape[-1] // 2
+    rot = np.concatenate([-x[..., half:], x[..., :half]], axis=-1)
+    c = _r(cos, act)[None, :, None, :]
+    s = _r(sin, act)[None, :, None, :]
+    if fused:
+        return _r(x * c + rot * s, act)
+    return _r(_r(x * c, act) + _r(rot * s, act), act)
+
+
+def attention(q, k, v, q_pos, k_pos, act=None, fused=False):
+    """q [B, Sq, Hq, D], k / v [B, Sk, Hkv, D]; causal on absolute
+    positions (key position <= query position).  Returns [B, Sq, Hq*D]."""
+    B, Sq, Hq, D = q.shape
+    Hkv = k.shape[2]
+    g = Hq // Hkv
+    out = np.empty((B, Sq, Hq, D), np.float32)
+    allowed = np.asarray(k_pos)[None, :] <= np.asarray(q_pos)[:, None]
+    for b in range(B):
+        for h in range(Hq):
+            kh = h // g
+            s = _r(q[b, :, h].astype(np.float32) @ k[b, :, kh].astype(np.float32).T, act)
+            s = s * np.float32(1.0 / np.sqrt(D))
+            if not fused:
+                s = _r(s, act)
+            s = np.where(allowed, s, np.float32(-np.inf))
+            p = _r(O.softmax(s, axis=-1), act)
+            out[b, :, h] = _r(p @ v[b, :, kh].astype(np.float32), act)
+    return out.reshape(B, Sq, Hq * D)
+
+
+def layer(h, w, cfg, positions, act=np.float16, kv_prefix=None, fused=False):
+    """One decoder layer.  h [B, S, hidden] at absolute `positions`;
+    kv_prefix = (k, v) [B, P, Hkv, D] of earlier positions (decode).
+    Returns (h_out, (k, v) of all positions)."""
+    B, S, _ = h.shape
+    H, Hkv, D = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+    x = _rmsnorm(h, w["attn_norm"], cfg.eps, act)
+    q = _linear(x, w["wq"], act).reshape(B, S, H, D)
+    k = _linear(x, w["wk"], act).reshape(B, S, Hkv, D)
+    v = _linear(x, w["wv"], act).reshape(B, S, Hkv, D)
+    cos, sin = rope_tables(D, positions, cfg.rope_theta)
+    q, k = _rope(q, cos, sin, act, fused), _rope(k, cos, sin, act, fused)
+    k_pos = np.asarray(positions)
+    if kv_prefix is not None:
+        k = np.concatenate([kv_prefix[0], k], axis=1)
+        v = np.concatenate([kv_prefix[1], v], axis=1)
+        k_pos = np.arange(k.shape[1])
+    a = attention(q, k, v, np.asarray(positions), k_pos, act, fused)
+    h = _r(h + _linear(a, w["wo"], act), act)
+    x = _rmsnorm(h, w["mlp_norm"], cfg.eps, act)
+    gte = _linear(x, w["wg"], act)
+    up = _linear(x, w["wu"], act)
+    m = _r((O.silu(gte) if fused else _r(O.silu(gte), act)) * up, act)
+    return _r(h + _linear(m, w["wd"], act), act), (k, v)
+
+
+def embed(tokens, table, act=np.float16):
+    return _r(np.asarray(table, np.float32)[np.asarray(tokens)], act)
+
+
+def block(tokens, params, cfg, act=np.float16, fused=False):
+    """c4: embedding + layers over tokens [B, S] -> hidden [B, S, hidden]."""
+    h = embed(tokens, params["embed"], act)
+    pos = np.arange(np.asarray(tokens).shape[1])
+    for w in params["layers"]:
+        h, _ = layer(h, w, cfg, pos, act, fused=fused)
+    return h
+
+
+def logits(h_last, params, cfg, act=np.float16):
+    x = _rmsnorm(h_last, params["final_norm"], cfg.eps, act)
+    return _linear(x, params["lm_head"], act)
+
+
+def generate_teacher_forced(prompt, teacher, params, cfg, act=np.float16, fused=False):
+    """Prefill `prompt` [B, S], then feed `teacher` [B, T] one token at a
+    time.  Returns logits [T+1, B, vocab] (prefill's last position first)."""
+    prompt = np.asarray(prompt)
+    B, S = prompt.shape
+    h = embed(prompt, params["embed"], act)
+    caches = []
+    for w in params["layers"]:
+        h, kv = layer(h, w, cfg, np.arange(S), act, fused=fused)
+        caches.append(kv)
+    out = [logits(h[:, -1], params, cfg, act)]
+    for t in range(np.asarray(teacher).shape[1]):
+        h = embed(np.asarray(teacher)[:, t:t + 1], params["embed"], act)
+        for i, w in enumerate(params["layers"]):
+            h, caches[i] = layer(h, w, cfg, np.array([S + t]), act, kv_prefix=caches[i])
+        out.append(logits(h[:, -1], params, cfg, act))
+    return np.stack(out, 0)

@@ -1,0 +1,136 @@
+"""The decoder workload (configs c4 / c5) on the CPU: the numpy oracle
+(oracle/decoder.py) pinned against an independent torch float32 decoder
+built on F.scaled_dot_product_attention, causality, RoPE's
+relative-position property and GQA == MHA with duplicated KV heads; then
+the product code (torch_spyre.examples.decoder) checked against the oracle
+on the CPU, prefill and teacher-forced decode.
+"""
+
+import dataclasses
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import decoder as OD
+from torch_spyre.examples import decoder as D
+
+TINY = D.DecoderConfig(hidden=64, n_heads=4, n_kv_heads=2, head_dim=16, intermediate=96,
+                       vocab=50, n_layers=2)
+
+
+def _params(cfg, dtype=torch.float32, seed=3):
+    return D.init_params(cfg, "cpu", dtype=dtype, seed=seed, std=0.2)
+
+
+def _np(params):
+    return {"embed": params["embed"].float().numpy(),
+            "layers": [{k: v.float().numpy() for k, v in w.items()} for w in params["layers"]],
+            "final_norm": params["final_norm"].float().numpy(),
+            "lm_head": params["lm_head"].float().numpy()}
+
+
+def _tokens(B, S, vocab, seed=5):
+    return torch.randint(0, vocab, (B, S), generator=torch.Generator().manual_seed(seed))
+
+
+def _sdpa_block(tokens, p, cfg):
+    """Independent float32 decoder: SDPA with is_causal and enable_gqa."""
+    h = p["embed"][tokens]
+    B, S = tokens.shape
+    pos = torch.arange(S, dtype=torch.float32)
+    inv = 1.0 / cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2).float() / cfg.head_dim)
+    ang = pos[:, None] * inv[None]
+    cos, sin = ang.cos(), ang.sin()
+
+    def rope(x):  # [B, H, S, D], complex-free rotate-half
+        x1, x2 = x[..., : cfg.head_dim // 2], x[..., cfg.head_dim // 2:]
+        return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], -1)
+
+    for w in p["layers"]:
+        x = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + cfg.eps) * w["attn_norm"]
+        q = (x @ w["wq"].T).view(B, S, cfg.n_heads, -1).transpose(1, 2)
+        k = (x @ w["wk"].T).view(B, S, cfg.n_kv_heads, -1).transpose(1, 2)
+        v = (x @ w["wv"].T).view(B, S, cfg.n_kv_heads, -1).transpose(1, 2)
+        a = F.scaled_dot_product_attention(rope(q), rope(k), v, is_causal=True, enable_gqa=True)
+        h = h + a.transpose(1, 2).reshape(B, S, -1) @ w["wo"].T
+        x = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + cfg.eps) * w["mlp_norm"]
+        h = h + (F.silu(x @ w["wg"].T) * (x @ w["wu"].T)) @ w["wd"].T
+    return h
+
+
+def test_oracle_matches_independent_sdpa_decoder():
+    p = _params(TINY)
+    tok = _tokens(2, 12, TINY.vocab)
+    want = _sdpa_block(tok, p, TINY).numpy()
+    got = OD.block(tok.numpy(), _np(p), TINY, act=None)
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4)
+
+
+def test_oracle_is_causal():
+    p = _np(_params(TINY))
+    tok = _tokens(1, 10, TINY.vocab).numpy()
+    h = OD.block(tok, p, TINY, act=None)
+    tok2 = tok.copy()
+    tok2[0, 6:] = (tok2[0, 6:] + 7) % TINY.vocab
+    h2 = OD.block(tok2, p, TINY, act=None)
+    np.testing.assert_array_equal(h[:, :6], h2[:, :6])
+    assert np.abs(h[:, 6:] - h2[:, 6:]).max() > 1e-3
+
+
+def test_rope_relative_position():
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((1, 1, 1, 16)).astype(np.float32)
+    k = rng.standard_normal((1, 1, 1, 16)).astype(np.float32)
+
+    def dot(m, n):
+        cq, sq = OD.rope_tables(16, [m])
+        ck, sk = OD.rope_tables(16, [n])
+        return float(np.sum(OD._rope(q, cq, sq, None) * OD._rope(k, ck, sk, None)))
+
+    assert dot(5, 2) == pytest.approx(dot(13, 10), rel=1e-4, abs=1e-5)
+    assert dot(0, 0) == pytest.approx(float(np.sum(q * k)), rel=1e-5)
+    assert dot(5, 2) != pytest.approx(dot(5, 3), rel=1e-3)
+
+
+def test_gqa_equals_mha_with_duplicated_heads():
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal((2, 5, 4, 8)).astype(np.float32)
+    k = rng.standard_normal((2, 5, 2, 8)).astype(np.float32)
+    v = rng.standard_normal((2, 5, 2, 8)).astype(np.float32)
+    pos = np.arange(5)
+    a = OD.attention(q, k, v, pos, pos)
+    b = OD.attention(q, np.repeat(k, 2, axis=2), np.repeat(v, 2, axis=2), pos, pos)
+    np.testing.assert_allclose(a, b, rtol=1e-6, atol=1e-6)
+
+
+def test_product_block_matches_oracle_on_cpu():
+    p = _params(TINY)
+    tok = _tokens(2, 12, TINY.vocab)
+    cos, sin = D.rope_tables(TINY, 12, "cpu", torch.float32)
+    mask = D.causal_mask(TINY, 12, "cpu", torch.float32)
+    h = D.block_forward(tok, p, cos, sin, mask, TINY)
+    np.testing.assert_allclose(h.numpy(), OD.block(tok.numpy(), _np(p), TINY, act=None),
+                               rtol=1e-4, atol=1e-4)
+
+
+def test_product_generate_teacher_forced_matches_oracle_on_cpu():
+    p = _params(TINY)
+    prompt = _tokens(2, 9, TINY.vocab)
+    teacher = _tokens(2, 4, TINY.vocab, seed=7)
+    toks, logits = D.generate(prompt, p, TINY, 4, "cpu", teacher=teacher)
+    want = OD.generate_teacher_forced(prompt.numpy(), teacher.numpy(), _np(p), TINY, act=None)
+    np.testing.assert_allclose(logits.float().numpy(), want, rtol=1e-4, atol=1e-4)
+    assert torch.equal(toks, logits[:-1].argmax(-1).T)
+
+
+def test_fp16_rounding_model_tracks_fp32():
+    # the act=fp16 oracle (the device's rounding points) stays within the
+    # 1e-2 gate of the fp32 one at c4-like magnitudes
+    cfg = dataclasses.replace(TINY, hidden=128, head_dim=32, intermediate=256)
+    p = _np(D.init_params(cfg, "cpu", dtype=torch.float16, seed=4))
+    tok = _tokens(1, 16, cfg.vocab).numpy()
+    a = OD.block(tok, p, cfg, act=np.float16)
+    b = OD.block(tok, p, cfg, act=None)
+    np.testing.assert_allclose(a, b, rtol=1e-2, atol=1e-2)

@@ -29,6 +29,9 @@ struct SpyreGuardImpl final : public c10::impl::DeviceGuardImplInterface {
   }
 
   c10::Device getDevice() const override {
+    // With no device visible (e.g. fake-tensor tracing on a host without a
+    // GPU) the only meaningful index is 0; nothing is launched then.
+    if (device_count() == 0) return c10::Device(kDev, 0);
     return c10::Device(kDev, static_cast<c10::DeviceIndex>(current_device()));
   }
 

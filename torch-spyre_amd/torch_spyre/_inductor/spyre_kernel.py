@@ -202,7 +202,9 @@ class SpyreOverrides(OpOverrides):
         if isinstance(result, tuple):
             raise Unsupported("masked tuple")
         other_s = hip_value(other) if not isinstance(other, CSEVariable) else str(other)
-        return f"(({new_mask}) ? ({result}) : ({other_s}))"
+        return V.kernel.cse.generate(V.kernel.compute,
+                                     f"(({new_mask}) ? ({result}) : ({other_s}))",
+                                     dtype=getattr(result, "dtype", None))
 
     @staticmethod
     def where(a, b, c):

@@ -1,0 +1,222 @@
+"""A random-init decoder (the benchmark's c4 / c5 workload) written with
+plain torch ops, so the same code runs on the CPU and, eagerly or under
+torch.compile, on the spyre device.
+
+Shape: hidden 4096, 32 query heads / 8 KV heads of 128, RoPE (theta 1e4,
+rotate-half), causal attention as bmm -> masked softmax -> bmm, SwiGLU MLP
+of 12800, RMSNorm (eps 1e-5), vocab 49155, untied LM head.
+
+Grouped-query attention is computed without copying K/V per query head:
+the 4 query heads that share a KV head are stacked along the rows of one
+bmm operand ([B*8, 4*S, 128] x [B*8, 128, S]), so each attention bmm is
+4x taller and reads each K/V tile once; the causal mask repeats every S
+rows.  Decoding uses a contiguous KV cache [layers, 2, B, 8, max_len, 128].
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import math
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+
+@dataclasses.dataclass(frozen=True)
+class DecoderConfig:
+    hidden: int = 4096
+    n_heads: int = 32
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    intermediate: int = 12800
+    vocab: int = 49155
+    n_layers: int = 40
+    rope_theta: float = 1e4
+    eps: float = 1e-5
+
+    @property
+    def group(self) -> int:
+        return self.n_heads // self.n_kv_heads
+
+
+C4 = DecoderConfig(n_layers=1)
+C5 = DecoderConfig(n_layers=40)
+
+LAYER_WEIGHTS = ("attn_norm", "wq", "wk", "wv", "wo", "mlp_norm", "wg", "wu", "wd")
+
+
+def layer_shapes(cfg: DecoderConfig) -> dict:
+    h, kv = cfg.hidden, cfg.n_kv_heads * cfg.head_dim
+    return {"attn_norm": (h,), "wq": (cfg.n_heads * cfg.head_dim, h), "wk": (kv, h),
+            "wv": (kv, h), "wo": (h, cfg.n_heads * cfg.head_dim), "mlp_norm": (h,),
+            "wg": (cfg.intermediate, h), "wu": (cfg.intermediate, h),
+            "wd": (h, cfg.intermediate)}
+
+
+def init_params(cfg: DecoderConfig, device, dtype=torch.float16, seed: int = 0xAFFE,
+                std: float = 0.02, pool_elems: Optional[int] = None) -> dict:
+    """Random-init weights ~ N(0, std) (norm weights = ones), drawn on the
+    CPU from a seeded generator and copied to `device`.
+
+    With `pool_elems`, one pool of that many N(0, std) values is drawn once
+    and every weight is a window of it at a seeded offset -- the same
+    marginal distribution at a fraction of the host time, for throughput
+    runs of the 40-layer model (16.7 GB of weights)."""
+    g = torch.Generator().manual_seed(seed)
+    pool = None
+    if pool_elems:
+        pool = (torch.randn(pool_elems, generator=g) * std).to(dtype)
+
+    def draw(shape):
+        n = math.prod(shape)
+        if pool is None:
+            return (torch.randn(*shape, generator=g) * std).to(dtype)
+        reps = -(-n // pool.numel())
+        src = pool if reps == 1 else pool.repeat(reps)
+        off = int(torch.randint(0, src.numel() - n + 1, (1,), generator=g))
+        return src[off:off + n].view(shape)
+
+    params = {"embed": draw((cfg.vocab, cfg.hidden)).to(device), "layers": []}
+    for _ in range(cfg.n_layers):
+        lw = {}
+        for name, shape in layer_shapes(cfg).items():
+            lw[name] = (torch.ones(shape, dtype=dtype) if name.endswith("norm")
+                        else draw(shape)).to(device)
+        params["layers"].append(lw)
+    params["final_norm"] = torch.ones(cfg.hidden, dtype=dtype).to(device)
+    params["lm_head"] = draw((cfg.vocab, cfg.hidden)).to(device)
+    return params
+
+
+def rope_tables(cfg: DecoderConfig, max_pos: int, device, dtype=torch.float16):
+    """cos / sin [max_pos, head_dim] (both halves equal), angles in fp32."""
+    d = cfg.head_dim
+    inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    ang = torch.arange(max_pos, dtype=torch.float32)[:, None] * inv[None, :]
+    ang = torch.cat([ang, ang], dim=-1)
+    return ang.cos().to(dtype).to(device), ang.sin().to(dtype).to(device)
+
+
+def causal_mask(cfg: DecoderConfig, seq: int, device, dtype=torch.float16):
+    """Additive mask [group*seq, seq]: 0 where key <= query, -inf above the
+    diagonal, repeated for the query heads stacked along the rows."""
+    m = torch.full((seq, seq), float("-inf"), dtype=torch.float32).triu(1)
+    return m.repeat(cfg.group, 1).to(dtype).to(device)
+
+
+def _rotate_half(x):
+    half = x.shape[-1] // 2
+    return torch.cat([-x[..., half:], x[..., :half]], dim=-1)
+
+
+def apply_rope(x, cos, sin):
+    """x [B, S, H, D]; cos/sin [S, D] broadcast over batch and heads."""
+    return x * cos[:, None, :] + _rotate_half(x) * sin[:, None, :]
+
+
+def _attention(q, k, v, cfg: DecoderConfig, mask):
+    """q [B, Sq, 32, D], k / v [B, 8, Sk, D] -> [B, Sq, 32*D]."""
+    B, Sq = q.shape[0], q.shape[1]
+    kv, g, D = cfg.n_kv_heads, cfg.group, cfg.head_dim
+    qg = q.view(B, Sq, kv, g, D).permute(0, 2, 3, 1, 4).reshape(B * kv, g * Sq, D)
+    kk = k.reshape(B * kv, -1, D)
+    vv = v.reshape(B * kv, -1, D)
+    s = torch.bmm(qg, kk.transpose(1, 2)) * (1.0 / math.sqrt(D))
+    if mask is not None:
+        s = s + mask
+    p = torch.softmax(s, dim=-1)
+    o = torch.bmm(p, vv)  # [B*kv, g*Sq, D]
+    return o.view(B, kv, g, Sq, D).permute(0, 3, 1, 2, 4).reshape(B, Sq, kv * g * D)
+
+
+def layer_forward(h, w: dict, cos, sin, mask, cfg: DecoderConfig, cache_kv=None):
+    """One decoder layer on h [B, S, hidden] (prefill).  If `cache_kv` is
+    given (a [2, B, 8, max_len, D] view), K/V of positions [0, S) are
+    written into it."""
+    B, S, _ = h.shape
+    x = F.rms_norm(h, (cfg.hidden,), w["attn_norm"], cfg.eps)
+    q = F.linear(x, w["wq"]).view(B, S, cfg.n_heads, cfg.head_dim)
+    k = F.linear(x, w["wk"]).view(B, S, cfg.n_kv_heads, cfg.head_dim)
+    v = F.linear(x, w["wv"]).view(B, S, cfg.n_kv_heads, cfg.head_dim)
+    q = apply_rope(q, cos[:S], sin[:S])
+    k = apply_rope(k, cos[:S], sin[:S]).transpose(1, 2)
+    v = v.transpose(1, 2)
+    if cache_kv is not None:
+        cache_kv[0, :, :, :S].copy_(k)
+        cache_kv[1, :, :, :S].copy_(v)
+    h = h + F.linear(_attention(q, k, v, cfg, mask), w["wo"])
+    x = F.rms_norm(h, (cfg.hidden,), w["mlp_norm"], cfg.eps)
+    return h + F.linear(F.silu(F.linear(x, w["wg"])) * F.linear(x, w["wu"]), w["wd"])
+
+
+def block_forward(tokens, params: dict, cos, sin, mask, cfg: DecoderConfig):
+    """c4: embedding + the model's layers over tokens [B, S] -> hidden."""
+    h = F.embedding(tokens, params["embed"])
+    for w in params["layers"]:
+        h = layer_forward(h, w, cos, sin, mask, cfg)
+    return h
+
+
+def new_cache(cfg: DecoderConfig, batch: int, max_len: int, device, dtype=torch.float16):
+    return torch.zeros((cfg.n_layers, 2, batch, cfg.n_kv_heads, max_len, cfg.head_dim),
+                       dtype=dtype, device=device)
+
+
+def lm_logits(h_last, params: dict, cfg: DecoderConfig):
+    """Final RMSNorm + LM head on h_last [B, hidden] -> logits [B, vocab]."""
+    x = F.rms_norm(h_last, (cfg.hidden,), params["final_norm"], cfg.eps)
+    return F.linear(x, params["lm_head"])
+
+
+def prefill(tokens, params: dict, cos, sin, mask, cache, cfg: DecoderConfig, layer_fn=None):
+    """Runs the prompt tokens [B, S] through every layer, filling the KV
+    cache, and returns the logits of the last position [B, vocab]."""
+    layer_fn = layer_fn or layer_forward
+    h = F.embedding(tokens, params["embed"])
+    for i, w in enumerate(params["layers"]):
+        h = layer_fn(h, w, cos, sin, mask, cfg, cache[i])
+    return lm_logits(h[:, -1], params, cfg)
+
+
+def decode_step(tokens, pos: int, params: dict, cos, sin, cache, cfg: DecoderConfig):
+    """One token per sequence (tokens [B]) at position `pos`: appends its
+    K/V to the cache and returns the logits [B, vocab]."""
+    B = tokens.shape[0]
+    h = F.embedding(tokens, params["embed"]).view(B, 1, cfg.hidden)
+    c, s = cos[pos:pos + 1], sin[pos:pos + 1]
+    for i, w in enumerate(params["layers"]):
+        x = F.rms_norm(h, (cfg.hidden,), w["attn_norm"], cfg.eps)
+        q = apply_rope(F.linear(x, w["wq"]).view(B, 1, cfg.n_heads, cfg.head_dim), c, s)
+        k = apply_rope(F.linear(x, w["wk"]).view(B, 1, cfg.n_kv_heads, cfg.head_dim), c, s)
+        v = F.linear(x, w["wv"]).view(B, 1, cfg.n_kv_heads, cfg.head_dim)
+        cache[i, 0, :, :, pos:pos + 1].copy_(k.transpose(1, 2))
+        cache[i, 1, :, :, pos:pos + 1].copy_(v.transpose(1, 2))
+        kc = cache[i, 0, :, :, :pos + 1]
+        vc = cache[i, 1, :, :, :pos + 1]
+        h = h + F.linear(_attention(q, kc, vc, cfg, None), w["wo"])
+        x = F.rms_norm(h, (cfg.hidden,), w["mlp_norm"], cfg.eps)
+        h = h + F.linear(F.silu(F.linear(x, w["wg"])) * F.linear(x, w["wu"]), w["wd"])
+    return lm_logits(h[:, 0], params, cfg)
+
+
+def generate(prompt, params: dict, cfg: DecoderConfig, steps: int, device, layer_fn=None,
+             teacher=None):
+    """Greedy decoding: prefill `prompt` [B, S], then `steps` decode steps.
+    Returns (the argmax token of each step [B, steps], the logits that chose
+    them [steps+1, B, vocab]).  With `teacher` ([B, steps] tokens) those
+    tokens are fed back instead of the argmax (teacher forcing), so the
+    logits of a device run and a CPU run can be compared step by step."""
+    B, S = prompt.shape
+    dt = params["embed"].dtype
+    cos, sin = rope_tables(cfg, S + steps, device, dt)
+    cache = new_cache(cfg, B, S + steps, device, dt)
+    logits = [prefill(prompt, params, cos, sin, causal_mask(cfg, S, device, dt), cache, cfg,
+                      layer_fn)]
+    out = []
+    for t in range(steps):
+        nxt = logits[-1].argmax(-1)
+        out.append(nxt)
+        feed = nxt if teacher is None else teacher[:, t]
+        logits.append(decode_step(feed, S + t, params, cos, sin, cache, cfg))
+    return torch.stack(out, 1), torch.stack(logits, 0)
