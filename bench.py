@@ -243,6 +243,100 @@ def bench_spyre_paths(steps, warmup):
     return out
 
 
+def bench_decoder(steps, warmup, c5_layers=40, decode_steps=128):
+    """c4: one decoder layer (+ embedding) compiled, prefill of 2048 tokens;
+    c5: the 40-layer model, compiled prefill of 4 x 1024 tokens into the KV
+    cache, then greedy decode steps (eager), all on "spyre" tensors."""
+    import torch
+
+    import torch_spyre  # noqa: F401
+    from torch_spyre.examples import decoder as D
+
+    dev = "spyre"
+    timer = _spyre_timer()
+    out = {}
+    # --- c4 -----------------------------------------------------------------
+    cfg = D.C4
+    S = 2048
+    params = D.init_params(cfg, dev, seed=SEED)
+    tok = torch.randint(0, cfg.vocab, (1, S), generator=_gen(0)).to(dev)
+    cos, sin = D.rope_tables(cfg, S, dev)
+    mask = D.causal_mask(cfg, S, dev)
+    blk = torch.compile(D.block_forward)
+    blk(tok, params, cos, sin, mask, cfg)
+    torch.spyre.synchronize()
+    ms, wall = timer.run(lambda: blk(tok, params, cos, sin, mask, cfg), steps, warmup)
+    flop = 2 * S * (cfg.hidden * (cfg.n_heads + 2 * cfg.n_kv_heads) * cfg.head_dim
+                    + cfg.n_heads * cfg.head_dim * cfg.hidden + 3 * cfg.hidden * cfg.intermediate) \
+        + 4 * S * S * cfg.n_heads * cfg.head_dim
+    out["c4_layer_prefill_compiled"] = {
+        "ms_per_step": round(ms, 3), "wall_ms": round(wall, 3),
+        "tok/s": round(S / (ms * 1e-3), 1), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1),
+        "mfma_frac": round(flop / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+        "flop_per_step": flop, "note": "dense attention FLOPs (no causal halving)"}
+    del params, blk
+    torch._dynamo.reset()
+    # --- c5 -----------------------------------------------------------------
+    if c5_layers <= 0:
+        return out
+    cfg = D.DecoderConfig(n_layers=c5_layers)
+    B, S = 4, 1024
+    t0 = time.perf_counter()
+    params = D.init_params(cfg, dev, seed=SEED, pool_elems=1 << 26)
+    torch.spyre.synchronize()
+    init_s = time.perf_counter() - t0
+    prompt = torch.randint(0, cfg.vocab, (B, S), generator=_gen(1)).to(dev)
+    cos, sin = D.rope_tables(cfg, S + decode_steps, dev)
+    mask = D.causal_mask(cfg, S, dev)
+    cache = D.new_cache(cfg, B, S + decode_steps, dev)
+    layer = torch.compile(D.layer_forward)
+
+    def run_prefill():
+        return D.prefill(prompt, params, cos, sin, mask, cache, cfg, layer)
+
+    logits = run_prefill()
+    torch.spyre.synchronize()
+    reps = 3
+    ms, wall = timer.run(run_prefill, reps, 1)
+    flop = cfg.n_layers * (2 * B * S * (cfg.hidden * (cfg.n_heads + 2 * cfg.n_kv_heads)
+                                        * cfg.head_dim + cfg.n_heads * cfg.head_dim * cfg.hidden
+                                        + 3 * cfg.hidden * cfg.intermediate)
+                           + 4 * B * S * S * cfg.n_heads * cfg.head_dim) \
+        + 2 * B * cfg.hidden * cfg.vocab
+    entry = {"layers": cfg.n_layers, "batch": B, "prompt": S, "init_s": round(init_s, 1),
+             "prefill_ms": round(ms, 2), "prefill_wall_ms": round(wall, 2),
+             "prefill_tok/s": round(B * S / (ms * 1e-3), 1),
+             "prefill_TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1)}
+    # greedy decode: eager steps appending to the cache
+    nxt = logits.argmax(-1)
+    for t in range(2):  # warm the decode kernels
+        D.decode_step(nxt, S + t, params, cos, sin, cache, cfg)
+    torch.spyre.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(timer.stream)
+    for t in range(decode_steps):
+        logits = D.decode_step(nxt, S + t, params, cos, sin, cache, cfg)
+        nxt = logits.argmax(-1)
+    ev1.record(timer.stream)
+    torch.spyre.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / decode_steps
+    dms = ev0.elapsed_time(ev1) / decode_steps
+    wbytes = sum(t.numel() * t.element_size() for w in params["layers"] for t in w.values()) \
+        + params["lm_head"].numel() * 2
+    entry.update({"decode_steps": decode_steps, "decode_ms_per_step": round(dms, 3),
+                  "decode_wall_ms_per_step": round(wall, 3),
+                  "decode_tok/s": round(B / (wall * 1e-3), 1),
+                  "decode_weight_GB/s": round(wbytes / (wall * 1e-3) / 1e9, 1),
+                  "decode_hbm_frac": round(wbytes / (wall * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                  "decode_path": "eager ops per step"})
+    out["c5_model"] = entry
+    del params, cache
+    torch._dynamo.reset()
+    return out
+
+
 def bench_eager_mm(steps, warmup):
     """torch.mm on "spyre" tensors: the drop-in (PrivateUse1) path to the same
     kernel, timed on the spyre stream."""
@@ -301,6 +395,9 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decoder", action="store_true")
+    ap.add_argument("--c5-layers", type=int, default=40)
+    ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--kernel", choices=["all", "gemm", "copy"], default="all",
                     help="gemm / copy: run only that kernel (for rocprofv3 counter passes)")
     args = ap.parse_args(argv)
@@ -332,6 +429,9 @@ def main(argv=None):
         extra["c2_mm_4096_spyre_device_eager"] = bench_eager_mm(max(10, args.steps), args.warmup)
         _log("spyre device paths (eager + torch.compile)")
         extra["spyre_device"] = bench_spyre_paths(max(10, args.steps), args.warmup)
+        if not args.no_decoder:
+            _log("decoder workloads (c4 layer, c5 model)")
+            extra["decoder"] = bench_decoder(5, 2, args.c5_layers, args.decode_steps)
     cpu = None
     if not args.no_cpu:
         _log("cpu baseline")
