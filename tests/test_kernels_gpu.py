@@ -281,6 +281,43 @@ def test_gemm_bf16_and_unaligned_ld():
     assert_close_fp(dd, O.gemm(big[:, 3:48].numpy(), Bd.cpu().numpy()))
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (4, 1024, 4096), (4, 12800, 4096),
+                                   (4, 4096, 12800), (3, 49155, 64), (8, 777, 2056),
+                                   (13, 33, 8), (16, 520, 136)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_gemm_small_m_weight_layout(m, n, k, dtype):
+    # decode-step shapes: x[M,K] @ W[N,K]^T, both K-contiguous (streaming
+    # small-M kernel), including K tails (k % 2048 != 0) and odd N
+    _log(f"gemm small-M {m}x{n}x{k} {dtype}")
+    X = uniform((m, k), k=11, dtype=dtype)
+    W = (uniform((n, k), k=12) * 0.05).to(dtype)
+    d = _gemm(X.to(DEV), W.to(DEV), trans_b=True, dtype=dtype)
+    tol = dict(rtol=1e-2, atol=1e-2) if dtype == torch.float16 else dict(rtol=2e-2, atol=2e-2)
+    assert_close_fp(d, O.gemm(X.float().numpy(), W.float().numpy().T), out_dtype=dtype,
+                    what=f"small-M {dtype}", **tol)
+
+
+def test_gemm_small_m_epilogue_and_batch():
+    _log("gemm small-M epilogue / batched")
+    m, n, k = 4, 200, 264
+    X, W = uniform((m, k), k=13), uniform((n, k), k=14) * 0.1
+    bias = uniform((n,), k=15)
+    d = _gemm(X.to(DEV), W.to(DEV), trans_b=True, alpha=0.5, beta=1.5, c=bias.to(DEV), crow=0,
+              ccol=1, epi=3)
+    want = O.gemm(X.numpy(), W.numpy().T, alpha=0.5, beta=1.5, c=bias.numpy()[None, :],
+                  epilogue="silu")
+    assert_close_fp(d, want, what="small-M silu epilogue")
+    # batched decode attention scores: q [b, 4, 128] x K[b, L, 128]^T
+    b, L = 32, 1030
+    Q, K = uniform((b, 4, 128), k=16), uniform((b, L, 128), k=17)
+    qd, kd = Q.to(DEV), K.to(DEV)
+    out = torch.empty(b, 4, L, dtype=torch.float16, device=DEV)
+    _capi.call("sph_gemm_strided_batched", _capi.F16, 0, 1, b, 4, L, 128, 1.0, _p(qd), 128,
+               4 * 128, _p(kd), 128, L * 128, 0.0, None, 0, 0, 0, _p(out), L, 4 * L, 0, _stream())
+    _sync()
+    assert_close_fp(out, O.gemm(Q.numpy(), K.numpy().transpose(0, 2, 1)), what="small-M batched")
+
+
 @pytest.mark.parametrize("batch,m,n,k,tb", [(32, 2048, 2048, 128, False), (32, 2048, 128, 2048, False),
                                             (4, 100, 36, 72, True), (3, 5, 7, 9, False)])
 def test_bmm(batch, m, n, k, tb):

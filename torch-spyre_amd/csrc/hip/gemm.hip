@@ -26,6 +26,11 @@
 //   * Workgroup ids are remapped so that the 8 XCDs (round-robin dispatch)
 //     each get a compact group of C tiles, sharing A rows and B columns in
 //     their own L2.
+//   * Products with at most 16 rows of A whose operands are both
+//     K-contiguous (decode steps and LM heads: x[M,K] times an nn.Linear
+//     weight W[N,K]) are HBM-bound on reading W once; they run a separate
+//     streaming kernel (gemm_skinny_kernel) with packed fp16 dot products
+//     instead of MFMA tiles, which would leave most CUs idle at M <= 16.
 #include "sph_common.h"
 
 namespace sph {
@@ -260,8 +265,8 @@ __device__ inline void store_slab_impl(const GemmArgs& p, const float* slab, T* 
     float v[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      v[e] = __builtin_bit_cast(float, sw ? h1[e] : h0[e]);
-      v[e + 4] = __builtin_bit_cast(float, sw ? h0[e] : h1[e]);
+      v[e] = __uint_as_float(sw ? h1[e] : h0[e]);
+      v[e + 4] = __uint_as_float(sw ? h0[e] : h1[e]);
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -495,6 +500,132 @@ gemm_kernel(const GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Small-M products: D[m, n] = epi(alpha * sum_k A[m, k] * B[n, k] + beta*C)
+// for M <= MT rows, A and B K-contiguous and 16-byte aligned, K % 8 == 0.
+// One workgroup (256 threads) computes R = 4 outputs columns n for all M
+// rows: thread t reads 16 bytes of each of the 4 weight rows at
+// k = 8t + 2048 j (whole 4 KiB row segments per wave group, coalesced), and
+// the 4 x 16-byte loads per step are independent, so each thread keeps 4..28
+// loads in flight.  A (at most 16 x K, shared by every workgroup) is read
+// through the caches.  fp16 uses v_dot2_f32_f16 (two products summed into
+// an fp32 accumulator), bf16 widens with shifts and uses fp32 FMAs.  The
+// M x R partial sums are reduced across the wave with butterflies and across
+// the 4 waves through LDS.
+// ---------------------------------------------------------------------------
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+template <typename T>
+__device__ inline float dot8_acc(u32x4 a, u32x4 b, float acc) {
+  if constexpr (__is_same(T, half_t)) {
+    // (vector elements are copied to scalars first: this compiler lowers
+    // __builtin_bit_cast of an indexed vector element to element 0)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t ai = a[i], bi = b[i];
+      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, ai), __builtin_bit_cast(f16x2, bi),
+                                   acc, false);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc = fmaf(__uint_as_float(a[i] << 16), __uint_as_float(b[i] << 16), acc);
+      acc = fmaf(__uint_as_float(a[i] & 0xffff0000u), __uint_as_float(b[i] & 0xffff0000u), acc);
+    }
+  }
+  return acc;
+}
+
+constexpr int kSkinnyR = 4;        // output columns per workgroup
+constexpr int kSkinnyThreads = 256;
+
+template <typename T, int MT>
+__global__ void __launch_bounds__(kSkinnyThreads) gemm_skinny_kernel(const GemmArgs p) {
+  constexpr int R = kSkinnyR;
+  const int64_t bz = blockIdx.y;
+  const uint16_t* A = static_cast<const uint16_t*>(p.a) + bz * p.stride_a;
+  const uint16_t* B = static_cast<const uint16_t*>(p.b) + bz * p.stride_b;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * R;
+  const int tid = threadIdx.x;
+  const int mrows = static_cast<int>(p.m);
+  const uint16_t* bp[R];
+  bool bv[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    bv[r] = n0 + r < p.n;
+    bp[r] = B + (bv[r] ? n0 + r : n0) * p.ldb;
+  }
+  float acc[MT][R];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
+  for (int64_t k = static_cast<int64_t>(tid) * 8; k < p.k; k += kSkinnyThreads * 8) {
+    u32x4 w[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      w[r] = bv[r] ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bp[r] + k))
+                   : zero4();
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m < mrows) {
+        const u32x4 x = *reinterpret_cast<const u32x4*>(A + m * p.lda + k);
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[m][r] = dot8_acc<T>(x, w[r], acc[m][r]);
+      }
+    }
+  }
+  // Reduce the MT x R partial sums over the workgroup.
+  __shared__ float red[kSkinnyThreads / 64][MT * R];
+  const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float v = acc[m][r];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+      if (lane == 0) red[wave][m * R + r] = v;
+    }
+  __syncthreads();
+  if (tid < MT * R) {
+    const int m = tid / R, r = tid % R;
+    const int64_t n = n0 + r;
+    if (m < mrows && n < p.n) {
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < kSkinnyThreads / 64; ++w) v += red[w][tid];
+      v *= p.alpha;
+      if (p.c != nullptr && p.beta != 0.f) {
+        const T* C = static_cast<const T*>(p.c) + bz * p.stride_c;
+        v += p.beta * Num<T>::to_f(C[m * p.ldc_row + n * p.ldc_col]);
+      }
+      if (p.epilogue == SPH_EPI_RELU) v = fmaxf(v, 0.f);
+      else if (p.epilogue == SPH_EPI_GELU) v = gelu_erf(v);
+      else if (p.epilogue == SPH_EPI_SILU) v = silu(v);
+      T* D = static_cast<T*>(p.d) + bz * p.stride_d;
+      D[m * p.ldd + n] = Num<T>::from_f(v);
+    }
+  }
+}
+
+template <typename T>
+int launch_skinny(const GemmArgs& p, int64_t batch, hipStream_t st) {
+  dim3 grid(static_cast<unsigned>(ceil_div(p.n, kSkinnyR)), static_cast<unsigned>(batch));
+  dim3 block(kSkinnyThreads);
+  if (p.m <= 1)
+    gemm_skinny_kernel<T, 1><<<grid, block, 0, st>>>(p);
+  else if (p.m <= 2)
+    gemm_skinny_kernel<T, 2><<<grid, block, 0, st>>>(p);
+  else if (p.m <= 4)
+    gemm_skinny_kernel<T, 4><<<grid, block, 0, st>>>(p);
+  else if (p.m <= 8)
+    gemm_skinny_kernel<T, 8><<<grid, block, 0, st>>>(p);
+  else
+    gemm_skinny_kernel<T, 16><<<grid, block, 0, st>>>(p);
+  return check_launch("sph_gemm (small M)");
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 template <typename T, int BM, int BN, int WM, int WN, bool FULL>
@@ -537,6 +668,9 @@ inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) 
 template <typename T>
 int gemm_dispatch(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
                   hipStream_t st) {
+  if (p.m <= 16 && a_kcont && b_kcont && p.vec_a && p.vec_b && p.k > 0 && p.k % 8 == 0 &&
+      ceil_div(p.n, kSkinnyR) < (1LL << 31))
+    return launch_skinny<T>(p, batch, st);
   const int64_t t256 = ceil_div(p.m, 256) * ceil_div(p.n, 256) * batch;
   const int64_t t128 = ceil_div(p.m, 128) * ceil_div(p.n, 128) * batch;
   // 256x256 whole tiles run 8 waves (128x64 each, two per SIMD, so one
