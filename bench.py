@@ -307,30 +307,46 @@ def bench_decoder(steps, warmup, c5_layers=40, decode_steps=128):
              "prefill_ms": round(ms, 2), "prefill_wall_ms": round(wall, 2),
              "prefill_tok/s": round(B * S / (ms * 1e-3), 1),
              "prefill_TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1)}
-    # greedy decode: eager steps appending to the cache
+    # greedy decode: the static decode step compiled (one graph for all 40
+    # layers; position tensor advanced on the device), 128 steps timed
+    dec = torch.compile(D.decode_step_static)
+    pos = torch.full((1,), S, dtype=torch.int64).to(dev)
     nxt = logits.argmax(-1)
-    for t in range(2):  # warm the decode kernels
-        D.decode_step(nxt, S + t, params, cos, sin, cache, cfg)
+    t0 = time.perf_counter()
+    for _ in range(2):  # compile + warm
+        dec(nxt, pos, params, cos, sin, cache, cfg)
     torch.spyre.synchronize()
+    entry["decode_compile_s"] = round(time.perf_counter() - t0, 1)
+    pos.fill_(S)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     ev0.record(timer.stream)
     for t in range(decode_steps):
-        logits = D.decode_step(nxt, S + t, params, cos, sin, cache, cfg)
+        logits = dec(nxt, pos, params, cos, sin, cache, cfg)
         nxt = logits.argmax(-1)
+        pos.add_(1)
     ev1.record(timer.stream)
     torch.spyre.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / decode_steps
     dms = ev0.elapsed_time(ev1) / decode_steps
     wbytes = sum(t.numel() * t.element_size() for w in params["layers"] for t in w.values()) \
         + params["lm_head"].numel() * 2
+    kvbytes = sum(k.numel() * k.element_size() * 2 for k, _ in cache)
     entry.update({"decode_steps": decode_steps, "decode_ms_per_step": round(dms, 3),
                   "decode_wall_ms_per_step": round(wall, 3),
                   "decode_tok/s": round(B / (wall * 1e-3), 1),
                   "decode_weight_GB/s": round(wbytes / (wall * 1e-3) / 1e9, 1),
-                  "decode_hbm_frac": round(wbytes / (wall * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                  "decode_path": "eager ops per step"})
+                  "decode_hbm_frac": round((wbytes + kvbytes) / (wall * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                                           4),
+                  "decode_path": "torch.compile(decode_step_static), KV over the full cache"})
+    # the eager decode step, for comparison (a few steps)
+    torch.spyre.synchronize()
+    t0 = time.perf_counter()
+    for t in range(8):
+        D.decode_step(nxt, S + t, params, cos, sin, cache, cfg)
+    torch.spyre.synchronize()
+    entry["decode_eager_wall_ms_per_step"] = round((time.perf_counter() - t0) * 1e3 / 8, 3)
     out["c5_model"] = entry
     del params, cache
     torch._dynamo.reset()

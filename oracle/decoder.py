@@ -144,6 +144,7 @@ def generate_teacher_forced(prompt, teacher, params, cfg, act=np.float16, fused=
     for t in range(np.asarray(teacher).shape[1]):
         h = embed(np.asarray(teacher)[:, t:t + 1], params["embed"], act)
         for i, w in enumerate(params["layers"]):
-            h, caches[i] = layer(h, w, cfg, np.array([S + t]), act, kv_prefix=caches[i])
+            h, caches[i] = layer(h, w, cfg, np.array([S + t]), act, kv_prefix=caches[i],
+                                 fused=fused)
         out.append(logits(h[:, -1], params, cfg, act))
     return np.stack(out, 0)

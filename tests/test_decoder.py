@@ -125,6 +125,15 @@ def test_product_generate_teacher_forced_matches_oracle_on_cpu():
     assert torch.equal(toks, logits[:-1].argmax(-1).T)
 
 
+def test_static_decode_step_matches_eager_decode_on_cpu():
+    p = _params(TINY)
+    prompt = _tokens(2, 9, TINY.vocab)
+    teacher = _tokens(2, 4, TINY.vocab, seed=7)
+    _, a = D.generate(prompt, p, TINY, 4, "cpu", teacher=teacher)
+    _, b = D.generate(prompt, p, TINY, 4, "cpu", teacher=teacher, decode_fn=D.decode_step_static)
+    torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
+
+
 def test_fp16_rounding_model_tracks_fp32():
     # the act=fp16 oracle (the device's rounding points) stays within the
     # 1e-2 gate of the fp32 one at c4-like magnitudes

@@ -103,18 +103,21 @@ def test_c4_block_compiled_vs_oracle():
 
 @pytest.mark.parametrize("compiled", [False, True])
 def test_c5_flow_teacher_forced_vs_oracle(compiled):
+    """compiled = prefill layers and the static decode step under
+    torch.compile (the decode step's fused kernels round like the eager
+    ops except RoPE and SiLU*up, which the fused oracle models)."""
     _log(f"c5 flow (2 layers of the c4 shape) compiled={compiled}")
     cfg = dataclasses.replace(D.C5, n_layers=2)
     params = D.init_params(cfg, "cpu", seed=0xAFFE + 1)
     prompt = _tokens(4, 64, cfg.vocab, seed=1)
     teacher = _tokens(4, 6, cfg.vocab, seed=2)
-    layer_fn = None
+    layer_fn = decode_fn = None
     if compiled:
         torch._dynamo.reset()
         layer_fn = torch.compile(D.layer_forward)
+        decode_fn = torch.compile(D.decode_step_static)
     toks, logits = D.generate(prompt.to(DEV), _to(params, DEV), cfg, 6, DEV, layer_fn=layer_fn,
-                              teacher=teacher.to(DEV))
-    # prefill layers are compiled, decode steps run eagerly
+                              teacher=teacher.to(DEV), decode_fn=decode_fn)
     want = OD.generate_teacher_forced(prompt.numpy(), teacher.numpy(), _np(params), cfg,
                                       fused=compiled)
     got = logits.cpu().float().numpy()

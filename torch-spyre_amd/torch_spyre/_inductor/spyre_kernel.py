@@ -385,7 +385,7 @@ class SpyreKernel(SIMDKernel):
         self._acc_ids = itertools.count()
         self._rloop_open = False
         self._pending_accum = False
-        # outer buffer name -> max element extent (None = not checkable)
+        # kernel argument name -> max element extent (None = not checkable)
         self._extents: dict[str, Optional[int]] = {}
 
     # -- sizes ----------------------------------------------------------------
@@ -477,7 +477,7 @@ class SpyreKernel(SIMDKernel):
         dtype = V.graph.get_dtype(name)
         self.dtype_to_str(dtype)
         masked = bool(self._load_mask)
-        self._record_extent(name, index, masked)
+        self._record_extent(str(var), index, masked)
         line = f"{var}[{self.index_to_str(index)}]"
         if dtype in _FLOAT_LOAD:
             line = f"spy::to_f({line})"
@@ -501,7 +501,7 @@ class SpyreKernel(SIMDKernel):
         var = self.args.output(name)
         index = self.prepare_indexing(index)
         dtype = V.graph.get_dtype(name)
-        self._record_extent(name, index, False)
+        self._record_extent(str(var), index, False)
         line = f"{var}[{self.index_to_str(index)}] = spy::cvt<{self.dtype_to_str(dtype)}>({value});"
         if self.inside_reduction:
             self.compute.writeline(DeferredLine(name, line))
@@ -512,7 +512,7 @@ class SpyreKernel(SIMDKernel):
         var = self.args.output(name)
         index = self.prepare_indexing(index)
         dtype = V.graph.get_dtype(name)
-        self._record_extent(name, index, False)
+        self._record_extent(str(var), index, False)
         line = (f"if (threadIdx.x == 0) {var}[{self.index_to_str(index)}] = "
                 f"spy::cvt<{self.dtype_to_str(dtype)}>({value});")
         self.stores.writeline(DeferredLine(name, line))
@@ -646,7 +646,10 @@ class SpyreKernel(SIMDKernel):
             else:
                 params.append(f"const {ctype}* __restrict__ {inner}")
                 is_input = True
-            ext = self._extents.get(outer, 0)
+            # keyed by the kernel-side argument name, so buffers that are
+            # mutated in place (passed under their graph-input name) keep
+            # their bound; an argument the body never touched is unbounded
+            ext = self._extents.get(inner)
             spec_args.append(f"TensorArg(is_input={is_input}, arg_index={i}, "
                              f"dtype={dt!r}, extent={ext!r})")
         code = IndentedBuffer()

@@ -10,7 +10,10 @@ Grouped-query attention is computed without copying K/V per query head:
 the 4 query heads that share a KV head are stacked along the rows of one
 bmm operand ([B*8, 4*S, 128] x [B*8, 128, S]), so each attention bmm is
 4x taller and reads each K/V tile once; the causal mask repeats every S
-rows.  Decoding uses a contiguous KV cache [layers, 2, B, 8, max_len, 128].
+rows.  Decoding uses a KV cache of one contiguous K and one contiguous V
+buffer [B, 8, max_len, 128] per layer (separate tensors, so a compiled
+decode step scatters the new token's K/V into them in place instead of
+copying an aliased cache).
 """
 
 from __future__ import annotations
@@ -116,7 +119,8 @@ def apply_rope(x, cos, sin):
 
 
 def _attention(q, k, v, cfg: DecoderConfig, mask):
-    """q [B, Sq, 32, D], k / v [B, 8, Sk, D] -> [B, Sq, 32*D]."""
+    """q [B, Sq, 32, D], k / v [B, 8, Sk, D] -> [B*Sq, 32*D] (2-D, so the
+    output projection is one GEMM with the weight read once)."""
     B, Sq = q.shape[0], q.shape[1]
     kv, g, D = cfg.n_kv_heads, cfg.group, cfg.head_dim
     qg = q.view(B, Sq, kv, g, D).permute(0, 2, 3, 1, 4).reshape(B * kv, g * Sq, D)
@@ -127,13 +131,13 @@ def _attention(q, k, v, cfg: DecoderConfig, mask):
         s = s + mask
     p = torch.softmax(s, dim=-1)
     o = torch.bmm(p, vv)  # [B*kv, g*Sq, D]
-    return o.view(B, kv, g, Sq, D).permute(0, 3, 1, 2, 4).reshape(B, Sq, kv * g * D)
+    return o.view(B, kv, g, Sq, D).permute(0, 3, 1, 2, 4).reshape(B * Sq, kv * g * D)
 
 
 def layer_forward(h, w: dict, cos, sin, mask, cfg: DecoderConfig, cache_kv=None):
     """One decoder layer on h [B, S, hidden] (prefill).  If `cache_kv` is
-    given (a [2, B, 8, max_len, D] view), K/V of positions [0, S) are
-    written into it."""
+    given (the layer's (K, V) cache buffers [B, 8, max_len, D]), K/V of
+    positions [0, S) are written into it."""
     B, S, _ = h.shape
     x = F.rms_norm(h, (cfg.hidden,), w["attn_norm"], cfg.eps)
     q = F.linear(x, w["wq"]).view(B, S, cfg.n_heads, cfg.head_dim)
@@ -143,9 +147,9 @@ def layer_forward(h, w: dict, cos, sin, mask, cfg: DecoderConfig, cache_kv=None)
     k = apply_rope(k, cos[:S], sin[:S]).transpose(1, 2)
     v = v.transpose(1, 2)
     if cache_kv is not None:
-        cache_kv[0, :, :, :S].copy_(k)
-        cache_kv[1, :, :, :S].copy_(v)
-    h = h + F.linear(_attention(q, k, v, cfg, mask), w["wo"])
+        cache_kv[0][:, :, :S].copy_(k)
+        cache_kv[1][:, :, :S].copy_(v)
+    h = h + F.linear(_attention(q, k, v, cfg, mask), w["wo"]).view(B, S, cfg.hidden)
     x = F.rms_norm(h, (cfg.hidden,), w["mlp_norm"], cfg.eps)
     return h + F.linear(F.silu(F.linear(x, w["wg"])) * F.linear(x, w["wu"]), w["wd"])
 
@@ -159,8 +163,11 @@ def block_forward(tokens, params: dict, cos, sin, mask, cfg: DecoderConfig):
 
 
 def new_cache(cfg: DecoderConfig, batch: int, max_len: int, device, dtype=torch.float16):
-    return torch.zeros((cfg.n_layers, 2, batch, cfg.n_kv_heads, max_len, cfg.head_dim),
-                       dtype=dtype, device=device)
+    """Per layer, a (K, V) pair of zeroed [batch, 8, max_len, head_dim]
+    buffers."""
+    shape = (batch, cfg.n_kv_heads, max_len, cfg.head_dim)
+    return [(torch.zeros(shape, dtype=dtype, device=device),
+             torch.zeros(shape, dtype=dtype, device=device)) for _ in range(cfg.n_layers)]
 
 
 def lm_logits(h_last, params: dict, cfg: DecoderConfig):
@@ -190,23 +197,51 @@ def decode_step(tokens, pos: int, params: dict, cos, sin, cache, cfg: DecoderCon
         q = apply_rope(F.linear(x, w["wq"]).view(B, 1, cfg.n_heads, cfg.head_dim), c, s)
         k = apply_rope(F.linear(x, w["wk"]).view(B, 1, cfg.n_kv_heads, cfg.head_dim), c, s)
         v = F.linear(x, w["wv"]).view(B, 1, cfg.n_kv_heads, cfg.head_dim)
-        cache[i, 0, :, :, pos:pos + 1].copy_(k.transpose(1, 2))
-        cache[i, 1, :, :, pos:pos + 1].copy_(v.transpose(1, 2))
-        kc = cache[i, 0, :, :, :pos + 1]
-        vc = cache[i, 1, :, :, :pos + 1]
-        h = h + F.linear(_attention(q, kc, vc, cfg, None), w["wo"])
+        kc, vc = cache[i]
+        kc[:, :, pos:pos + 1].copy_(k.transpose(1, 2))
+        vc[:, :, pos:pos + 1].copy_(v.transpose(1, 2))
+        kc, vc = kc[:, :, :pos + 1], vc[:, :, :pos + 1]
+        h = h + F.linear(_attention(q, kc, vc, cfg, None), w["wo"]).view(B, 1, cfg.hidden)
+        x = F.rms_norm(h, (cfg.hidden,), w["mlp_norm"], cfg.eps)
+        h = h + F.linear(F.silu(F.linear(x, w["wg"])) * F.linear(x, w["wu"]), w["wd"])
+    return lm_logits(h[:, 0], params, cfg)
+
+
+def decode_step_static(tokens, pos, params: dict, cos, sin, cache, cfg: DecoderConfig):
+    """decode_step with every shape fixed, for torch.compile: `pos` is a
+    one-element int64 tensor on the device, the new K/V are scattered into
+    the cache at `pos` and attention runs over the whole cache length with
+    keys after `pos` masked out, so one compiled graph serves every step."""
+    B = tokens.shape[0]
+    L = cache[0][0].shape[2]
+    h = F.embedding(tokens, params["embed"]).view(B, 1, cfg.hidden)
+    c, s = cos.index_select(0, pos), sin.index_select(0, pos)
+    keys = torch.arange(L, device=tokens.device)
+    mask = torch.where(keys <= pos, 0.0, float("-inf")).to(h.dtype)
+    for i, w in enumerate(params["layers"]):
+        x = F.rms_norm(h, (cfg.hidden,), w["attn_norm"], cfg.eps)
+        q = apply_rope(F.linear(x, w["wq"]).view(B, 1, cfg.n_heads, cfg.head_dim), c, s)
+        k = apply_rope(F.linear(x, w["wk"]).view(B, 1, cfg.n_kv_heads, cfg.head_dim), c, s)
+        v = F.linear(x, w["wv"]).view(B, 1, cfg.n_kv_heads, cfg.head_dim)
+        kc, vc = cache[i]
+        kc.index_copy_(2, pos, k.transpose(1, 2))
+        vc.index_copy_(2, pos, v.transpose(1, 2))
+        h = h + F.linear(_attention(q, kc, vc, cfg, mask), w["wo"]).view(B, 1, cfg.hidden)
         x = F.rms_norm(h, (cfg.hidden,), w["mlp_norm"], cfg.eps)
         h = h + F.linear(F.silu(F.linear(x, w["wg"])) * F.linear(x, w["wu"]), w["wd"])
     return lm_logits(h[:, 0], params, cfg)
 
 
 def generate(prompt, params: dict, cfg: DecoderConfig, steps: int, device, layer_fn=None,
-             teacher=None):
+             teacher=None, decode_fn=None):
     """Greedy decoding: prefill `prompt` [B, S], then `steps` decode steps.
     Returns (the argmax token of each step [B, steps], the logits that chose
     them [steps+1, B, vocab]).  With `teacher` ([B, steps] tokens) those
     tokens are fed back instead of the argmax (teacher forcing), so the
-    logits of a device run and a CPU run can be compared step by step."""
+    logits of a device run and a CPU run can be compared step by step.
+    `decode_fn` (e.g. torch.compile(decode_step_static)) replaces the
+    eager decode step; its position tensor lives on the device and is
+    advanced there, so no step waits on the host."""
     B, S = prompt.shape
     dt = params["embed"].dtype
     cos, sin = rope_tables(cfg, S + steps, device, dt)
@@ -214,9 +249,14 @@ def generate(prompt, params: dict, cfg: DecoderConfig, steps: int, device, layer
     logits = [prefill(prompt, params, cos, sin, causal_mask(cfg, S, device, dt), cache, cfg,
                       layer_fn)]
     out = []
+    pos = torch.full((1,), S, dtype=torch.int64).to(device) if decode_fn is not None else None
     for t in range(steps):
         nxt = logits[-1].argmax(-1)
         out.append(nxt)
         feed = nxt if teacher is None else teacher[:, t]
-        logits.append(decode_step(feed, S + t, params, cos, sin, cache, cfg))
+        if decode_fn is None:
+            logits.append(decode_step(feed, S + t, params, cos, sin, cache, cfg))
+        else:
+            logits.append(decode_fn(feed, pos, params, cos, sin, cache, cfg))
+            pos.add_(1)
     return torch.stack(out, 1), torch.stack(logits, 0)
