@@ -308,29 +308,40 @@ def bench_decoder(steps, warmup, c5_layers=40, decode_steps=128):
              "prefill_tok/s": round(B * S / (ms * 1e-3), 1),
              "prefill_TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1)}
     # greedy decode: the static decode step compiled (one graph for all 40
-    # layers; position tensor advanced on the device), 128 steps timed
+    # layers; position tensor advanced on the device) and captured with the
+    # argmax and the position update into one HIP graph; a step is one
+    # replay plus the copy of the chosen tokens into the next step's input
+    import torch_spyre.graphs as graphs
+
     dec = torch.compile(D.decode_step_static)
     pos = torch.full((1,), S, dtype=torch.int64).to(dev)
-    nxt = logits.argmax(-1)
+    feed = logits.argmax(-1)
     t0 = time.perf_counter()
-    for _ in range(2):  # compile + warm
-        dec(nxt, pos, params, cos, sin, cache, cfg)
+    for _ in range(2):  # compile + warm (rewrites cache position S each time)
+        dec(feed, pos, params, cos, sin, cache, cfg)
     torch.spyre.synchronize()
     entry["decode_compile_s"] = round(time.perf_counter() - t0, 1)
-    pos.fill_(S)
+    g = graphs.SpyreGraph()
+    with graphs.graph(g):
+        step_logits = dec(feed, pos, params, cos, sin, cache, cfg)
+        step_arg = step_logits.argmax(-1)
+        pos.add_(1)
+    tokens = torch.empty((B, decode_steps), dtype=torch.int64, device=dev)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     ev0.record(timer.stream)
     for t in range(decode_steps):
-        logits = dec(nxt, pos, params, cos, sin, cache, cfg)
-        nxt = logits.argmax(-1)
-        pos.add_(1)
+        g.replay()
+        tokens[:, t].copy_(step_arg)
+        feed.copy_(step_arg)
     ev1.record(timer.stream)
     torch.spyre.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / decode_steps
     dms = ev0.elapsed_time(ev1) / decode_steps
-    wbytes = sum(t.numel() * t.element_size() for w in params["layers"] for t in w.values()) \
+    g.reset()
+    wbytes = sum(t.numel() * t.element_size() for w in params["layers"]
+                 for k, t in w.items() if k in ("attn_norm", "wqkv", "wo", "mlp_norm", "wgu", "wd")) \
         + params["lm_head"].numel() * 2
     kvbytes = sum(k.numel() * k.element_size() * 2 for k, _ in cache)
     entry.update({"decode_steps": decode_steps, "decode_ms_per_step": round(dms, 3),
@@ -339,12 +350,21 @@ def bench_decoder(steps, warmup, c5_layers=40, decode_steps=128):
                   "decode_weight_GB/s": round(wbytes / (wall * 1e-3) / 1e9, 1),
                   "decode_hbm_frac": round((wbytes + kvbytes) / (wall * 1e-3) / 1e9 / PEAK_HBM_GBS,
                                            4),
-                  "decode_path": "torch.compile(decode_step_static), KV over the full cache"})
+                  "decode_path": "torch.compile(decode_step_static) + argmax captured in one "
+                                 "HIP graph per step; KV over the full cache"})
+    # without the graph (the compiled step called from Python)
+    torch.spyre.synchronize()
+    t0 = time.perf_counter()
+    for t in range(8):
+        lg = dec(feed, pos, params, cos, sin, cache, cfg)
+        feed = lg.argmax(-1)
+    torch.spyre.synchronize()
+    entry["decode_nograph_wall_ms_per_step"] = round((time.perf_counter() - t0) * 1e3 / 8, 3)
     # the eager decode step, for comparison (a few steps)
     torch.spyre.synchronize()
     t0 = time.perf_counter()
     for t in range(8):
-        D.decode_step(nxt, S + t, params, cos, sin, cache, cfg)
+        D.decode_step(feed, S + t, params, cos, sin, cache, cfg)
     torch.spyre.synchronize()
     entry["decode_eager_wall_ms_per_step"] = round((time.perf_counter() - t0) * 1e3 / 8, 3)
     out["c5_model"] = entry

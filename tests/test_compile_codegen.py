@@ -106,6 +106,12 @@ def test_pointwise_chain_fuses_into_one_kernel(fake_device):
     assert "if (xindex >= 3000LL) return;" in code
 
 
+def test_transposing_copy_uses_flat_index(fake_device):
+    code = _compile(lambda x: x.transpose(1, 2).contiguous() * 2,
+                    [((4, 96, 64), torch.float16)])
+    assert len(_kernels(code)) == 1 and "yindex" not in code
+
+
 def test_unsupported_dynamic_shapes_raise(fake_device):
     from torch_spyre._inductor import Unsupported
 

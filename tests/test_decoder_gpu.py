@@ -121,7 +121,19 @@ def test_c5_flow_teacher_forced_vs_oracle(compiled):
     want = OD.generate_teacher_forced(prompt.numpy(), teacher.numpy(), _np(params), cfg,
                                       fused=compiled)
     got = logits.cpu().float().numpy()
-    np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2)
+    if not compiled:
+        np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2)
+    else:
+        # the noise-floor gate of the c4 test (two fp16 rounding regimes of
+        # the oracle bound the device's deviation)
+        eager = OD.generate_teacher_forced(prompt.numpy(), teacher.numpy(), _np(params), cfg,
+                                           fused=False)
+        frac_dev, max_dev = _violations(got, want)
+        frac_floor, max_floor = _violations(eager, want)
+        print(f"device vs oracle: {frac_dev:.2e}, max {max_dev:.4f}; "
+              f"floor: {frac_floor:.2e}, max {max_floor:.4f}", flush=True)
+        assert frac_dev <= 1e-4
+        assert frac_dev <= max(frac_floor, 1e-5) and max_dev <= max(max_floor, 1e-2) * 1.5
     # greedy tokens: equal to the oracle's argmax wherever that argmax is
     # decided by more than the tolerance
     top2 = np.sort(want, axis=-1)[..., -2:]

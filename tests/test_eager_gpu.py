@@ -161,6 +161,25 @@ def test_item_and_argmax():
     assert torch.equal(d.max(dim=1).values.cpu(), x.max(dim=1).values)
 
 
+def test_long_row_reductions():
+    # few long rows (LM-head argmax over the vocabulary): one workgroup per row
+    _log("long-row reductions")
+    x = randn((4, 49155), k=3, scale=3.0)
+    x[1, 40000] = 100.0
+    x[2, 7] = 100.0
+    x[2, 49000] = 100.0  # tie: the first index wins
+    d = x.to(DEV)
+    assert torch.equal(d.argmax(-1).cpu(), x.argmax(-1))
+    assert torch.equal(d.argmin(-1).cpu(), x.argmin(-1))
+    assert torch.equal(d.amax(-1).cpu(), x.amax(-1))
+    y = randn((3, 100003), k=4, dtype=torch.float32)
+    torch.testing.assert_close(y.to(DEV).sum(-1).cpu(), y.double().sum(-1).float(),
+                               rtol=1e-5, atol=1e-3)
+    n = torch.zeros(2, 20000)
+    n[1, 12345] = float("nan")
+    assert n.to(DEV).argmax(-1).cpu().tolist() == [0, 12345]
+
+
 # ---------------------------------------------------------------------------
 # eager op known answers (reference tests/test_ops.py)
 # ---------------------------------------------------------------------------

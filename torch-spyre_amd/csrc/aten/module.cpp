@@ -87,6 +87,17 @@ PYBIND11_MODULE(_C, m) {
     return r;
   }, py::arg("device") = -1);
 
+  py::class_<spyre::Graph>(m, "Graph", "HIP graph of the spyre stream (capture / replay).")
+      .def(py::init<>())
+      .def("capture_begin", &spyre::Graph::capture_begin)
+      .def("capture_end", &spyre::Graph::capture_end)
+      .def("replay", [](spyre::Graph& g) {
+        py::gil_scoped_release nogil;
+        g.replay();
+      })
+      .def("reset", &spyre::Graph::reset)
+      .def("pool", &spyre::Graph::pool);
+
   using STL = spyre::SpyreTensorLayout;
   py::class_<STL> cls(m, "SpyreTensorLayout");
   py::enum_<STL::StickFormat>(cls, "StickFormat")

@@ -165,6 +165,13 @@ uint64_t get_seed(int device) { return g_seeds[device < 0 ? 0 : device].load(); 
 // after its last use: every spyre kernel and copy of a device runs on that
 // device's single spyre stream, so stream order guarantees it.  On an
 // out-of-memory error the cache is released and hipMalloc retried.
+//
+// Private pools (graph capture): while a pool is active on a device, that
+// device's allocations are served from, and freed back to, the pool only,
+// so the addresses a captured HIP graph uses are never handed to other work;
+// blocks keep their pool when freed after the capture.  Releasing the pool
+// (when its graph is destroyed) moves its free blocks to the general cache
+// and redirects later frees of its blocks there as well.
 // ---------------------------------------------------------------------------
 namespace {
 
@@ -172,6 +179,7 @@ struct Block {
   void* ptr;
   size_t size;
   int device;
+  int64_t pool;  // 0: general cache, else a private pool id
 };
 
 class CachingAllocator final : public c10::Allocator {
@@ -183,9 +191,11 @@ class CachingAllocator final : public c10::Allocator {
     if (nbytes == 0) return {nullptr, nullptr, &noop_delete, device};
     const size_t size = round_size(nbytes);
     Block* b = nullptr;
+    int64_t pool_id = 0;
     {
       std::lock_guard<std::mutex> lk(mu_);
-      auto& pool = free_[dev];
+      pool_id = active_pool_[dev];
+      auto& pool = pool_id ? private_free_[pool_id] : free_[dev];
       // Best fit, without handing a block more than twice the request.
       auto it = pool.lower_bound(size);
       if (it != pool.end() && it->first <= 2 * size) {
@@ -194,7 +204,7 @@ class CachingAllocator final : public c10::Allocator {
       }
       stats_[dev].num_alloc_calls++;
     }
-    if (!b) b = fresh_block(dev, size);
+    if (!b) b = fresh_block(dev, size, pool_id);
     {
       std::lock_guard<std::mutex> lk(mu_);
       auto& st = stats_[dev];
@@ -236,6 +246,35 @@ class CachingAllocator final : public c10::Allocator {
     return *inst;
   }
 
+  int64_t begin_pool(int dev) {
+    std::lock_guard<std::mutex> lk(mu_);
+    TORCH_CHECK(active_pool_[dev] == 0, "spyre: a private pool is already active on spyre:",
+                dev);
+    const int64_t id = ++next_pool_;
+    live_pools_.insert(id);
+    active_pool_[dev] = id;
+    return id;
+  }
+
+  void end_pool(int dev) {
+    std::lock_guard<std::mutex> lk(mu_);
+    active_pool_[dev] = 0;
+  }
+
+  void release_pool(int64_t id) {
+    std::lock_guard<std::mutex> lk(mu_);
+    live_pools_.erase(id);
+    for (int d = 0; d < kMaxDevices; ++d)
+      if (active_pool_[d] == id) active_pool_[d] = 0;
+    auto it = private_free_.find(id);
+    if (it == private_free_.end()) return;
+    for (auto& kv : it->second) {
+      kv.second->pool = 0;
+      free_[kv.second->device].emplace(kv.first, kv.second);
+    }
+    private_free_.erase(it);
+  }
+
  private:
   static size_t round_size(size_t n) {
     constexpr size_t kSmall = 512, kLarge = size_t(2) << 20, kSplit = size_t(1) << 20;
@@ -243,7 +282,7 @@ class CachingAllocator final : public c10::Allocator {
     return (n + kLarge - 1) / kLarge * kLarge;
   }
 
-  Block* fresh_block(int dev, size_t size) {
+  Block* fresh_block(int dev, size_t size, int64_t pool_id) {
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, size);
     if (e == hipErrorOutOfMemory) {
@@ -261,7 +300,7 @@ class CachingAllocator final : public c10::Allocator {
     std::lock_guard<std::mutex> lk(mu_);
     stats_[dev].reserved += static_cast<int64_t>(size);
     stats_[dev].num_device_mallocs++;
-    return new Block{p, size, dev};
+    return new Block{p, size, dev, pool_id};
   }
 
   static void release(void* ctx) {
@@ -269,7 +308,12 @@ class CachingAllocator final : public c10::Allocator {
     auto& self = instance();
     std::lock_guard<std::mutex> lk(self.mu_);
     self.stats_[b->device].allocated -= static_cast<int64_t>(b->size);
-    self.free_[b->device].emplace(b->size, b);
+    if (b->pool != 0 && self.live_pools_.count(b->pool)) {
+      self.private_free_[b->pool].emplace(b->size, b);
+    } else {
+      b->pool = 0;
+      self.free_[b->device].emplace(b->size, b);
+    }
   }
 
   static void noop_delete(void*) {}
@@ -277,6 +321,10 @@ class CachingAllocator final : public c10::Allocator {
   std::mutex mu_;
   std::array<std::multimap<size_t, Block*>, kMaxDevices> free_;
   std::array<MemoryStats, kMaxDevices> stats_{};
+  std::array<int64_t, kMaxDevices> active_pool_{};
+  std::unordered_map<int64_t, std::multimap<size_t, Block*>> private_free_;
+  std::unordered_set<int64_t> live_pools_;
+  int64_t next_pool_ = 0;
 };
 
 // Pinned host memory for copy staging (hipHostMalloc, never hipHostRegister).
@@ -332,6 +380,70 @@ MemoryStats memory_stats(int device) {
 }
 
 void empty_cache() { CachingAllocator::instance().empty_cache(); }
+
+// ---------------------------------------------------------------------------
+// HIP graphs of the spyre stream
+// ---------------------------------------------------------------------------
+Graph::~Graph() { reset(); }
+
+void Graph::capture_begin() {
+  TORCH_CHECK(!capturing_ && exec_ == nullptr, "spyre graph: already captured; reset() first");
+  device_ = current_device();
+  hipStream_t s = stream(device_);
+  // Work queued before the capture must not be part of it (and must not be
+  // waited on from inside it).
+  synchronize(device_);
+  pool_ = CachingAllocator::instance().begin_pool(device_);
+  hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed);
+  if (e != hipSuccess) {
+    CachingAllocator::instance().end_pool(device_);
+    CachingAllocator::instance().release_pool(pool_);
+    pool_ = 0;
+    SPYRE_HIP_CHECK(e);
+  }
+  capturing_ = true;
+}
+
+void Graph::capture_end() {
+  TORCH_CHECK(capturing_, "spyre graph: capture_end without capture_begin");
+  capturing_ = false;
+  CachingAllocator::instance().end_pool(device_);
+  hipGraph_t g = nullptr;
+  SPYRE_HIP_CHECK(hipStreamEndCapture(stream(device_), &g));
+  graph_ = g;
+  hipGraphExec_t x = nullptr;
+  SPYRE_HIP_CHECK(hipGraphInstantiate(&x, g, nullptr, nullptr, 0));
+  exec_ = x;
+}
+
+void Graph::replay() {
+  TORCH_CHECK(exec_ != nullptr, "spyre graph: nothing captured");
+  SPYRE_HIP_CHECK(hipGraphLaunch(static_cast<hipGraphExec_t>(exec_), stream(device_)));
+}
+
+void Graph::reset() {
+  if (capturing_) {
+    hipGraph_t g = nullptr;
+    (void)hipStreamEndCapture(stream(device_), &g);
+    if (g) (void)hipGraphDestroy(g);
+    (void)hipGetLastError();
+    CachingAllocator::instance().end_pool(device_);
+    capturing_ = false;
+  }
+  if (exec_) {
+    synchronize(device_);
+    (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(exec_));
+    exec_ = nullptr;
+  }
+  if (graph_) {
+    (void)hipGraphDestroy(static_cast<hipGraph_t>(graph_));
+    graph_ = nullptr;
+  }
+  if (pool_) {
+    CachingAllocator::instance().release_pool(pool_);
+    pool_ = 0;
+  }
+}
 
 void free_runtime() {
   if (!runtime_started()) return;

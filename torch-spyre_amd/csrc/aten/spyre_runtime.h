@@ -71,6 +71,32 @@ struct MemoryStats {
 MemoryStats memory_stats(int device);
 void empty_cache();
 
+// A HIP graph captured from the spyre stream of the current device.
+// Allocations made during the capture come from a private pool that stays
+// reserved for the graph until reset() (or destruction), so replays read
+// and write the same buffers the capture saw.  Work captured must be
+// stream-ordered spyre work only (no host synchronisation, no memory set
+// nodes); a replay is asynchronous like any other spyre op.
+class Graph {
+ public:
+  Graph() = default;
+  ~Graph();
+  Graph(const Graph&) = delete;
+  Graph& operator=(const Graph&) = delete;
+  void capture_begin();
+  void capture_end();
+  void replay();
+  void reset();
+  int64_t pool() const { return pool_; }
+
+ private:
+  int device_ = 0;
+  int64_t pool_ = 0;
+  bool capturing_ = false;
+  void* graph_ = nullptr;
+  void* exec_ = nullptr;
+};
+
 // Bytes the reference's stick-granular sizing gives a tensor of `sizes`
 // (torch_spyre/csrc/spyre_mem.cpp:598-611, with the stick count rounded up):
 // 128 bytes per 128-byte stick of the last dim, times the other dims; 128

@@ -502,15 +502,18 @@ gemm_kernel(const GemmArgs p) {
 // ---------------------------------------------------------------------------
 // Small-M products: D[m, n] = epi(alpha * sum_k A[m, k] * B[n, k] + beta*C)
 // for M <= MT rows, A and B K-contiguous and 16-byte aligned, K % 8 == 0.
-// One workgroup (256 threads) computes R = 4 outputs columns n for all M
-// rows: thread t reads 16 bytes of each of the 4 weight rows at
-// k = 8t + 2048 j (whole 4 KiB row segments per wave group, coalesced), and
-// the 4 x 16-byte loads per step are independent, so each thread keeps 4..28
-// loads in flight.  A (at most 16 x K, shared by every workgroup) is read
-// through the caches.  fp16 uses v_dot2_f32_f16 (two products summed into
-// an fp32 accumulator), bf16 widens with shifts and uses fp32 FMAs.  The
-// M x R partial sums are reduced across the wave with butterflies and across
-// the 4 waves through LDS.
+// A group of TPR threads computes R output columns n for all M rows: thread t
+// reads 16 bytes of each of the R weight rows at k = 8t + 8*TPR*j (whole row
+// segments per group, coalesced) and keeps the R loads of two K steps in
+// flight.  TPR follows K (256 threads for K >= 2048 down to 16 for K = 128,
+// so short rows such as attention keys do not idle most of the workgroup)
+// and a workgroup holds 256/TPR groups.  Workgroups loop over row blocks
+// (grid capped near the number of resident workgroups), so long matrices do
+// not end in a partial wave of workgroups.  A (at most 16 x K, read by every
+// workgroup) comes through the caches.  fp16 uses v_dot2_f32_f16 (two
+// products summed into an fp32 accumulator), bf16 widens with shifts and
+// uses fp32 FMAs.  Partial sums are reduced within the group by butterflies
+// and, for groups wider than a wave, through LDS.
 // ---------------------------------------------------------------------------
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
@@ -535,93 +538,154 @@ __device__ inline float dot8_acc(u32x4 a, u32x4 b, float acc) {
   return acc;
 }
 
-constexpr int kSkinnyR = 4;        // output columns per workgroup
 constexpr int kSkinnyThreads = 256;
 
-template <typename T, int MT>
-__global__ void __launch_bounds__(kSkinnyThreads) gemm_skinny_kernel(const GemmArgs p) {
-  constexpr int R = kSkinnyR;
+template <typename T>
+__device__ inline float skinny_epilogue(const GemmArgs& p, float v, int64_t bz, int m, int64_t n) {
+  v *= p.alpha;
+  if (p.c != nullptr && p.beta != 0.f) {
+    const T* C = static_cast<const T*>(p.c) + bz * p.stride_c;
+    v += p.beta * Num<T>::to_f(C[m * p.ldc_row + n * p.ldc_col]);
+  }
+  if (p.epilogue == SPH_EPI_RELU) v = fmaxf(v, 0.f);
+  else if (p.epilogue == SPH_EPI_GELU) v = gelu_erf(v);
+  else if (p.epilogue == SPH_EPI_SILU) v = silu(v);
+  return v;
+}
+
+template <typename T, int MT, int R, int TPR>
+__global__ void __launch_bounds__(kSkinnyThreads) gemm_skinny_kernel(const GemmArgs p,
+                                                                     int64_t nblocks) {
+  constexpr int G = kSkinnyThreads / TPR;   // row groups per workgroup
+  constexpr int WPG = TPR > 64 ? TPR / 64 : 1;  // waves per group
+  __shared__ float red[TPR > 64 ? G * WPG * MT * R : 1];
+  const int g = threadIdx.x / TPR, t = threadIdx.x % TPR;
   const int64_t bz = blockIdx.y;
   const uint16_t* A = static_cast<const uint16_t*>(p.a) + bz * p.stride_a;
   const uint16_t* B = static_cast<const uint16_t*>(p.b) + bz * p.stride_b;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * R;
-  const int tid = threadIdx.x;
+  T* D = static_cast<T*>(p.d) + bz * p.stride_d;
   const int mrows = static_cast<int>(p.m);
-  const uint16_t* bp[R];
-  bool bv[R];
+  // Every thread runs the same number of outer iterations (the bound does
+  // not depend on the group), so the barriers below are uniform.
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * G; base < nblocks;
+       base += static_cast<int64_t>(gridDim.x) * G) {
+    const int64_t blk = base + g;
+    const int64_t n0 = blk * R;
+    float acc[MT][R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    bv[r] = n0 + r < p.n;
-    bp[r] = B + (bv[r] ? n0 + r : n0) * p.ldb;
-  }
-  float acc[MT][R];
+    for (int m = 0; m < MT; ++m)
 #pragma unroll
-  for (int m = 0; m < MT; ++m)
+      for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
+    if (blk < nblocks) {
+      const uint16_t* bp[R];
+      bool bv[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
-  for (int64_t k = static_cast<int64_t>(tid) * 8; k < p.k; k += kSkinnyThreads * 8) {
-    u32x4 w[R];
+      for (int r = 0; r < R; ++r) {
+        bv[r] = n0 + r < p.n;
+        bp[r] = B + (bv[r] ? n0 + r : n0) * p.ldb;
+      }
+#pragma unroll 2
+      for (int64_t k = static_cast<int64_t>(t) * 8; k < p.k; k += TPR * 8) {
+        u32x4 w[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      w[r] = bv[r] ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bp[r] + k))
-                   : zero4();
+        for (int r = 0; r < R; ++r)
+          w[r] = bv[r] ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bp[r] + k))
+                       : zero4();
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      if (m < mrows) {
-        const u32x4 x = *reinterpret_cast<const u32x4*>(A + m * p.lda + k);
+        for (int m = 0; m < MT; ++m) {
+          if (m < mrows) {
+            const u32x4 x = *reinterpret_cast<const u32x4*>(A + m * p.lda + k);
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[m][r] = dot8_acc<T>(x, w[r], acc[m][r]);
+            for (int r = 0; r < R; ++r) acc[m][r] = dot8_acc<T>(x, w[r], acc[m][r]);
+          }
+        }
       }
     }
-  }
-  // Reduce the MT x R partial sums over the workgroup.
-  __shared__ float red[kSkinnyThreads / 64][MT * R];
-  const int lane = tid & 63, wave = tid >> 6;
+    // Butterflies within the group's wave segment (all lanes take part).
+    constexpr int LANES = TPR > 64 ? 64 : TPR;
 #pragma unroll
-  for (int m = 0; m < MT; ++m)
+    for (int m = 0; m < MT; ++m)
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float v = acc[m][r];
+      for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-      if (lane == 0) red[wave][m * R + r] = v;
-    }
-  __syncthreads();
-  if (tid < MT * R) {
-    const int m = tid / R, r = tid % R;
-    const int64_t n = n0 + r;
-    if (m < mrows && n < p.n) {
-      float v = 0.f;
+        for (int off = LANES / 2; off > 0; off >>= 1)
+          acc[m][r] += __shfl_xor(acc[m][r], off, 64);
+    if constexpr (TPR > 64) {
+      const int wig = t / 64;  // wave within the group
+      if ((t & 63) == 0) {
 #pragma unroll
-      for (int w = 0; w < kSkinnyThreads / 64; ++w) v += red[w][tid];
-      v *= p.alpha;
-      if (p.c != nullptr && p.beta != 0.f) {
-        const T* C = static_cast<const T*>(p.c) + bz * p.stride_c;
-        v += p.beta * Num<T>::to_f(C[m * p.ldc_row + n * p.ldc_col]);
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+          for (int r = 0; r < R; ++r) red[((g * WPG) + wig) * MT * R + m * R + r] = acc[m][r];
       }
-      if (p.epilogue == SPH_EPI_RELU) v = fmaxf(v, 0.f);
-      else if (p.epilogue == SPH_EPI_GELU) v = gelu_erf(v);
-      else if (p.epilogue == SPH_EPI_SILU) v = silu(v);
-      T* D = static_cast<T*>(p.d) + bz * p.stride_d;
-      D[m * p.ldd + n] = Num<T>::from_f(v);
+      __syncthreads();
+      for (int q = t; q < MT * R; q += TPR) {
+        const int m = q / R, r = q % R;
+        const int64_t n = n0 + r;
+        if (blk < nblocks && m < mrows && n < p.n) {
+          float v = 0.f;
+#pragma unroll
+          for (int w = 0; w < WPG; ++w) v += red[(g * WPG + w) * MT * R + q];
+          D[m * p.ldd + n] = Num<T>::from_f(skinny_epilogue<T>(p, v, bz, m, n));
+        }
+      }
+      __syncthreads();
+    } else {
+      if (blk < nblocks) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const int64_t n = n0 + r;
+            if (t == (m * R + r) % TPR && m < mrows && n < p.n)
+              D[m * p.ldd + n] = Num<T>::from_f(skinny_epilogue<T>(p, acc[m][r], bz, m, n));
+          }
+      }
     }
   }
 }
 
+template <typename T, int MT, int R>
+void launch_skinny_tpr(const GemmArgs& p, int64_t batch, int tpr, hipStream_t st) {
+  const int64_t nblocks = ceil_div(p.n, R);
+  const int g = kSkinnyThreads / tpr;
+  int64_t gx = ceil_div(nblocks, g);
+  const int64_t cap = batch >= 1024 ? 1 : 1024 / batch;  // ~4 resident workgroups per CU
+  if (gx > cap) gx = cap;
+  dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(batch));
+  dim3 block(kSkinnyThreads);
+  switch (tpr) {
+    case 256: gemm_skinny_kernel<T, MT, R, 256><<<grid, block, 0, st>>>(p, nblocks); break;
+    case 128: gemm_skinny_kernel<T, MT, R, 128><<<grid, block, 0, st>>>(p, nblocks); break;
+    case 64: gemm_skinny_kernel<T, MT, R, 64><<<grid, block, 0, st>>>(p, nblocks); break;
+    case 32: gemm_skinny_kernel<T, MT, R, 32><<<grid, block, 0, st>>>(p, nblocks); break;
+    default: gemm_skinny_kernel<T, MT, R, 16><<<grid, block, 0, st>>>(p, nblocks); break;
+  }
+}
+
+template <typename T, int MT>
+void launch_skinny_r(const GemmArgs& p, int64_t batch, int tpr, hipStream_t st) {
+  // 4 columns per group when there are enough of them to fill the GPU
+  if (p.n * batch >= 8192)
+    launch_skinny_tpr<T, MT, 4>(p, batch, tpr, st);
+  else
+    launch_skinny_tpr<T, MT, 2>(p, batch, tpr, st);
+}
+
 template <typename T>
 int launch_skinny(const GemmArgs& p, int64_t batch, hipStream_t st) {
-  dim3 grid(static_cast<unsigned>(ceil_div(p.n, kSkinnyR)), static_cast<unsigned>(batch));
-  dim3 block(kSkinnyThreads);
+  int tpr = 256;
+  while (tpr > 16 && static_cast<int64_t>(tpr) * 8 > p.k) tpr >>= 1;
   if (p.m <= 1)
-    gemm_skinny_kernel<T, 1><<<grid, block, 0, st>>>(p);
+    launch_skinny_r<T, 1>(p, batch, tpr, st);
   else if (p.m <= 2)
-    gemm_skinny_kernel<T, 2><<<grid, block, 0, st>>>(p);
+    launch_skinny_r<T, 2>(p, batch, tpr, st);
   else if (p.m <= 4)
-    gemm_skinny_kernel<T, 4><<<grid, block, 0, st>>>(p);
+    launch_skinny_r<T, 4>(p, batch, tpr, st);
   else if (p.m <= 8)
-    gemm_skinny_kernel<T, 8><<<grid, block, 0, st>>>(p);
+    launch_skinny_r<T, 8>(p, batch, tpr, st);
   else
-    gemm_skinny_kernel<T, 16><<<grid, block, 0, st>>>(p);
+    launch_skinny_r<T, 16>(p, batch, tpr, st);
   return check_launch("sph_gemm (small M)");
 }
 
@@ -669,7 +733,7 @@ template <typename T>
 int gemm_dispatch(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
                   hipStream_t st) {
   if (p.m <= 16 && a_kcont && b_kcont && p.vec_a && p.vec_b && p.k > 0 && p.k % 8 == 0 &&
-      ceil_div(p.n, kSkinnyR) < (1LL << 31))
+      ceil_div(p.n, 2) < (1LL << 40))
     return launch_skinny<T>(p, batch, st);
   const int64_t t256 = ceil_div(p.m, 256) * ceil_div(p.n, 256) * batch;
   const int64_t t128 = ceil_div(p.m, 128) * ceil_div(p.n, 128) * batch;

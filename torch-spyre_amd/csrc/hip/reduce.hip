@@ -3,8 +3,10 @@
 //
 // The host reorders the iteration space as [kept dims..., reduced dims...].
 // When the innermost reduced dim is contiguous in memory a wave reduces one
-// output (lanes stride the reduced elements -> coalesced reads); otherwise one
-// thread reduces one output and adjacent threads read adjacent kept elements.
+// output (lanes stride the reduced elements -> coalesced reads), or, for a
+// few long rows (e.g. argmax over an LM head's logits), a whole 1024-thread
+// workgroup reduces one output; otherwise one thread reduces one output and
+// adjacent threads read adjacent kept elements.
 #include <math.h>
 
 #include "sph_common.h"
@@ -161,6 +163,7 @@ __device__ inline void outer_offsets(const RedArgs& p, int64_t o, int64_t& in_of
 }
 
 __device__ inline int64_t inner_offset(const RedArgs& p, int64_t i) {
+  if (p.n_inner == 1) return i * p.inner_stride[0];
   int64_t off = 0;
   for (int d = p.n_inner - 1; d >= 0; --d) {
     const int64_t c = i % p.inner_size[d];
@@ -202,6 +205,45 @@ __global__ void __launch_bounds__(256) reduce_wave(const RedArgs p) {
       combine<A>(p.op, a, b);
     }
     if (lane == 0) finish<A>(p, out_off, a);
+  }
+}
+
+// One 1024-thread workgroup per output: threads stride over the reduced
+// elements, waves combine with butterflies, the 16 wave results through LDS.
+constexpr int kBlockRed = 1024;
+
+template <typename A>
+__global__ void __launch_bounds__(kBlockRed) reduce_block(const RedArgs p) {
+  __shared__ A sv[kBlockRed / 64];
+  __shared__ int64_t si[kBlockRed / 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int64_t o = blockIdx.x; o < p.outer_numel; o += gridDim.x) {
+    int64_t in_off, out_off;
+    outer_offsets(p, o, in_off, out_off);
+    Acc<A> a = init_acc<A>(p.op);
+    for (int64_t i = threadIdx.x; i < p.inner_numel; i += kBlockRed) {
+      const A v = load_val<A>(p.in, p.in_dt, in_off + inner_offset(p, i));
+      fold<A>(p.op, a, v, i);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      Acc<A> b = shfl_acc<A>(a, off);
+      combine<A>(p.op, a, b);
+    }
+    if (lane == 0) {
+      sv[wave] = a.v;
+      si[wave] = a.idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      Acc<A> r{sv[0], si[0]};
+      for (int w = 1; w < kBlockRed / 64; ++w) {
+        Acc<A> b{sv[w], si[w]};
+        combine<A>(p.op, r, b);
+      }
+      finish<A>(p, out_off, r);
+    }
+    __syncthreads();
   }
 }
 
@@ -276,7 +318,12 @@ extern "C" int sph_reduce(int op, const sph_operand* in, const sph_operand* out,
     if (g > 65536) g = 65536;
     return static_cast<unsigned>(g < 1 ? 1 : g);
   };
-  if (inner_contig) {
+  if (inner_contig && p.inner_numel >= 8192 && p.outer_numel < 2048) {
+    const unsigned g = static_cast<unsigned>(p.outer_numel < 65536 ? p.outer_numel : 65536);
+    if (f64) reduce_block<double><<<g, kBlockRed, 0, st>>>(p);
+    else if (ints) reduce_block<int64_t><<<g, kBlockRed, 0, st>>>(p);
+    else reduce_block<float><<<g, kBlockRed, 0, st>>>(p);
+  } else if (inner_contig) {
     const unsigned g = grid(p.outer_numel * 64);
     if (f64) reduce_wave<double><<<g, 256, 0, st>>>(p);
     else if (ints) reduce_wave<int64_t><<<g, 256, 0, st>>>(p);

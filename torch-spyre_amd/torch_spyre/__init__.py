@@ -134,6 +134,11 @@ def make_spyre_module() -> types.ModuleType:
     mod._lazy_init = impl._lazy_init
     mod._is_compiled = lambda: True
 
+    from . import graphs as _graphs
+
+    mod.SpyreGraph = _graphs.SpyreGraph
+    mod.graph = _graphs.graph
+
     def __getattr__(name):
         if hasattr(type(impl), name):
             return getattr(impl, name)

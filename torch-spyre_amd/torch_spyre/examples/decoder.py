@@ -10,10 +10,13 @@ Grouped-query attention is computed without copying K/V per query head:
 the 4 query heads that share a KV head are stacked along the rows of one
 bmm operand ([B*8, 4*S, 128] x [B*8, 128, S]), so each attention bmm is
 4x taller and reads each K/V tile once; the causal mask repeats every S
-rows.  Decoding uses a KV cache of one contiguous K and one contiguous V
-buffer [B, 8, max_len, 128] per layer (separate tensors, so a compiled
-decode step scatters the new token's K/V into them in place instead of
-copying an aliased cache).
+rows.  Decoding uses a KV cache of one contiguous K buffer
+[B, 8, max_len, 128] and one V buffer stored transposed, [B, 8, 128, max_len],
+per layer: both attention products of a decode step then read their cache
+operand along its contiguous dimension (scores: K rows; output: V^T rows),
+which is the small-M streaming GEMM's layout.  The buffers are separate
+tensors, so a compiled decode step scatters the new token's K/V into them
+in place instead of copying an aliased cache.
 """
 
 from __future__ import annotations
@@ -81,11 +84,20 @@ def init_params(cfg: DecoderConfig, device, dtype=torch.float16, seed: int = 0xA
         return src[off:off + n].view(shape)
 
     params = {"embed": draw((cfg.vocab, cfg.hidden)).to(device), "layers": []}
+    shp = layer_shapes(cfg)
+    nq, nkv, ni = shp["wq"][0], shp["wk"][0], cfg.intermediate
     for _ in range(cfg.n_layers):
-        lw = {}
-        for name, shape in layer_shapes(cfg).items():
-            lw[name] = (torch.ones(shape, dtype=dtype) if name.endswith("norm")
-                        else draw(shape)).to(device)
+        # Q/K/V and gate/up weights live in one buffer each (one GEMM per
+        # group reads the shared input once); the per-projection weights are
+        # row views of them.
+        wqkv = draw((nq + 2 * nkv, cfg.hidden)).to(device)
+        wgu = draw((2 * ni, cfg.hidden)).to(device)
+        lw = {"attn_norm": torch.ones(shp["attn_norm"], dtype=dtype).to(device),
+              "wqkv": wqkv, "wq": wqkv[:nq], "wk": wqkv[nq:nq + nkv], "wv": wqkv[nq + nkv:],
+              "wo": draw(shp["wo"]).to(device),
+              "mlp_norm": torch.ones(shp["mlp_norm"], dtype=dtype).to(device),
+              "wgu": wgu, "wg": wgu[:ni], "wu": wgu[ni:],
+              "wd": draw(shp["wd"]).to(device)}
         params["layers"].append(lw)
     params["final_norm"] = torch.ones(cfg.hidden, dtype=dtype).to(device)
     params["lm_head"] = draw((cfg.vocab, cfg.hidden)).to(device)
@@ -134,24 +146,46 @@ def _attention(q, k, v, cfg: DecoderConfig, mask):
     return o.view(B, kv, g, Sq, D).permute(0, 3, 1, 2, 4).reshape(B * Sq, kv * g * D)
 
 
+def _qkv(x, w: dict, cfg: DecoderConfig):
+    """Q, K, V projections of x [..., hidden]: one GEMM over the fused
+    weight when the layer has one."""
+    if "wqkv" in w:
+        nq, nkv = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+        qkv = F.linear(x, w["wqkv"])
+        return qkv[..., :nq], qkv[..., nq:nq + nkv], qkv[..., nq + nkv:]
+    return F.linear(x, w["wq"]), F.linear(x, w["wk"]), F.linear(x, w["wv"])
+
+
+def _mlp(x, w: dict, cfg: DecoderConfig):
+    """SwiGLU: down(silu(gate(x)) * up(x)), gate and up as one GEMM when
+    the layer has the fused weight."""
+    if "wgu" in w:
+        gu = F.linear(x, w["wgu"])
+        g, u = gu[..., :cfg.intermediate], gu[..., cfg.intermediate:]
+    else:
+        g, u = F.linear(x, w["wg"]), F.linear(x, w["wu"])
+    return F.linear(F.silu(g) * u, w["wd"])
+
+
 def layer_forward(h, w: dict, cos, sin, mask, cfg: DecoderConfig, cache_kv=None):
     """One decoder layer on h [B, S, hidden] (prefill).  If `cache_kv` is
     given (the layer's (K, V) cache buffers [B, 8, max_len, D]), K/V of
     positions [0, S) are written into it."""
     B, S, _ = h.shape
     x = F.rms_norm(h, (cfg.hidden,), w["attn_norm"], cfg.eps)
-    q = F.linear(x, w["wq"]).view(B, S, cfg.n_heads, cfg.head_dim)
-    k = F.linear(x, w["wk"]).view(B, S, cfg.n_kv_heads, cfg.head_dim)
-    v = F.linear(x, w["wv"]).view(B, S, cfg.n_kv_heads, cfg.head_dim)
+    q, k, v = _qkv(x, w, cfg)
+    q = q.reshape(B, S, cfg.n_heads, cfg.head_dim)
+    k = k.reshape(B, S, cfg.n_kv_heads, cfg.head_dim)
+    v = v.reshape(B, S, cfg.n_kv_heads, cfg.head_dim)
     q = apply_rope(q, cos[:S], sin[:S])
     k = apply_rope(k, cos[:S], sin[:S]).transpose(1, 2)
     v = v.transpose(1, 2)
     if cache_kv is not None:
         cache_kv[0][:, :, :S].copy_(k)
-        cache_kv[1][:, :, :S].copy_(v)
+        cache_kv[1][:, :, :, :S].copy_(v.transpose(2, 3))
     h = h + F.linear(_attention(q, k, v, cfg, mask), w["wo"]).view(B, S, cfg.hidden)
     x = F.rms_norm(h, (cfg.hidden,), w["mlp_norm"], cfg.eps)
-    return h + F.linear(F.silu(F.linear(x, w["wg"])) * F.linear(x, w["wu"]), w["wd"])
+    return h + _mlp(x, w, cfg)
 
 
 def block_forward(tokens, params: dict, cos, sin, mask, cfg: DecoderConfig):
@@ -163,11 +197,12 @@ def block_forward(tokens, params: dict, cos, sin, mask, cfg: DecoderConfig):
 
 
 def new_cache(cfg: DecoderConfig, batch: int, max_len: int, device, dtype=torch.float16):
-    """Per layer, a (K, V) pair of zeroed [batch, 8, max_len, head_dim]
-    buffers."""
-    shape = (batch, cfg.n_kv_heads, max_len, cfg.head_dim)
-    return [(torch.zeros(shape, dtype=dtype, device=device),
-             torch.zeros(shape, dtype=dtype, device=device)) for _ in range(cfg.n_layers)]
+    """Per layer, a zeroed K buffer [batch, 8, max_len, head_dim] and a
+    zeroed transposed V buffer [batch, 8, head_dim, max_len]."""
+    kshape = (batch, cfg.n_kv_heads, max_len, cfg.head_dim)
+    vshape = (batch, cfg.n_kv_heads, cfg.head_dim, max_len)
+    return [(torch.zeros(kshape, dtype=dtype, device=device),
+             torch.zeros(vshape, dtype=dtype, device=device)) for _ in range(cfg.n_layers)]
 
 
 def lm_logits(h_last, params: dict, cfg: DecoderConfig):
@@ -194,16 +229,17 @@ def decode_step(tokens, pos: int, params: dict, cos, sin, cache, cfg: DecoderCon
     c, s = cos[pos:pos + 1], sin[pos:pos + 1]
     for i, w in enumerate(params["layers"]):
         x = F.rms_norm(h, (cfg.hidden,), w["attn_norm"], cfg.eps)
-        q = apply_rope(F.linear(x, w["wq"]).view(B, 1, cfg.n_heads, cfg.head_dim), c, s)
-        k = apply_rope(F.linear(x, w["wk"]).view(B, 1, cfg.n_kv_heads, cfg.head_dim), c, s)
-        v = F.linear(x, w["wv"]).view(B, 1, cfg.n_kv_heads, cfg.head_dim)
+        q, k, v = _qkv(x, w, cfg)
+        q = apply_rope(q.reshape(B, 1, cfg.n_heads, cfg.head_dim), c, s)
+        k = apply_rope(k.reshape(B, 1, cfg.n_kv_heads, cfg.head_dim), c, s)
+        v = v.reshape(B, 1, cfg.n_kv_heads, cfg.head_dim)
         kc, vc = cache[i]
         kc[:, :, pos:pos + 1].copy_(k.transpose(1, 2))
-        vc[:, :, pos:pos + 1].copy_(v.transpose(1, 2))
-        kc, vc = kc[:, :, :pos + 1], vc[:, :, :pos + 1]
+        vc[:, :, :, pos:pos + 1].copy_(v.permute(0, 2, 3, 1))
+        kc, vc = kc[:, :, :pos + 1], vc[:, :, :, :pos + 1].transpose(2, 3)
         h = h + F.linear(_attention(q, kc, vc, cfg, None), w["wo"]).view(B, 1, cfg.hidden)
         x = F.rms_norm(h, (cfg.hidden,), w["mlp_norm"], cfg.eps)
-        h = h + F.linear(F.silu(F.linear(x, w["wg"])) * F.linear(x, w["wu"]), w["wd"])
+        h = h + _mlp(x, w, cfg)
     return lm_logits(h[:, 0], params, cfg)
 
 
@@ -213,27 +249,29 @@ def decode_step_static(tokens, pos, params: dict, cos, sin, cache, cfg: DecoderC
     the cache at `pos` and attention runs over the whole cache length with
     keys after `pos` masked out, so one compiled graph serves every step."""
     B = tokens.shape[0]
-    L = cache[0][0].shape[2]
+    L = cache[0][0].shape[2]  # K buffer [B, 8, max_len, D]
     h = F.embedding(tokens, params["embed"]).view(B, 1, cfg.hidden)
     c, s = cos.index_select(0, pos), sin.index_select(0, pos)
     keys = torch.arange(L, device=tokens.device)
     mask = torch.where(keys <= pos, 0.0, float("-inf")).to(h.dtype)
     for i, w in enumerate(params["layers"]):
         x = F.rms_norm(h, (cfg.hidden,), w["attn_norm"], cfg.eps)
-        q = apply_rope(F.linear(x, w["wq"]).view(B, 1, cfg.n_heads, cfg.head_dim), c, s)
-        k = apply_rope(F.linear(x, w["wk"]).view(B, 1, cfg.n_kv_heads, cfg.head_dim), c, s)
-        v = F.linear(x, w["wv"]).view(B, 1, cfg.n_kv_heads, cfg.head_dim)
+        q, k, v = _qkv(x, w, cfg)
+        q = apply_rope(q.reshape(B, 1, cfg.n_heads, cfg.head_dim), c, s)
+        k = apply_rope(k.reshape(B, 1, cfg.n_kv_heads, cfg.head_dim), c, s)
+        v = v.reshape(B, 1, cfg.n_kv_heads, cfg.head_dim)
         kc, vc = cache[i]
         kc.index_copy_(2, pos, k.transpose(1, 2))
-        vc.index_copy_(2, pos, v.transpose(1, 2))
-        h = h + F.linear(_attention(q, kc, vc, cfg, mask), w["wo"]).view(B, 1, cfg.hidden)
+        vc.index_copy_(3, pos, v.permute(0, 2, 3, 1))
+        h = h + F.linear(_attention(q, kc, vc.transpose(2, 3), cfg, mask),
+                         w["wo"]).view(B, 1, cfg.hidden)
         x = F.rms_norm(h, (cfg.hidden,), w["mlp_norm"], cfg.eps)
-        h = h + F.linear(F.silu(F.linear(x, w["wg"])) * F.linear(x, w["wu"]), w["wd"])
+        h = h + _mlp(x, w, cfg)
     return lm_logits(h[:, 0], params, cfg)
 
 
 def generate(prompt, params: dict, cfg: DecoderConfig, steps: int, device, layer_fn=None,
-             teacher=None, decode_fn=None):
+             teacher=None, decode_fn=None, use_graph=False):
     """Greedy decoding: prefill `prompt` [B, S], then `steps` decode steps.
     Returns (the argmax token of each step [B, steps], the logits that chose
     them [steps+1, B, vocab]).  With `teacher` ([B, steps] tokens) those
@@ -241,7 +279,9 @@ def generate(prompt, params: dict, cfg: DecoderConfig, steps: int, device, layer
     logits of a device run and a CPU run can be compared step by step.
     `decode_fn` (e.g. torch.compile(decode_step_static)) replaces the
     eager decode step; its position tensor lives on the device and is
-    advanced there, so no step waits on the host."""
+    advanced there, so no step waits on the host.  With `use_graph` the
+    decode step (decode_fn, the argmax and the position update) is captured
+    once into a HIP graph of the spyre stream and each step is one replay."""
     B, S = prompt.shape
     dt = params["embed"].dtype
     cos, sin = rope_tables(cfg, S + steps, device, dt)
@@ -250,6 +290,11 @@ def generate(prompt, params: dict, cfg: DecoderConfig, steps: int, device, layer
                       layer_fn)]
     out = []
     pos = torch.full((1,), S, dtype=torch.int64).to(device) if decode_fn is not None else None
+    if use_graph and steps > 0:
+        if decode_fn is None:
+            raise ValueError("use_graph needs a decode_fn with static shapes")
+        return _generate_graph(logits, pos, params, cfg, steps, cos, sin, cache, decode_fn,
+                               teacher)
     for t in range(steps):
         nxt = logits[-1].argmax(-1)
         out.append(nxt)
@@ -259,4 +304,29 @@ def generate(prompt, params: dict, cfg: DecoderConfig, steps: int, device, layer
         else:
             logits.append(decode_fn(feed, pos, params, cos, sin, cache, cfg))
             pos.add_(1)
+    return torch.stack(out, 1), torch.stack(logits, 0)
+
+
+def _generate_graph(logits, pos, params, cfg, steps, cos, sin, cache, decode_fn, teacher):
+    import torch_spyre.graphs as graphs
+
+    feed = logits[0].argmax(-1)
+    out = [feed.clone()]
+    if teacher is not None:
+        feed.copy_(teacher[:, 0])
+    # one real step outside the capture loads every kernel; it writes the
+    # cache at `pos` exactly as the first replay will
+    decode_fn(feed, pos, params, cos, sin, cache, cfg)
+    g = graphs.SpyreGraph()
+    with graphs.graph(g):
+        step_logits = decode_fn(feed, pos, params, cos, sin, cache, cfg)
+        step_arg = step_logits.argmax(-1)
+        pos.add_(1)
+    for t in range(steps):
+        g.replay()
+        logits.append(step_logits.clone())
+        if t + 1 < steps:
+            out.append(step_arg.clone())
+            feed.copy_(step_arg if teacher is None else teacher[:, t + 1])
+    g.reset()
     return torch.stack(out, 1), torch.stack(logits, 0)
