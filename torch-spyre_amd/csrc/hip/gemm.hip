@@ -577,27 +577,45 @@ __global__ void __launch_bounds__(kSkinnyThreads) gemm_skinny_kernel(const GemmA
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
     if (blk < nblocks) {
+      // Loads are unconditional (rows past N and M read a valid row, whose
+      // results are never stored) so no branch separates them: the R + MT
+      // loads of the next K step are issued before the current step's dot
+      // products and one wait covers them.
       const uint16_t* bp[R];
-      bool bv[R];
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        bv[r] = n0 + r < p.n;
-        bp[r] = B + (bv[r] ? n0 + r : n0) * p.ldb;
-      }
-#pragma unroll 2
-      for (int64_t k = static_cast<int64_t>(t) * 8; k < p.k; k += TPR * 8) {
-        u32x4 w[R];
+      for (int r = 0; r < R; ++r) bp[r] = B + (n0 + r < p.n ? n0 + r : p.n - 1) * p.ldb;
+      const uint16_t* ap[MT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) ap[m] = A + (m < mrows ? m : mrows - 1) * p.lda;
+      constexpr int64_t STEP = TPR * 8;
+      int64_t k = static_cast<int64_t>(t) * 8;
+      if (k < p.k) {
+        u32x4 w[R], x[MT];
 #pragma unroll
         for (int r = 0; r < R; ++r)
-          w[r] = bv[r] ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bp[r] + k))
-                       : zero4();
+          w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bp[r] + k));
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-          if (m < mrows) {
-            const u32x4 x = *reinterpret_cast<const u32x4*>(A + m * p.lda + k);
+        for (int m = 0; m < MT; ++m) x[m] = *reinterpret_cast<const u32x4*>(ap[m] + k);
+        while (true) {
+          const int64_t kn = k + STEP;
+          const bool more = kn < p.k;
+          const int64_t kl = more ? kn : k;  // reload the current step when done
+          u32x4 w2[R], x2[MT];
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[m][r] = dot8_acc<T>(x, w[r], acc[m][r]);
-          }
+          for (int r = 0; r < R; ++r)
+            w2[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bp[r] + kl));
+#pragma unroll
+          for (int m = 0; m < MT; ++m) x2[m] = *reinterpret_cast<const u32x4*>(ap[m] + kl);
+#pragma unroll
+          for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[m][r] = dot8_acc<T>(x[m], w[r], acc[m][r]);
+          if (!more) break;
+#pragma unroll
+          for (int r = 0; r < R; ++r) w[r] = w2[r];
+#pragma unroll
+          for (int m = 0; m < MT; ++m) x[m] = x2[m];
+          k = kn;
         }
       }
     }
@@ -645,47 +663,52 @@ __global__ void __launch_bounds__(kSkinnyThreads) gemm_skinny_kernel(const GemmA
   }
 }
 
-template <typename T, int MT, int R>
-void launch_skinny_tpr(const GemmArgs& p, int64_t batch, int tpr, hipStream_t st) {
+template <typename T, int MT, int R, int TPR>
+void launch_skinny_cfg(const GemmArgs& p, int64_t batch, hipStream_t st) {
   const int64_t nblocks = ceil_div(p.n, R);
-  const int g = kSkinnyThreads / tpr;
-  int64_t gx = ceil_div(nblocks, g);
-  const int64_t cap = batch >= 1024 ? 1 : 1024 / batch;  // ~4 resident workgroups per CU
+  constexpr int G = kSkinnyThreads / TPR;
+  int64_t gx = ceil_div(nblocks, G);
+  const int64_t cap = batch >= 4096 ? 1 : 4096 / batch;
   if (gx > cap) gx = cap;
   dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(batch));
-  dim3 block(kSkinnyThreads);
-  switch (tpr) {
-    case 256: gemm_skinny_kernel<T, MT, R, 256><<<grid, block, 0, st>>>(p, nblocks); break;
-    case 128: gemm_skinny_kernel<T, MT, R, 128><<<grid, block, 0, st>>>(p, nblocks); break;
-    case 64: gemm_skinny_kernel<T, MT, R, 64><<<grid, block, 0, st>>>(p, nblocks); break;
-    case 32: gemm_skinny_kernel<T, MT, R, 32><<<grid, block, 0, st>>>(p, nblocks); break;
-    default: gemm_skinny_kernel<T, MT, R, 16><<<grid, block, 0, st>>>(p, nblocks); break;
-  }
+  gemm_skinny_kernel<T, MT, R, TPR><<<grid, dim3(kSkinnyThreads), 0, st>>>(p, nblocks);
 }
 
+// Launch shape from a sweep on MI355X over the decode shapes (x[4, K] times
+// W[N, K], 32 MB .. 400 MB of weights): two-wave groups (TPR 128) with two
+// columns each for K ~ 4096, four columns for long rows, one-wave groups of
+// four columns for very wide W (LM heads), whole-workgroup groups for narrow
+// W; TPR never exceeds K / 8 (every thread owns at least one K chunk).
 template <typename T, int MT>
-void launch_skinny_r(const GemmArgs& p, int64_t batch, int tpr, hipStream_t st) {
-  // 4 columns per group when there are enough of them to fill the GPU
-  if (p.n * batch >= 8192)
-    launch_skinny_tpr<T, MT, 4>(p, batch, tpr, st);
-  else
-    launch_skinny_tpr<T, MT, 2>(p, batch, tpr, st);
+void launch_skinny_m(const GemmArgs& p, int64_t batch, hipStream_t st) {
+  int tmax = 256;
+  while (tmax > 16 && static_cast<int64_t>(tmax) * 8 > p.k) tmax >>= 1;
+  const int64_t cols = p.n * batch;
+  int tpr = 128, r = p.k >= 8192 ? 4 : 2;
+  if (cols >= 32768) tpr = 64, r = 4;
+  else if (cols <= 2048) tpr = 256, r = 2;
+  if (tpr > tmax) tpr = tmax, r = 2;
+  if (r == 4 && tpr == 64) return launch_skinny_cfg<T, MT, 4, 64>(p, batch, st);
+  if (r == 4) return launch_skinny_cfg<T, MT, 4, 128>(p, batch, st);
+  switch (tpr) {
+    case 256: return launch_skinny_cfg<T, MT, 2, 256>(p, batch, st);
+    case 128: return launch_skinny_cfg<T, MT, 2, 128>(p, batch, st);
+    case 64: return launch_skinny_cfg<T, MT, 2, 64>(p, batch, st);
+    case 32: return launch_skinny_cfg<T, MT, 2, 32>(p, batch, st);
+    default: return launch_skinny_cfg<T, MT, 2, 16>(p, batch, st);
+  }
 }
 
 template <typename T>
 int launch_skinny(const GemmArgs& p, int64_t batch, hipStream_t st) {
-  int tpr = 256;
-  while (tpr > 16 && static_cast<int64_t>(tpr) * 8 > p.k) tpr >>= 1;
   if (p.m <= 1)
-    launch_skinny_r<T, 1>(p, batch, tpr, st);
-  else if (p.m <= 2)
-    launch_skinny_r<T, 2>(p, batch, tpr, st);
+    launch_skinny_m<T, 1>(p, batch, st);
   else if (p.m <= 4)
-    launch_skinny_r<T, 4>(p, batch, tpr, st);
+    launch_skinny_m<T, 4>(p, batch, st);
   else if (p.m <= 8)
-    launch_skinny_r<T, 8>(p, batch, tpr, st);
+    launch_skinny_m<T, 8>(p, batch, st);
   else
-    launch_skinny_r<T, 16>(p, batch, tpr, st);
+    launch_skinny_m<T, 16>(p, batch, st);
   return check_launch("sph_gemm (small M)");
 }
 
