@@ -434,8 +434,8 @@ def main(argv=None):
     ap.add_argument("--no-decoder", action="store_true")
     ap.add_argument("--c5-layers", type=int, default=40)
     ap.add_argument("--decode-steps", type=int, default=128)
-    ap.add_argument("--kernel", choices=["all", "gemm", "copy"], default="all",
-                    help="gemm / copy: run only that kernel (for rocprofv3 counter passes)")
+    ap.add_argument("--kernel", choices=["all", "gemm", "copy", "decoder"], default="all",
+                    help="gemm / copy / decoder: run only that part (for rocprofv3 passes)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; runs on more than one GPU are not "
@@ -452,6 +452,10 @@ def main(argv=None):
     stream = torch.cuda.current_stream()
     if args.kernel == "copy":
         print(json.dumps({"kernel": "copy", **bench_copy(args.steps, args.warmup, stream, _capi)}))
+        return 0
+    if args.kernel == "decoder":
+        print(json.dumps({"kernel": "decoder",
+                          **bench_decoder(5, 2, args.c5_layers, args.decode_steps)}))
         return 0
     if args.kernel == "gemm":
         args.no_extra = args.no_cpu = True
