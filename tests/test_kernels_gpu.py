@@ -263,6 +263,59 @@ def test_gemm_bias_alpha_beta_epilogue(epi, name):
     assert_close_fp(d2, O.gemm(A.numpy(), B.numpy(), beta=-1.0, c=C.numpy()))
 
 
+@pytest.mark.parametrize("m,n,k,tb,pad", [(256, 512, 192, False, 0), (512, 256, 320, True, 0),
+                                          (256, 256, 64, True, 8), (512, 768, 128, False, 64),
+                                          (2048, 4096, 12800, True, 0), (768, 1024, 4096, False, 0)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_gemm_whole_tile_direct_load(m, n, k, tb, pad, dtype):
+    # whole 256x256 tiles with K-contiguous A run the direct-to-LDS kernel:
+    # odd and even K-tile counts (k/64 = 1, 2, 3, 5, 64, 200), row-major and
+    # K-contiguous B, leading dimensions wider than the matrix (pad)
+    _log(f"gemm direct-load {m}x{n}x{k} tb={tb} pad={pad} {dtype}")
+    A = uniform((m, k), k=21, dtype=dtype)
+    B = uniform((k, n), k=22, dtype=dtype)
+    if k > 2048:
+        B = (B.float() * 0.05).to(dtype)
+    bst = B.t().contiguous() if tb else B
+    a_buf = torch.zeros(m, k + pad, dtype=dtype)
+    a_buf[:, :k] = A
+    b_buf = torch.zeros(bst.shape[0], bst.shape[1] + pad, dtype=dtype)
+    b_buf[:, :bst.shape[1]] = bst
+    ad, bd = a_buf.to(DEV), b_buf.to(DEV)
+    d = torch.empty(m, n, dtype=dtype, device=DEV)
+    _capi.call("sph_gemm", DT[dtype], 0, int(tb), m, n, k, 1.0, _p(ad), k + pad, _p(bd),
+               bst.shape[1] + pad, 0.0, None, 0, 0, _p(d), n, 0, _stream())
+    _sync()
+    tol = dict(rtol=1e-2, atol=1e-2) if dtype == torch.float16 else dict(rtol=2e-2, atol=2e-2)
+    assert_close_fp(d, O.gemm(A.float().numpy(), B.float().numpy()), out_dtype=dtype,
+                    what="direct-load gemm", **tol)
+
+
+@pytest.mark.parametrize("tb", [False, True])
+def test_gemm_whole_tile_epilogue_and_batch(tb):
+    # direct-load kernel with alpha / beta / per-column C / SiLU, and batched
+    _log(f"gemm direct-load epilogue/batch tb={tb}")
+    m, n, k = 512, 256, 256
+    A, B = uniform((m, k), k=23), uniform((k, n), k=24)
+    bias = uniform((n,), k=25)
+    bst = B.t().contiguous() if tb else B
+    d = _gemm(A.to(DEV), bst.to(DEV), trans_b=tb, alpha=0.5, beta=1.5, c=bias.to(DEV), crow=0,
+              ccol=1, epi=3)
+    want = O.gemm(A.numpy(), B.numpy(), alpha=0.5, beta=1.5, c=bias.numpy()[None, :],
+                  epilogue="silu")
+    assert_close_fp(d, want, what="direct-load silu epilogue")
+    batch = 3
+    Ab, Bb = uniform((batch, m, k), k=26), uniform((batch, k, n), k=27)
+    ad = Ab.to(DEV)
+    bd = (Bb.transpose(1, 2).contiguous() if tb else Bb).to(DEV)
+    out = torch.empty(batch, m, n, dtype=torch.float16, device=DEV)
+    _capi.call("sph_gemm_strided_batched", _capi.F16, 0, int(tb), batch, m, n, k, 1.0, _p(ad), k,
+               m * k, _p(bd), k if tb else n, k * n, 0.0, None, 0, 0, 0, _p(out), n, m * n, 0,
+               _stream())
+    _sync()
+    assert_close_fp(out, O.gemm(Ab.numpy(), Bb.numpy()), what="direct-load batched")
+
+
 def test_gemm_bf16_and_unaligned_ld():
     _log("gemm bf16 / unaligned")
     A, B = uniform((70, 45), k=7, dtype=torch.bfloat16), uniform((45, 33), k=8, dtype=torch.bfloat16)

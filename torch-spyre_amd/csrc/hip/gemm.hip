@@ -500,6 +500,272 @@ gemm_kernel(const GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Whole 256x256 tiles with A K-contiguous: direct global -> LDS loads.
+//
+//   * Each 64-deep K tile moves from memory into LDS with
+//     buffer_load_dwordx4 ... lds: no VGPR staging and no LDS write
+//     instructions.  Lane l's 16 bytes land at line base + 16 l (one 1 KB
+//     line per instruction), so the swizzled LDS layout is produced by
+//     choosing which 16 global bytes each lane fetches.  The loads are
+//     raw-buffer loads whose range ends where the tile's operand rows end:
+//     an offset past it reads zeros instead of touching other memory.
+//   * A (and a K-contiguous B) sits K-contiguous in LDS with the swizzle of
+//     the register-staged kernel.  A row-major B ([K, N], N contiguous) sits
+//     as 64 K rows of 256 N values; its MFMA fragments are read with
+//     ds_read_b64_tr_b16, which works on groups of 16 lanes: lane 4e + q
+//     points at 4 consecutive values of one row and lane i receives value
+//     i % 4 of the rows addressed by lanes i / 4, 4 + i / 4, 8 + i / 4,
+//     12 + i / 4.  Pointing lane 4e + q at (k0 + e, n0 + 4q) therefore gives
+//     lane i the column n0 + i at k0 .. k0 + 3, half of a B fragment.  Row
+//     k's 16-byte chunk c is stored at slot c ^ 4 (k & 3): the 4 rows x 4
+//     chunks a half-wave reads then cover all 64 banks.
+//   * Two LDS stages.  The K step is ordered by hand (sched_barrier): each of
+//     the four 16-deep MFMA sub-steps issues its MFMAs one-for-one with the
+//     LDS reads of the next sub-step's fragments.  Before sub-step 3 a wave
+//     waits for its own DMA of the next tile and its own LDS reads, then
+//     joins the barrier; sub-step 3 then also issues the DMA of the tile
+//     after next into the stage just vacated and reads the next tile's
+//     first fragments.  (Reading two sub-steps ahead measured no faster.)  Past the last tile the DMA re-loads the last tile
+//     and the fragment reads fetch values nobody uses, so the loop has no
+//     branches.
+//   * The DMA is issued from inline asm: as an intrinsic, the compiler waits
+//     for every outstanding LDS DMA before any later LDS read (it cannot tell
+//     the stages apart), which would serialise load and compute.  Completion
+//     is awaited explicitly (vmcnt) before the barrier.
+//   * 8 waves (2 x 4, two per SIMD), each owning a 128 x 64 block of 32x32
+//     MFMA tiles; epilogue as in the register-staged kernel.
+// ---------------------------------------------------------------------------
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+#define SPH_LDS __attribute__((address_space(3)))
+
+// Raw buffer resource over [base, base + bytes) (stride 0; gfx9 dword 3).
+__device__ inline i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(static_cast<uint32_t>(a)));
+  r[1] = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(static_cast<uint32_t>(a >> 32) & 0xffffu));
+  r[2] = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(bytes));
+  r[3] = 0x00020000;
+  return r;
+}
+
+// 16 bytes per lane from rsrc[voff + soff] into LDS at lds_addr + 16 * lane.
+__device__ inline void dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory", "m0");
+}
+template <int N>
+__device__ inline void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ inline void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+namespace dl {
+constexpr int BM = 256, BN = 256, BKD = 64, WM = 2, WN = 4, NW = WM * WN, NT = NW * 64;
+constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
+constexpr int CPR = BKD / 8;                    // 16-byte chunks per K row
+constexpr int A_BYTES = BM * BKD * 2, B_BYTES = BN * BKD * 2, STAGE = A_BYTES + B_BYTES;
+constexpr int LPW = A_BYTES / 1024 / NW;         // 1 KB DMA lines per wave per operand
+constexpr int KK = BKD / 16;                     // MFMA sub-steps per K tile
+constexpr int P = 1;                             // fragment prefetch distance (sub-steps)
+constexpr int NB = 2;                            // fragment buffers (kk % NB)
+constexpr int NMF = TM * TN;                     // MFMAs per sub-step
+constexpr int EPITCH = WTN + 8;
+static_assert(LPW * NW * 1024 == A_BYTES, "DMA lines");
+static_assert(P * NMF >= 2 * LPW, "DMA fits in the post-barrier sub-steps");
+static_assert(NW * 32 * EPITCH * 4 <= 2 * STAGE, "epilogue staging exceeds LDS");
+// K-contiguous row r, chunk c -> 16-byte slot (c ^ ((r >> 1) & 7)).
+__device__ inline int kslot(int r, int c) { return r * CPR + (c ^ ((r >> 1) & 7)); }
+}  // namespace dl
+
+template <typename T, bool B_KCONT>
+__global__ void __launch_bounds__(dl::NT) gemm_dl_kernel(const GemmArgs p) {
+  using namespace dl;
+  constexpr int NBR = B_KCONT ? 1 : 2;           // LDS reads per B fragment
+  constexpr int NDS = TM + TN * NBR;             // LDS reads per sub-step
+  static_assert(NDS <= NMF, "one read per MFMA");
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+
+  int tm, tn;
+  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int64_t batch = blockIdx.y;
+  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+  const uint16_t* A = static_cast<const uint16_t*>(p.a) + batch * p.stride_a;
+  const uint16_t* B = static_cast<const uint16_t*>(p.b) + batch * p.stride_b;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int lda = static_cast<int>(p.lda), ldb = static_cast<int>(p.ldb);
+  const int ksteps = static_cast<int>(p.k / BKD);
+
+  // Buffer ranges: exactly the bytes this tile's rows (columns) span.
+  const i32x4 ra = buffer_rsrc(A + m0 * lda, static_cast<uint32_t>(((BM - 1) * static_cast<int64_t>(lda) + p.k) * 2));
+  const i32x4 rb = B_KCONT
+      ? buffer_rsrc(B + n0 * ldb, static_cast<uint32_t>(((BN - 1) * static_cast<int64_t>(ldb) + p.k) * 2))
+      : buffer_rsrc(B + n0, static_cast<uint32_t>(((p.k - 1) * ldb + BN) * 2));
+  // Per-lane global byte offsets of this wave's DMA lines (K tile 0).
+  uint32_t va[LPW], vb[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int s = (wave * LPW + i) * 64 + lane;  // LDS slot filled by this lane
+    {
+      const int r = s / CPR, c = (s % CPR) ^ ((r >> 1) & 7);
+      va[i] = static_cast<uint32_t>(r * lda * 2 + c * 16);
+    }
+    if constexpr (B_KCONT) {
+      const int r = s / CPR, c = (s % CPR) ^ ((r >> 1) & 7);
+      vb[i] = static_cast<uint32_t>(r * ldb * 2 + c * 16);
+    } else {
+      const int k = s >> 5, c = (s & 31) ^ (4 * (k & 3));
+      vb[i] = static_cast<uint32_t>(k * ldb * 2 + c * 16);
+    }
+  }
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((SPH_LDS char*)(lds)));
+  const int row_in = lane & 31, khalf = lane >> 5;
+  int boff[TN];  // row-major B: byte offset of this lane's transpose-read pointer
+  {
+    const int g = lane >> 4, jj = lane & 15, e = jj >> 2, q = jj & 3;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = wn * WTN + j * 32 + 16 * (g & 1) + 4 * q;
+      const int k = 8 * (g >> 1) + e;
+      boff[j] = A_BYTES + k * (BN * 2) + (((n >> 3) ^ (4 * e)) << 4) + 8 * (q & 1);
+    }
+  }
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  u32x4 af[NB][TM];
+  u32x2 bl[NB][TN], bh[NB][TN];
+
+// LDS read number X (0 .. NDS-1) of sub-step KK_'s fragments from the stage at
+// byte offset STB_, into buffer BUF_.  Order: A0, the B fragments, A1 ..: the
+// first MFMAs of a sub-step need A0 and all of B.
+#define SPH_DL_READ(BUF_, X_, STB_, KK_)                                                    \
+  do {                                                                                      \
+    const int x_ = (X_);                                                                    \
+    const char* st_ = lds + (STB_);                                                         \
+    if (x_ == 0 || x_ > TN * NBR) {                                                         \
+      const int i_ = x_ == 0 ? 0 : x_ - TN * NBR;                                           \
+      const int r_ = wm * WTM + i_ * 32 + row_in;                                          \
+      af[BUF_][i_] = *reinterpret_cast<const u32x4*>(st_ + kslot(r_, (KK_) * 2 + khalf) * 16); \
+    } else if constexpr (B_KCONT) {                                                         \
+      const int j_ = x_ - 1;                                                                \
+      const int r_ = wn * WTN + j_ * 32 + row_in;                                          \
+      const u32x4 v_ =                                                                      \
+          *reinterpret_cast<const u32x4*>(st_ + A_BYTES + kslot(r_, (KK_) * 2 + khalf) * 16); \
+      bl[BUF_][j_] = u32x2{v_[0], v_[1]};                                                   \
+      bh[BUF_][j_] = u32x2{v_[2], v_[3]};                                                   \
+    } else {                                                                                \
+      const int j_ = (x_ - 1) >> 1, h_ = (x_ - 1) & 1;                                      \
+      const SPH_LDS char* p_ =                                                              \
+          (const SPH_LDS char*)(st_) + boff[j_] + ((KK_) * 16 + 4 * h_) * (BN * 2);         \
+      const u32x2 v_ = __builtin_bit_cast(                                                  \
+          u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((SPH_LDS s16x4*)(p_)));            \
+      if (h_) bh[BUF_][j_] = v_;                                                            \
+      else bl[BUF_][j_] = v_;                                                               \
+    }                                                                                       \
+  } while (0)
+#define SPH_DL_MFMA(BUF_, X_)                                                               \
+  do {                                                                                      \
+    const int i_ = (X_) / TN, j_ = (X_) % TN;                                               \
+    const u32x4 b_ = __builtin_shufflevector(bl[BUF_][j_], bh[BUF_][j_], 0, 1, 2, 3);       \
+    acc[i_][j_] = mfma32<T>(af[BUF_][i_], b_, acc[i_][j_]);                                 \
+  } while (0)
+// DMA line LINE_ (A lines first, then B) of K tile T_ into stage SL_ & 1.
+#define SPH_DL_DMA(T_, SL_, LINE_)                                                          \
+  do {                                                                                      \
+    const int t_ = (T_), l_ = (LINE_);                                                      \
+    const uint32_t wb_ = __builtin_amdgcn_readfirstlane(lds_base + ((SL_) & 1) * STAGE +    \
+                                                        wave * LPW * 1024);                 \
+    if (l_ < LPW)                                                                           \
+      dma16(ra, wb_ + l_ * 1024, va[l_], __builtin_amdgcn_readfirstlane(t_ * BKD * 2));     \
+    else                                                                                    \
+      dma16(rb, wb_ + A_BYTES + (l_ - LPW) * 1024, vb[l_ - LPW],                             \
+            __builtin_amdgcn_readfirstlane(B_KCONT ? t_ * BKD * 2 : t_ * BKD * ldb * 2));   \
+  } while (0)
+
+  // Prologue: K tiles 0 and 1 in flight; wait for tile 0; fragments of the
+  // first P sub-steps.
+#pragma unroll
+  for (int l = 0; l < 2 * LPW; ++l) SPH_DL_DMA(0, 0, l);
+  if (ksteps > 1) {
+#pragma unroll
+    for (int l = 0; l < 2 * LPW; ++l) SPH_DL_DMA(1, 1, l);
+    wait_vmcnt<2 * LPW>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  __syncthreads();
+#pragma unroll
+  for (int kk = 0; kk < P; ++kk)
+#pragma unroll
+    for (int x = 0; x < NDS; ++x) SPH_DL_READ(kk % NB, x, 0, kk);
+
+  for (int ks = 0; ks < ksteps; ++ks) {
+    const int cs = (ks & 1) * STAGE, ns = ((ks + 1) & 1) * STAGE;
+    const int tnext = ks + 2 < ksteps ? ks + 2 : ksteps - 1;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      if (kk == KK - P) {
+        // This wave's DMA of tile ks+1 has landed and its reads of tile ks
+        // are complete; past the barrier every wave is.
+        wait_vmcnt<0>();
+        wait_lgkmcnt0();
+        __syncthreads();
+      }
+#pragma unroll
+      for (int x = 0; x < NMF; ++x) {
+        SPH_DL_MFMA(kk % NB, x);
+        if (x < NDS) {
+          if (kk + P < KK)
+            SPH_DL_READ((kk + P) % NB, x, cs, kk + P);
+          else
+            SPH_DL_READ((kk + P) % NB, x, ns, kk + P - KK);
+        }
+        if (kk >= KK - P) {
+          const int d = (kk - (KK - P)) * NMF + x;
+          if (d < 2 * LPW) SPH_DL_DMA(tnext, ks, d);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+#undef SPH_DL_READ
+#undef SPH_DL_MFMA
+#undef SPH_DL_DMA
+
+  // Epilogue (LDS reused as fp32 slabs once every DMA has landed).
+  wait_vmcnt<0>();
+  __syncthreads();
+  T* D = static_cast<T*>(p.d) + batch * p.stride_d;
+  const T* C = p.c ? static_cast<const T*>(p.c) + batch * p.stride_c : nullptr;
+  float* slab = reinterpret_cast<float*>(lds) + wave * (32 * EPITCH);
+  const int64_t row0 = m0 + wm * WTM;
+  const int64_t colw = n0 + wn * WTN;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        slab[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * EPITCH + j * 32 + (lane & 31)] =
+            acc[i][j][r];
+    __syncthreads();
+    store_slab<T, WTN, EPITCH>(p, slab, D, C, row0 + i * 32, colw, lane);
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Small-M products: D[m, n] = epi(alpha * sum_k A[m, k] * B[n, k] + beta*C)
 // for M <= MT rows, A and B K-contiguous and 16-byte aligned, K % 8 == 0.
 // A group of TPR threads computes R output columns n for all M rows: thread t
@@ -728,8 +994,19 @@ void launch_full(const GemmArgs& p, dim3 grid, dim3 block, bool a_kcont, bool b_
     gemm_kernel<T, BM, BN, WM, WN, false, false, FULL><<<grid, block, 0, st>>>(p);
 }
 
-// Launches BM x BN tiles: whole tiles with the FULL kernel on WMF x WNF
-// waves, otherwise the checked kernel on WMP x WNP waves.
+// The direct-load kernel addresses a tile's operand rows with 32-bit buffer
+// offsets: every byte it may touch must lie within 2^31 of the tile origin.
+inline bool dl_fits(const GemmArgs& p, bool b_kcont) {
+  constexpr int64_t kLim = (1LL << 31) - 1;
+  if (p.lda > kLim / 2 || p.ldb > kLim / 2) return false;
+  const int64_t a_bytes = ((dl::BM - 1) * p.lda + p.k) * 2;
+  const int64_t b_bytes = b_kcont ? ((dl::BN - 1) * p.ldb + p.k) * 2 : ((p.k - 1) * p.ldb + dl::BN) * 2;
+  return a_bytes < kLim && b_bytes < kLim;
+}
+
+// Launches BM x BN tiles: whole 256x256 tiles with K-contiguous A on the
+// direct-load kernel, other whole tiles with the FULL register-staged kernel
+// on WMF x WNF waves, otherwise the checked kernel on WMP x WNP waves.
 template <typename T, int BM, int BN, int WMF, int WNF, int WMP, int WNP>
 int launch_cfg(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
                hipStream_t st) {
@@ -740,7 +1017,12 @@ int launch_cfg(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
   // alignment checks in the K loop.
   const bool full = p.m % BM == 0 && p.n % BN == 0 && p.k % BK == 0 && p.k > 0 &&
                     p.vec_a && p.vec_b;
-  if (full)
+  if (full && BM == dl::BM && BN == dl::BN && a_kcont && dl_fits(p, b_kcont)) {
+    if (b_kcont)
+      gemm_dl_kernel<T, true><<<grid, dim3(dl::NT), 0, st>>>(p);
+    else
+      gemm_dl_kernel<T, false><<<grid, dim3(dl::NT), 0, st>>>(p);
+  } else if (full)
     launch_full<T, BM, BN, WMF, WNF, true>(p, grid, dim3(WMF * WNF * 64), a_kcont, b_kcont, st);
   else
     launch_full<T, BM, BN, WMP, WNP, false>(p, grid, dim3(WMP * WNP * 64), a_kcont, b_kcont, st);
