@@ -155,7 +155,18 @@ def bench_extra(steps, warmup, stream, capi):
                                                      yy.data_ptr(), rs.data_ptr(), R, C, s))
     del x, r, yy, h
 
-    # c2 bmm 32 x [2048,128] x [128,2048]: HBM-bound (AI 113.8 < ridge 314.6)
+    out.update(bench_bmm(steps, warmup, stream, capi))
+    return out
+
+
+def bench_bmm(steps, warmup, stream, capi):
+    """c2 bmm 32 x [2048,128] x [128,2048]: HBM-bound (AI 113.8 < ridge 314.6)."""
+    import torch
+
+    s = stream.cuda_stream
+    lib = capi.lib()
+    out = {}
+    timer = Timer(stream)
     Bt, M, N, K = 32, 2048, 2048, 128
     A = (torch.rand(Bt, M, K, generator=_gen(0)) * 2 - 1).half().cuda()
     Bm = (torch.rand(Bt, K, N, generator=_gen(1)) * 2 - 1).half().cuda()
@@ -434,8 +445,8 @@ def main(argv=None):
     ap.add_argument("--no-decoder", action="store_true")
     ap.add_argument("--c5-layers", type=int, default=40)
     ap.add_argument("--decode-steps", type=int, default=128)
-    ap.add_argument("--kernel", choices=["all", "gemm", "copy", "decoder"], default="all",
-                    help="gemm / copy / decoder: run only that part (for rocprofv3 passes)")
+    ap.add_argument("--kernel", choices=["all", "gemm", "copy", "decoder", "bmm"], default="all",
+                    help="gemm / copy / decoder / bmm: run only that part (for rocprofv3 passes)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; runs on more than one GPU are not "
@@ -452,6 +463,9 @@ def main(argv=None):
     stream = torch.cuda.current_stream()
     if args.kernel == "copy":
         print(json.dumps({"kernel": "copy", **bench_copy(args.steps, args.warmup, stream, _capi)}))
+        return 0
+    if args.kernel == "bmm":
+        print(json.dumps({"kernel": "bmm", **bench_bmm(args.steps, args.warmup, stream, _capi)}))
         return 0
     if args.kernel == "decoder":
         print(json.dumps({"kernel": "decoder",

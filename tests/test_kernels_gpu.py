@@ -177,7 +177,7 @@ def test_norm_fp32_weight_and_bf16():
 # ---------------------------------------------------------------------------
 # GELU chain
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("rows,cols", [(8192, 4096), (3, 100), (2, 70000)])
+@pytest.mark.parametrize("rows,cols", [(8192, 4096), (3, 100), (2, 70000), (7, 2048), (5, 8192)])
 def test_gelu_affine_rowsum(rows, cols):
     _log(f"gelu_rowsum {rows}x{cols}")
     x = randn((rows, cols), k=0)
@@ -192,6 +192,34 @@ def test_gelu_affine_rowsum(rows, cols):
     y, r = O.gelu_affine_rowsum(x.numpy(), s.numpy(), b.numpy())
     assert_close_fp(yd, y, what="gelu y")
     assert_close_fp(rd, r, what="gelu rowsum")
+
+
+def test_gelu_whole_row_bf16_and_tails():
+    # whole-row path (cols = 2048 * k) in bf16, and the GELU tails: x over
+    # [-12, 12] against the oracle's erf form (the device evaluates erfc by
+    # Abramowitz & Stegun 7.1.26, absolute error below 5e-7)
+    _log("gelu whole-row bf16 / tails")
+    rows, cols = 6, 4096
+    x = (torch.linspace(-12, 12, rows * cols).view(rows, cols)).to(torch.bfloat16)
+    s = torch.ones(cols, dtype=torch.bfloat16)
+    b = torch.zeros(cols, dtype=torch.bfloat16)
+    xd, sd, bd = x.to(DEV), s.to(DEV), b.to(DEV)
+    yd = torch.empty_like(xd)
+    rd = torch.empty(rows, dtype=torch.bfloat16, device=DEV)
+    _capi.call("sph_gelu_affine_rowsum", _capi.BF16, _p(xd), _p(sd), _p(bd), 1.0, 0.0, _p(yd),
+               _p(rd), rows, cols, _stream())
+    _sync()
+    y, r = O.gelu_affine_rowsum(x.float().numpy(), s.float().numpy(), b.float().numpy())
+    assert_close_fp(yd, y, out_dtype=torch.bfloat16, rtol=2e-2, atol=2e-2, what="gelu bf16 y")
+    assert_close_fp(rd, r, out_dtype=torch.bfloat16, rtol=2e-2, atol=2e-2, what="gelu bf16 rowsum")
+    xf = torch.linspace(-12, 12, 4 * 2048).view(4, 2048).half()
+    xd = xf.to(DEV)
+    yd = torch.empty_like(xd)
+    _capi.call("sph_gelu_affine_rowsum", _capi.F16, _p(xd), None, None, 1.0, 0.0, _p(yd), None,
+               4, 2048, _stream())
+    _sync()
+    y, _ = O.gelu_affine_rowsum(xf.float().numpy(), np.float32(1.0), np.float32(0.0))
+    assert_close_fp(yd, y, rtol=1e-3, atol=1e-3, what="gelu tails")
 
 
 def test_gelu_scalar_affine():
@@ -289,6 +317,33 @@ def test_gemm_whole_tile_direct_load(m, n, k, tb, pad, dtype):
     tol = dict(rtol=1e-2, atol=1e-2) if dtype == torch.float16 else dict(rtol=2e-2, atol=2e-2)
     assert_close_fp(d, O.gemm(A.float().numpy(), B.float().numpy()), out_dtype=dtype,
                     what="direct-load gemm", **tol)
+
+
+@pytest.mark.parametrize("batch,m,n,k,tb,pad", [(1, 128, 128, 64, False, 0), (2, 256, 384, 64, True, 8),
+                                                (3, 384, 128, 128, False, 64), (4, 128, 256, 128, True, 0),
+                                                (32, 2048, 2048, 128, True, 0)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_gemm_short_k(batch, m, n, k, tb, pad, dtype):
+    # K = 64 / 128 on whole 128x128 tiles: the short-K kernel (attention
+    # scores), batched, both B layouts, padded leading dimensions
+    _log(f"gemm short-K b={batch} {m}x{n}x{k} tb={tb} pad={pad} {dtype}")
+    A = uniform((batch, m, k), k=31, dtype=dtype)
+    B = uniform((batch, k, n), k=32, dtype=dtype)
+    bst = B.transpose(1, 2).contiguous() if tb else B
+    a_buf = torch.zeros(batch, m, k + pad, dtype=dtype)
+    a_buf[:, :, :k] = A
+    b_buf = torch.zeros(batch, bst.shape[1], bst.shape[2] + pad, dtype=dtype)
+    b_buf[:, :, :bst.shape[2]] = bst
+    ad, bd = a_buf.to(DEV), b_buf.to(DEV)
+    out = torch.empty(batch, m, n, dtype=dtype, device=DEV)
+    lda, ldb = k + pad, bst.shape[2] + pad
+    _capi.call("sph_gemm_strided_batched", DT[dtype], 0, int(tb), batch, m, n, k, 1.0, _p(ad), lda,
+               a_buf[0].numel(), _p(bd), ldb, b_buf[0].numel(), 0.0, None, 0, 0, 0, _p(out), n,
+               m * n, 0, _stream())
+    _sync()
+    tol = dict(rtol=1e-2, atol=1e-2) if dtype == torch.float16 else dict(rtol=2e-2, atol=2e-2)
+    assert_close_fp(out, O.gemm(A.float().numpy(), B.float().numpy()), out_dtype=dtype,
+                    what="short-K gemm", **tol)
 
 
 @pytest.mark.parametrize("tb", [False, True])

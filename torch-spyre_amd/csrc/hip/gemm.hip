@@ -766,6 +766,156 @@ __global__ void __launch_bounds__(dl::NT) gemm_dl_kernel(const GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Short-K products (K = 64 or 128; e.g. attention scores Q K^T with head
+// dim 128): at 2 M N K FLOP against 2 M N bytes of output they are bound by
+// memory.  Design:
+//   * 128x128 tiles on 4 waves (64x64 each); the whole K range is one LDS
+//     stage (64 KB at K = 128), so two workgroups share a CU and one's
+//     operand loads overlap the other's MFMAs and stores.  (A persistent
+//     one-workgroup-per-CU variant with a two-stage operand ring, with and
+//     without producer/consumer wave roles, measured slower: its DMA keeps
+//     at most one tile in flight per CU, and under the output stream the
+//     load latency, not bandwidth, then sets the pace.)
+//   * Operands arrive by direct global->LDS DMA as in the whole-tile kernel
+//     (one 64-deep K block after another, same layouts; row-major B rows
+//     are 256 bytes here and use chunk slot c ^ 4 (k & 3)).
+//   * The MFMAs take B as the first operand, so each lane's accumulators
+//     hold 4 consecutive output columns of one row: converted to T they are
+//     8-byte LDS writes into a per-wave 64 x 64 slab (16-byte chunk c of row
+//     m at slot c ^ ((m >> 1) & 7)), read back as whole 128-byte rows and
+//     stored with 16-byte stores.
+//   * Plain products only (alpha = 1, no C, no activation): D rounds each
+//     fp32 sum once.
+// ---------------------------------------------------------------------------
+namespace sk {
+constexpr int BM = 128, BN = 128, WM = 2, WN = 2, NW = WM * WN, NT = NW * 64;
+constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
+constexpr int KB = 64;                           // K block (one A and one B block per 64 K)
+constexpr int A_BLK = BM * KB * 2, B_BLK = BN * KB * 2;  // 16 KB each
+constexpr int LPW = A_BLK / 1024 / NW;           // DMA lines per wave per block
+constexpr int SLAB = WTM * WTN * 2;              // per-wave output slab (bytes)
+static_assert(LPW * NW * 1024 == A_BLK, "DMA lines");
+__device__ inline int aslot(int r, int c) { return r * 8 + (c ^ ((r >> 1) & 7)); }
+}  // namespace sk
+
+template <typename T, bool B_KCONT, int KT>
+__global__ void __launch_bounds__(sk::NT) gemm_shortk_kernel(const GemmArgs p) {
+  using namespace sk;
+  constexpr int OPS = KT * (A_BLK + B_BLK);
+  static_assert(NW * SLAB <= OPS, "slab fits in the operand space");
+  __shared__ __attribute__((aligned(1024))) char lds[OPS];
+  int tm, tn;
+  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int64_t batch = blockIdx.y;
+  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+  const uint16_t* A = static_cast<const uint16_t*>(p.a) + batch * p.stride_a;
+  const uint16_t* B = static_cast<const uint16_t*>(p.b) + batch * p.stride_b;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int lda = static_cast<int>(p.lda), ldb = static_cast<int>(p.ldb);
+
+  const i32x4 ra = buffer_rsrc(A + m0 * lda, static_cast<uint32_t>(((BM - 1) * static_cast<int64_t>(lda) + p.k) * 2));
+  const i32x4 rb = B_KCONT
+      ? buffer_rsrc(B + n0 * ldb, static_cast<uint32_t>(((BN - 1) * static_cast<int64_t>(ldb) + p.k) * 2))
+      : buffer_rsrc(B + n0, static_cast<uint32_t>(((p.k - 1) * ldb + BN) * 2));
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((SPH_LDS char*)(lds)));
+#pragma unroll
+  for (int kb = 0; kb < KT; ++kb) {
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int line = wave * LPW + i;
+      const int s = line * 64 + lane;
+      const int r = s >> 3, c = (s & 7) ^ ((r >> 1) & 7);
+      dma16(ra, __builtin_amdgcn_readfirstlane(lds_base + kb * A_BLK + line * 1024),
+            static_cast<uint32_t>(r * lda * 2 + c * 16), __builtin_amdgcn_readfirstlane(kb * KB * 2));
+      uint32_t vb;
+      if constexpr (B_KCONT) {
+        vb = static_cast<uint32_t>(r * ldb * 2 + c * 16);
+      } else {
+        const int k = s >> 4, cb = (s & 15) ^ (4 * (k & 3));
+        vb = static_cast<uint32_t>(k * ldb * 2 + cb * 16);
+      }
+      dma16(rb, __builtin_amdgcn_readfirstlane(lds_base + KT * A_BLK + kb * B_BLK + line * 1024), vb,
+            __builtin_amdgcn_readfirstlane(B_KCONT ? kb * KB * 2 : kb * KB * ldb * 2));
+    }
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  const int row_in = lane & 31, khalf = lane >> 5;
+  const int g = lane >> 4, jj = lane & 15, e = jj >> 2, q = jj & 3;
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+#pragma unroll
+  for (int kb = 0; kb < KT; ++kb) {
+    const char* sa = lds + kb * A_BLK;
+    const char* sb = lds + KT * A_BLK + kb * B_BLK;
+#pragma unroll
+    for (int kk = 0; kk < KB / 16; ++kk) {
+      u32x4 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const u32x4*>(sa + aslot(wm * WTM + i * 32 + row_in, kk * 2 + khalf) * 16);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        if constexpr (B_KCONT) {
+          bf[j] = *reinterpret_cast<const u32x4*>(sb + aslot(wn * WTN + j * 32 + row_in, kk * 2 + khalf) * 16);
+        } else {
+          const int n = wn * WTN + j * 32 + 16 * (g & 1) + 4 * q;
+          const int k = kk * 16 + 8 * (g >> 1) + e;
+          const SPH_LDS char* p0 =
+              (const SPH_LDS char*)(sb) + k * (BN * 2) + (((n >> 3) ^ (4 * e)) << 4) + 8 * (q & 1);
+          const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((SPH_LDS s16x4*)(p0)));
+          const u32x2 hi = __builtin_bit_cast(
+              u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((SPH_LDS s16x4*)(p0 + 4 * BN * 2)));
+          bf[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32<T>(bf[j], af[i], acc[i][j]);
+    }
+  }
+  // acc[i][j][r]: row m = i*32 + lane%32, columns n = j*32 + 8*(r/4) + 4*(lane/32) + r%4
+  __syncthreads();
+  char* slab = lds + wave * SLAB;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = i * 32 + row_in;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int n = j * 32 + 8 * rg + 4 * khalf;
+        uint32_t w[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint16_t lo = __builtin_bit_cast(uint16_t, Num<T>::from_f(acc[i][j][4 * rg + 2 * h]));
+          const uint16_t hi = __builtin_bit_cast(uint16_t, Num<T>::from_f(acc[i][j][4 * rg + 2 * h + 1]));
+          w[h] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+        }
+        const int c = n >> 3;
+        *reinterpret_cast<u32x2*>(slab + (m * 8 + (c ^ ((m >> 1) & 7))) * 16 + (n & 7) * 2) =
+            u32x2{w[0], w[1]};
+      }
+  }
+  // The slab belongs to this wave alone; a wave's LDS accesses run in order.
+  T* D = static_cast<T*>(p.d) + batch * p.stride_d;
+#pragma unroll
+  for (int it = 0; it < WTM / 8; ++it) {
+    const int m = it * 8 + (lane >> 3), c = lane & 7;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(slab + (m * 8 + (c ^ ((m >> 1) & 7))) * 16);
+    *reinterpret_cast<u32x4*>(D + (m0 + wm * WTM + m) * p.ldd + n0 + wn * WTN + c * 8) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Small-M products: D[m, n] = epi(alpha * sum_k A[m, k] * B[n, k] + beta*C)
 // for M <= MT rows, A and B K-contiguous and 16-byte aligned, K % 8 == 0.
 // A group of TPR threads computes R output columns n for all M rows: thread t
@@ -1004,6 +1154,21 @@ inline bool dl_fits(const GemmArgs& p, bool b_kcont) {
   return a_bytes < kLim && b_bytes < kLim;
 }
 
+// Short-K kernel: K of 64 or 128, whole 128x128 tiles, K-contiguous A,
+// 16-byte aligned rows everywhere, plain product, 32-bit buffer offsets.
+inline bool shortk_fits(const GemmArgs& p, bool a_kcont, bool b_kcont) {
+  if (!(p.k == 64 || p.k == 128) || p.m % sk::BM != 0 || p.n % sk::BN != 0 || !a_kcont ||
+      !p.vec_a || !p.vec_b || !p.vec_d || p.alpha != 1.f || p.c != nullptr ||
+      p.epilogue != SPH_EPI_NONE)
+    return false;
+  if (p.m / sk::BM * (p.n / sk::BN) >= (1LL << 31)) return false;
+  constexpr int64_t kLim = (1LL << 31) - 1;
+  if (p.lda > kLim / 2 || p.ldb > kLim / 2) return false;
+  const int64_t a_bytes = ((sk::BM - 1) * p.lda + p.k) * 2;
+  const int64_t b_bytes = b_kcont ? ((sk::BN - 1) * p.ldb + p.k) * 2 : ((p.k - 1) * p.ldb + sk::BN) * 2;
+  return a_bytes < kLim && b_bytes < kLim;
+}
+
 // Launches BM x BN tiles: whole 256x256 tiles with K-contiguous A on the
 // direct-load kernel, other whole tiles with the FULL register-staged kernel
 // on WMF x WNF waves, otherwise the checked kernel on WMP x WNP waves.
@@ -1040,6 +1205,19 @@ int gemm_dispatch(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
   if (p.m <= 16 && a_kcont && b_kcont && p.vec_a && p.vec_b && p.k > 0 && p.k % 8 == 0 &&
       ceil_div(p.n, 2) < (1LL << 40))
     return launch_skinny<T>(p, batch, st);
+  if (shortk_fits(p, a_kcont, b_kcont)) {
+    p.tiles_m = static_cast<int>(p.m / sk::BM);
+    p.tiles_n = static_cast<int>(p.n / sk::BN);
+    dim3 grid(static_cast<unsigned>(p.tiles_m) * p.tiles_n, static_cast<unsigned>(batch));
+    if (p.k == 64) {
+      if (b_kcont) gemm_shortk_kernel<T, true, 1><<<grid, dim3(sk::NT), 0, st>>>(p);
+      else gemm_shortk_kernel<T, false, 1><<<grid, dim3(sk::NT), 0, st>>>(p);
+    } else {
+      if (b_kcont) gemm_shortk_kernel<T, true, 2><<<grid, dim3(sk::NT), 0, st>>>(p);
+      else gemm_shortk_kernel<T, false, 2><<<grid, dim3(sk::NT), 0, st>>>(p);
+    }
+    return check_launch("sph_gemm (short K)");
+  }
   const int64_t t256 = ceil_div(p.m, 256) * ceil_div(p.n, 256) * batch;
   const int64_t t128 = ceil_div(p.m, 128) * ceil_div(p.n, 128) * batch;
   // 256x256 whole tiles run 8 waves (128x64 each, two per SIMD, so one

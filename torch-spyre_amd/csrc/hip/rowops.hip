@@ -355,6 +355,80 @@ gelu_rowsum_regs(const T* __restrict__ x, const T* __restrict__ sv,
   if (rowsum && t == 0) rowsum[row] = Num<T>::from_f(acc);
 }
 
+// Whole-row path for rows of exactly 2048 * VPT 16-bit values (16-byte
+// aligned): a workgroup of 256 threads handles RPW consecutive rows.  The
+// per-column scale and shift are loaded and widened once per thread and
+// reused for every row, all RPW rows' loads are issued before any math
+// (RPW * VPT 16-byte loads in flight per thread), and the RPW row sums share
+// one block reduction.  Rows past the end are clamped for loading and not
+// stored.
+template <typename T, int VPT, int RPW>
+__global__ void __launch_bounds__(256)
+gelu_rowsum_rows(const T* __restrict__ x, const T* __restrict__ sv, const T* __restrict__ bv,
+                 float s0, float b0, T* __restrict__ y, T* __restrict__ rowsum, int64_t rows) {
+  constexpr int COLS = 2048 * VPT, NWAVE = 256 / kWave;
+  __shared__ float red[NWAVE][RPW];
+  const int t = threadIdx.x;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * RPW;
+  float s[VPT][8], b[VPT][8];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int c0 = (i * 256 + t) * 8;
+    if (sv) {
+      load8<T>(sv + c0, s[i]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s[i][j] = s0;
+    }
+    if (bv) {
+      load8<T>(bv + c0, b[i]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) b[i][j] = b0;
+    }
+  }
+  u32x4 raw[RPW][VPT];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int64_t row = r0 + r < rows ? r0 + r : rows - 1;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+      raw[r][i] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(x + row * COLS + (i * 256 + t) * 8));
+  }
+  float acc[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    acc[r] = 0.f;
+    const int64_t row = r0 + r;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const T* e = reinterpret_cast<const T*>(&raw[r][i]);
+      float g[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        g[j] = gelu_erf(fmaf(Num<T>::to_f(e[j]), s[i][j], b[i][j]));
+        acc[r] += g[j];
+      }
+      if (y && row < rows) store8<T>(y + row * COLS + (i * 256 + t) * 8, g);
+    }
+  }
+  if (!rowsum) return;
+  const int wave = t / kWave, lane = t % kWave;
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const float v = wave_reduce<SumOp>(acc[r]);
+    if (lane == 0) red[wave][r] = v;
+  }
+  __syncthreads();
+  if (t < RPW && r0 + t < rows) {
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) v += red[w][t];
+    rowsum[r0 + t] = Num<T>::from_f(v);
+  }
+}
+
 template <typename T>
 __global__ void __launch_bounds__(256)
 gelu_rowsum_looped(const T* __restrict__ x, const T* __restrict__ sv,
@@ -481,8 +555,26 @@ int gelu_impl(const void* x, const void* s, const void* b, float s0, float b0,
   auto ro = static_cast<T*>(rowsum);
   const bool vec = vec_ok<T>(x, cols) && vec_ok<T>(s, cols) &&
                    vec_ok<T>(b, cols) && vec_ok<T>(y, cols);
+  if constexpr (sizeof(T) == 2) {
+    constexpr int RPW = 4;
+    const unsigned grid = static_cast<unsigned>(ceil_div(rows, RPW));
+    if (vec && rows <= 0x7fffffffLL * RPW) {
+      if (cols == 2048) {
+        gelu_rowsum_rows<T, 1, RPW><<<grid, 256, 0, st>>>(xi, si, bi, s0, b0, yo, ro, rows);
+        return check_launch("sph_gelu_affine_rowsum");
+      }
+      if (cols == 4096) {
+        gelu_rowsum_rows<T, 2, RPW><<<grid, 256, 0, st>>>(xi, si, bi, s0, b0, yo, ro, rows);
+        return check_launch("sph_gelu_affine_rowsum");
+      }
+      if (cols == 8192) {
+        gelu_rowsum_rows<T, 4, RPW><<<grid, 256, 0, st>>>(xi, si, bi, s0, b0, yo, ro, rows);
+        return check_launch("sph_gelu_affine_rowsum");
+      }
+    }
+  }
   const int cfg = pick_cfg(cols);
-#define SPH_GELU_CASE(I)                                                         \
+#define SPH_GELU_CASE(I)                                                       \
   case I: {                                                                      \
     constexpr int TPR = kCfgs[I].tpr, VPT = kCfgs[I].vpt;                        \
     if (vec)                                                                     \

