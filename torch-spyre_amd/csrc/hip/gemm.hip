@@ -565,26 +565,37 @@ __device__ inline void wait_vmcnt() {
 __device__ inline void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 namespace dl {
-constexpr int BM = 256, BN = 256, BKD = 64, WM = 2, WN = 4, NW = WM * WN, NT = NW * 64;
-constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
+// Shared by both tile widths: 256-row tiles, 64-deep K tiles, two waves
+// along M, each wave owning a 128 x 64 block of 32x32 MFMA tiles.
+constexpr int BM = 256, BKD = 64, WM = 2, WTM = 128, WTN = 64, TM = WTM / 32, TN = WTN / 32;
 constexpr int CPR = BKD / 8;                    // 16-byte chunks per K row
-constexpr int A_BYTES = BM * BKD * 2, B_BYTES = BN * BKD * 2, STAGE = A_BYTES + B_BYTES;
-constexpr int LPW = A_BYTES / 1024 / NW;         // 1 KB DMA lines per wave per operand
+constexpr int A_BYTES = BM * BKD * 2;
 constexpr int KK = BKD / 16;                     // MFMA sub-steps per K tile
 constexpr int P = 1;                             // fragment prefetch distance (sub-steps)
 constexpr int NB = 2;                            // fragment buffers (kk % NB)
 constexpr int NMF = TM * TN;                     // MFMAs per sub-step
 constexpr int EPITCH = WTN + 8;
-static_assert(LPW * NW * 1024 == A_BYTES, "DMA lines");
-static_assert(P * NMF >= 2 * LPW, "DMA fits in the post-barrier sub-steps");
-static_assert(NW * 32 * EPITCH * 4 <= 2 * STAGE, "epilogue staging exceeds LDS");
 // K-contiguous row r, chunk c -> 16-byte slot (c ^ ((r >> 1) & 7)).
 __device__ inline int kslot(int r, int c) { return r * CPR + (c ^ ((r >> 1) & 7)); }
+
+// BN = 256 (8 waves, 2 x 4) or 128 (4 waves, 2 x 2).
+template <int BN_>
+struct Cfg {
+  static constexpr int BN = BN_, WN = BN / WTN, NW = WM * WN, NT = NW * 64;
+  static constexpr int B_BYTES = BN * BKD * 2, STAGE = A_BYTES + B_BYTES;
+  static constexpr int LPA = A_BYTES / 1024 / NW, LPB = B_BYTES / 1024 / NW;  // DMA lines per wave
+  static constexpr int BCH = BN / 8;             // 16-byte chunks per row-major B row
+  static_assert(LPA * NW * 1024 == A_BYTES && LPB * NW * 1024 == B_BYTES, "DMA lines");
+  static_assert(P * NMF * 2 >= LPA + LPB, "DMA fits in the post-barrier sub-steps");
+  static_assert(NW * 32 * EPITCH * 4 <= 2 * STAGE, "epilogue staging exceeds LDS");
+};
 }  // namespace dl
 
-template <typename T, bool B_KCONT>
-__global__ void __launch_bounds__(dl::NT) gemm_dl_kernel(const GemmArgs p) {
+template <typename T, bool B_KCONT, int BN_>
+__global__ void __launch_bounds__(dl::Cfg<BN_>::NT) gemm_dl_kernel(const GemmArgs p) {
   using namespace dl;
+  using DC = Cfg<BN_>;
+  constexpr int BN = DC::BN, WN = DC::WN, STAGE = DC::STAGE, LPA = DC::LPA, LPB = DC::LPB;
   constexpr int NBR = B_KCONT ? 1 : 2;           // LDS reads per B fragment
   constexpr int NDS = TM + TN * NBR;             // LDS reads per sub-step
   static_assert(NDS <= NMF, "one read per MFMA");
@@ -607,19 +618,21 @@ __global__ void __launch_bounds__(dl::NT) gemm_dl_kernel(const GemmArgs p) {
       ? buffer_rsrc(B + n0 * ldb, static_cast<uint32_t>(((BN - 1) * static_cast<int64_t>(ldb) + p.k) * 2))
       : buffer_rsrc(B + n0, static_cast<uint32_t>(((p.k - 1) * ldb + BN) * 2));
   // Per-lane global byte offsets of this wave's DMA lines (K tile 0).
-  uint32_t va[LPW], vb[LPW];
+  uint32_t va[LPA], vb[LPB];
 #pragma unroll
-  for (int i = 0; i < LPW; ++i) {
-    const int s = (wave * LPW + i) * 64 + lane;  // LDS slot filled by this lane
-    {
-      const int r = s / CPR, c = (s % CPR) ^ ((r >> 1) & 7);
-      va[i] = static_cast<uint32_t>(r * lda * 2 + c * 16);
-    }
+  for (int i = 0; i < LPA; ++i) {
+    const int s = (wave * LPA + i) * 64 + lane;  // LDS slot filled by this lane
+    const int r = s / CPR, c = (s % CPR) ^ ((r >> 1) & 7);
+    va[i] = static_cast<uint32_t>(r * lda * 2 + c * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < LPB; ++i) {
+    const int s = (wave * LPB + i) * 64 + lane;
     if constexpr (B_KCONT) {
       const int r = s / CPR, c = (s % CPR) ^ ((r >> 1) & 7);
       vb[i] = static_cast<uint32_t>(r * ldb * 2 + c * 16);
     } else {
-      const int k = s >> 5, c = (s & 31) ^ (4 * (k & 3));
+      const int k = s / DC::BCH, c = (s % DC::BCH) ^ (4 * (k & 3));
       vb[i] = static_cast<uint32_t>(k * ldb * 2 + c * 16);
     }
   }
@@ -684,23 +697,24 @@ __global__ void __launch_bounds__(dl::NT) gemm_dl_kernel(const GemmArgs p) {
 #define SPH_DL_DMA(T_, SL_, LINE_)                                                          \
   do {                                                                                      \
     const int t_ = (T_), l_ = (LINE_);                                                      \
-    const uint32_t wb_ = __builtin_amdgcn_readfirstlane(lds_base + ((SL_) & 1) * STAGE +    \
-                                                        wave * LPW * 1024);                 \
-    if (l_ < LPW)                                                                           \
-      dma16(ra, wb_ + l_ * 1024, va[l_], __builtin_amdgcn_readfirstlane(t_ * BKD * 2));     \
+    const uint32_t sb_ = lds_base + ((SL_) & 1) * STAGE;                                    \
+    if (l_ < LPA)                                                                           \
+      dma16(ra, __builtin_amdgcn_readfirstlane(sb_ + (wave * LPA + l_) * 1024), va[l_],     \
+            __builtin_amdgcn_readfirstlane(t_ * BKD * 2));                                  \
     else                                                                                    \
-      dma16(rb, wb_ + A_BYTES + (l_ - LPW) * 1024, vb[l_ - LPW],                             \
+      dma16(rb, __builtin_amdgcn_readfirstlane(sb_ + A_BYTES + (wave * LPB + l_ - LPA) * 1024), \
+            vb[l_ - LPA],                                                                   \
             __builtin_amdgcn_readfirstlane(B_KCONT ? t_ * BKD * 2 : t_ * BKD * ldb * 2));   \
   } while (0)
 
   // Prologue: K tiles 0 and 1 in flight; wait for tile 0; fragments of the
   // first P sub-steps.
 #pragma unroll
-  for (int l = 0; l < 2 * LPW; ++l) SPH_DL_DMA(0, 0, l);
+  for (int l = 0; l < LPA + LPB; ++l) SPH_DL_DMA(0, 0, l);
   if (ksteps > 1) {
 #pragma unroll
-    for (int l = 0; l < 2 * LPW; ++l) SPH_DL_DMA(1, 1, l);
-    wait_vmcnt<2 * LPW>();
+    for (int l = 0; l < LPA + LPB; ++l) SPH_DL_DMA(1, 1, l);
+    wait_vmcnt<LPA + LPB>();
   } else {
     wait_vmcnt<0>();
   }
@@ -732,8 +746,9 @@ __global__ void __launch_bounds__(dl::NT) gemm_dl_kernel(const GemmArgs p) {
             SPH_DL_READ((kk + P) % NB, x, ns, kk + P - KK);
         }
         if (kk >= KK - P) {
-          const int d = (kk - (KK - P)) * NMF + x;
-          if (d < 2 * LPW) SPH_DL_DMA(tnext, ks, d);
+#pragma unroll
+          for (int d = (kk - (KK - P)) * NMF + x; d < LPA + LPB; d += P * NMF)
+            SPH_DL_DMA(tnext, ks, d);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -1146,12 +1161,26 @@ void launch_full(const GemmArgs& p, dim3 grid, dim3 block, bool a_kcont, bool b_
 
 // The direct-load kernel addresses a tile's operand rows with 32-bit buffer
 // offsets: every byte it may touch must lie within 2^31 of the tile origin.
-inline bool dl_fits(const GemmArgs& p, bool b_kcont) {
+inline bool dl_fits(const GemmArgs& p, bool b_kcont, int bn) {
   constexpr int64_t kLim = (1LL << 31) - 1;
   if (p.lda > kLim / 2 || p.ldb > kLim / 2) return false;
   const int64_t a_bytes = ((dl::BM - 1) * p.lda + p.k) * 2;
-  const int64_t b_bytes = b_kcont ? ((dl::BN - 1) * p.ldb + p.k) * 2 : ((p.k - 1) * p.ldb + dl::BN) * 2;
+  const int64_t b_bytes = b_kcont ? ((bn - 1) * p.ldb + p.k) * 2 : ((p.k - 1) * p.ldb + bn) * 2;
   return a_bytes < kLim && b_bytes < kLim;
+}
+
+constexpr int64_t kNumCUs = 256;  // MI355X compute units
+
+template <typename T, int BN>
+int launch_dl(GemmArgs& p, int64_t batch, bool b_kcont, hipStream_t st) {
+  p.tiles_m = static_cast<int>(p.m / dl::BM);
+  p.tiles_n = static_cast<int>(p.n / BN);
+  dim3 grid(static_cast<unsigned>(p.tiles_m) * p.tiles_n, static_cast<unsigned>(batch));
+  if (b_kcont)
+    gemm_dl_kernel<T, true, BN><<<grid, dim3(dl::Cfg<BN>::NT), 0, st>>>(p);
+  else
+    gemm_dl_kernel<T, false, BN><<<grid, dim3(dl::Cfg<BN>::NT), 0, st>>>(p);
+  return check_launch("sph_gemm");
 }
 
 // Short-K kernel: K of 64 or 128, whole 128x128 tiles, K-contiguous A,
@@ -1169,9 +1198,8 @@ inline bool shortk_fits(const GemmArgs& p, bool a_kcont, bool b_kcont) {
   return a_bytes < kLim && b_bytes < kLim;
 }
 
-// Launches BM x BN tiles: whole 256x256 tiles with K-contiguous A on the
-// direct-load kernel, other whole tiles with the FULL register-staged kernel
-// on WMF x WNF waves, otherwise the checked kernel on WMP x WNP waves.
+// Launches BM x BN tiles on the register-staged kernel: whole tiles with the
+// FULL variant on WMF x WNF waves, otherwise the checked one on WMP x WNP.
 template <typename T, int BM, int BN, int WMF, int WNF, int WMP, int WNP>
 int launch_cfg(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
                hipStream_t st) {
@@ -1182,12 +1210,7 @@ int launch_cfg(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
   // alignment checks in the K loop.
   const bool full = p.m % BM == 0 && p.n % BN == 0 && p.k % BK == 0 && p.k > 0 &&
                     p.vec_a && p.vec_b;
-  if (full && BM == dl::BM && BN == dl::BN && a_kcont && dl_fits(p, b_kcont)) {
-    if (b_kcont)
-      gemm_dl_kernel<T, true><<<grid, dim3(dl::NT), 0, st>>>(p);
-    else
-      gemm_dl_kernel<T, false><<<grid, dim3(dl::NT), 0, st>>>(p);
-  } else if (full)
+  if (full)
     launch_full<T, BM, BN, WMF, WNF, true>(p, grid, dim3(WMF * WNF * 64), a_kcont, b_kcont, st);
   else
     launch_full<T, BM, BN, WMP, WNP, false>(p, grid, dim3(WMP * WNP * 64), a_kcont, b_kcont, st);
@@ -1217,6 +1240,23 @@ int gemm_dispatch(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
       else gemm_shortk_kernel<T, false, 2><<<grid, dim3(sk::NT), 0, st>>>(p);
     }
     return check_launch("sph_gemm (short K)");
+  }
+  // Whole 256-row tiles with K-contiguous A run the direct-load kernel, 256
+  // or 128 columns wide: the width whose tile count fills the 256 CUs in
+  // the fewest rounds, 128-wide tiles counted at 0.75 (they run 4 waves, one
+  // per SIMD, and move 1.5x the bytes per FLOP: ~800 against ~1000 TFLOP/s
+  // measured per tile-round).
+  if (a_kcont && p.m % dl::BM == 0 && p.k % dl::BKD == 0 && p.k > 0 && p.vec_a && p.vec_b &&
+      p.n % 128 == 0) {
+    auto fill = [](int64_t tiles) {
+      return static_cast<double>(tiles) / (static_cast<double>(ceil_div(tiles, kNumCUs)) * kNumCUs);
+    };
+    const int64_t tw = (p.m / dl::BM) * (p.n / 256) * batch;
+    const int64_t tn = (p.m / dl::BM) * (p.n / 128) * batch;
+    const bool w256 = p.n % 256 == 0 && dl_fits(p, b_kcont, 256) && tw < (1LL << 31);
+    const bool w128 = dl_fits(p, b_kcont, 128) && tn < (1LL << 31);
+    if (w256 && (!w128 || fill(tw) >= 0.75 * fill(tn))) return launch_dl<T, 256>(p, batch, b_kcont, st);
+    if (w128) return launch_dl<T, 128>(p, batch, b_kcont, st);
   }
   const int64_t t256 = ceil_div(p.m, 256) * ceil_div(p.n, 256) * batch;
   const int64_t t128 = ceil_div(p.m, 128) * ceil_div(p.n, 128) * batch;

@@ -58,6 +58,14 @@ DTYPE_TO_HIP = {
 _FLOAT_LOAD = {torch.float16, torch.bfloat16, torch.float32, torch.float64}
 
 MAX_BLOCK = 512
+# Row loops of at most this many trips keep each loaded value in registers
+# for the later phases of the row (softmax's sum and normalise, LayerNorm's
+# normalise): the row is read from memory once.
+MAX_CACHED_TRIPS = 8
+# Pointwise kernels give each thread EPT elements (strided by the block, so
+# accesses stay coalesced) once there are enough elements to fill the GPU:
+# EPT independent loads in flight per thread instead of one.
+PW_BLOCK = 256
 
 
 def _next_pow2(n: int) -> int:
@@ -387,6 +395,9 @@ class SpyreKernel(SIMDKernel):
         self._pending_accum = False
         # kernel argument name -> max element extent (None = not checkable)
         self._extents: dict[str, Optional[int]] = {}
+        # (argument, index) -> register array holding that load for each
+        # trip of a short row loop
+        self._row_cache: dict[tuple[str, str], str] = {}
 
     # -- sizes ----------------------------------------------------------------
     def _static(self, e) -> int:
@@ -409,9 +420,23 @@ class SpyreKernel(SIMDKernel):
         return n
 
     def _block(self) -> int:
+        # Row reductions: about 8 elements per thread (fewer, larger
+        # workgroups amortise the block reductions' barriers), 64 .. 512.
         if self.inside_reduction or self.features.is_reduction():
-            return min(MAX_BLOCK, max(64, _next_pow2(self._rnumel())))
-        return 256
+            return min(MAX_BLOCK, max(64, _next_pow2(self._rnumel()) // 8))
+        return PW_BLOCK
+
+    def _trips(self) -> int:
+        r, b = self._rnumel(), self._block()
+        return (r + b - 1) // b
+
+    @staticmethod
+    def _ept(xnumel: int) -> int:
+        # keep at least ~1024 workgroups (4 per CU) before packing elements
+        for ept in (8, 4, 2):
+            if xnumel >= PW_BLOCK * ept * 1024:
+                return ept
+        return 1
 
     def dtype_to_str(self, dtype: torch.dtype) -> str:
         try:
@@ -454,6 +479,8 @@ class SpyreKernel(SIMDKernel):
             return
         r, b = self._rnumel(), self._block()
         loops = (r + b - 1) // b
+        if loops <= MAX_CACHED_TRIPS:
+            self.body.writeline("#pragma unroll")
         self.body.writeline(f"for (int64_t r0_cnt = 0; r0_cnt < {loops}LL; ++r0_cnt) {{")
         with self.body.indent():
             self.body.writeline(f"const int64_t r0_index = r0_cnt * {b}LL + threadIdx.x;")
@@ -492,7 +519,27 @@ class SpyreKernel(SIMDKernel):
             buf = self.compute
         elif self.is_indirect_indexing(index):
             buf = self.compute
+        elif self._cacheable_row_load(index):
+            key = (str(var), self.index_to_str(index))
+            arr = self._row_cache.get(key)
+            if arr is None:
+                arr = f"rc{len(self._row_cache)}"
+                ctype = "float" if dtype in _FLOAT_LOAD else self.dtype_to_str(dtype)
+                self.indexing_code.writeline(f"{ctype} {arr}[{self._trips()}];")
+                self._row_cache[key] = arr
+                self.loads.writeline(f"{arr}[r0_cnt] = {line};")
+            return self.cse.generate(buf, f"{arr}[r0_cnt]", dtype=out_dtype)
         return self.cse.generate(buf, line, dtype=out_dtype)
+
+    def _cacheable_row_load(self, index: sympy.Expr) -> bool:
+        """A load inside a short row loop whose index depends on the row
+        position: later phases of the same row read it from registers."""
+        if not (self.inside_reduction and self.features.is_reduction()):
+            return False
+        if self._trips() > MAX_CACHED_TRIPS:
+            return False
+        return any(e.is_reduction and sym in index.free_symbols
+                   for sym, e in self.range_tree_nodes.items())
 
     def store(self, name: str, index: sympy.Expr, value: CSEVariable,
               mode: Any = None) -> None:
@@ -665,12 +712,44 @@ class SpyreKernel(SIMDKernel):
                 code.writeline("const int64_t xindex = blockIdx.x;")
                 grid = xnumel
             else:
+                ept = self._ept(xnumel)
+                span = block * ept
+                grid = (xnumel + span - 1) // span
+            if is_red:
+                code.splice(self.indexing_code)
+                code.splice(self.body)
+            elif ept == 1:
                 code.writeline(f"const int64_t xindex = static_cast<int64_t>(blockIdx.x) * {block}LL"
                                " + threadIdx.x;")
                 code.writeline(f"if (xindex >= {xnumel}LL) return;")
-                grid = (xnumel + block - 1) // block
-            code.splice(self.indexing_code)
-            code.splice(self.body)
+                code.splice(self.indexing_code)
+                code.splice(self.body)
+            else:
+                # Whole spans run EPT straight-line copies of the body (all
+                # loads can be issued before the first store); the tail span
+                # checks each element.
+                code.writeline(f"const int64_t spy_base = static_cast<int64_t>(blockIdx.x) * {span}LL;")
+                code.writeline(f"if (spy_base + {span}LL <= {xnumel}LL) {{")
+                with code.indent():
+                    code.writeline("#pragma unroll")
+                    code.writeline(f"for (int spy_e = 0; spy_e < {ept}; ++spy_e) {{")
+                    with code.indent():
+                        code.writeline(f"const int64_t xindex = spy_base + spy_e * {block}LL + threadIdx.x;")
+                        code.splice(self.indexing_code)
+                        code.splice(self.body)
+                    code.writeline("}")
+                code.writeline("} else {")
+                with code.indent():
+                    code.writeline(f"for (int spy_e = 0; spy_e < {ept}; ++spy_e) {{")
+                    with code.indent():
+                        code.writeline(f"const int64_t xindex = spy_base + spy_e * {block}LL + threadIdx.x;")
+                        code.writeline(f"if (xindex < {xnumel}LL) {{")
+                        with code.indent():
+                            code.splice(self.indexing_code)
+                            code.splice(self.body)
+                        code.writeline("}")
+                    code.writeline("}")
+                code.writeline("}")
         code.writeline("}")
         src = code.getvalue()
         if grid <= 0 or grid >= 2**31:
