@@ -104,6 +104,30 @@ __device__ inline float isnan_(float x) { return x != x ? 1.f : 0.f; }
 __device__ inline float isinf_(float x) { return (x == inf() || x == -inf()) ? 1.f : 0.f; }
 __device__ inline float round_even(float x) { return rintf(x); }
 
+// erf without the branches of a full-precision erff (it sits on the GELU
+// path of compiled graphs).  |x| < 0.5: the odd Maclaurin series
+// 2/sqrt(pi) (x - x^3/3 + x^5/10 - x^7/42 + x^9/216 - x^11/1320), truncation
+// error below 2e-8.  |x| >= 0.5: 1 - erfc(|x|) with erfc from Abramowitz &
+// Stegun, Handbook of Mathematical Functions, 7.1.26 (error at most 1.5e-7):
+// erfc(a) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-a^2), t = 1/(1 + p a).
+__device__ inline float erf_fast(float x) {
+  const float y = x * x;
+  float s = fmaf(y, -1.0f / 1320.0f, 1.0f / 216.0f);
+  s = fmaf(s, y, -1.0f / 42.0f);
+  s = fmaf(s, y, 1.0f / 10.0f);
+  s = fmaf(s, y, -1.0f / 3.0f);
+  s = fmaf(s, y, 1.0f);
+  const float small = 1.1283791670955126f * x * s;  // 2 / sqrt(pi)
+  const float a = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, a, 1.0f));
+  float q = fmaf(1.061405429f, t, -1.453152027f);
+  q = fmaf(q, t, 1.421413741f);
+  q = fmaf(q, t, -0.284496736f);
+  q = fmaf(q, t, 0.254829592f);
+  const float large = copysignf(1.0f - q * t * __expf(-y), x);
+  return a < 0.5f ? small : large;
+}
+
 // Integer index helpers used by printed index expressions.
 __device__ inline int64_t floordiv_i(int64_t a, int64_t b) {
   int64_t q = a / b;

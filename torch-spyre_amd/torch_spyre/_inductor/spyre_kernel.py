@@ -62,10 +62,16 @@ MAX_BLOCK = 512
 # for the later phases of the row (softmax's sum and normalise, LayerNorm's
 # normalise): the row is read from memory once.
 MAX_CACHED_TRIPS = 8
-# Pointwise kernels give each thread EPT elements (strided by the block, so
-# accesses stay coalesced) once there are enough elements to fill the GPU:
-# EPT independent loads in flight per thread instead of one.
+# Row reductions over >= 512 elements give each thread VEC consecutive row
+# elements per trip, emitted as VEC straight-line copies of the body: loads
+# and stores of contiguous rows at consecutive indices merge into 16-byte
+# accesses.  Pointwise kernels give each thread EPT elements strided by the
+# block (every wave instruction stays one coalesced run; index expressions
+# with broadcasts do not merge reliably into wide accesses, and partly merged
+# ones lose the coalescing) once there are enough elements to keep ~1024
+# workgroups: EPT independent loads in flight per thread instead of one.
 PW_BLOCK = 256
+VEC = 8
 
 
 def _next_pow2(n: int) -> int:
@@ -370,7 +376,7 @@ for _name, _fn in {
     "log10": "log10f", "log1p": "log1pf", "sqrt": "sqrtf", "sin": "sinf", "cos": "cosf",
     "tan": "tanf", "tanh": "tanhf", "asin": "asinf", "acos": "acosf", "atan": "atanf",
     "sinh": "sinhf", "cosh": "coshf", "asinh": "asinhf", "acosh": "acoshf", "atanh": "atanhf",
-    "erf": "erff", "erfc": "erfcf", "floor": "floorf", "ceil": "ceilf", "trunc": "truncf",
+    "erf": "spy::erf_fast", "erfc": "erfcf", "floor": "floorf", "ceil": "ceilf", "trunc": "truncf",
     "lgamma": "lgammaf",
 }.items():
     setattr(SpyreOverrides, _name, _unary_fn(_fn))
@@ -426,9 +432,12 @@ class SpyreKernel(SIMDKernel):
             return min(MAX_BLOCK, max(64, _next_pow2(self._rnumel()) // 8))
         return PW_BLOCK
 
+    def _rvec(self) -> int:
+        return VEC if self._rnumel() >= 64 * VEC else 1
+
     def _trips(self) -> int:
-        r, b = self._rnumel(), self._block()
-        return (r + b - 1) // b
+        r, span = self._rnumel(), self._block() * self._rvec()
+        return (r + span - 1) // span
 
     @staticmethod
     def _ept(xnumel: int) -> int:
@@ -477,14 +486,17 @@ class SpyreKernel(SIMDKernel):
     def _open_rloop(self) -> None:
         if self._rloop_open:
             return
-        r, b = self._rnumel(), self._block()
-        loops = (r + b - 1) // b
+        r, b, v = self._rnumel(), self._block(), self._rvec()
+        loops = self._trips()
         if loops <= MAX_CACHED_TRIPS:
             self.body.writeline("#pragma unroll")
         self.body.writeline(f"for (int64_t r0_cnt = 0; r0_cnt < {loops}LL; ++r0_cnt) {{")
+        self.body.writeline("#pragma unroll")
+        self.body.writeline(f"for (int spy_v = 0; spy_v < {v}; ++spy_v) {{")
         with self.body.indent():
-            self.body.writeline(f"const int64_t r0_index = r0_cnt * {b}LL + threadIdx.x;")
-            if loops * b != r:
+            self.body.writeline(
+                f"const int64_t r0_index = (r0_cnt * {b}LL + threadIdx.x) * {v}LL + spy_v;")
+            if loops * b * v != r:
                 self.body.writeline(f"if (r0_index >= {r}LL) break;")
         self._rloop_open = True
 
@@ -525,10 +537,11 @@ class SpyreKernel(SIMDKernel):
             if arr is None:
                 arr = f"rc{len(self._row_cache)}"
                 ctype = "float" if dtype in _FLOAT_LOAD else self.dtype_to_str(dtype)
-                self.indexing_code.writeline(f"{ctype} {arr}[{self._trips()}];")
+                self.indexing_code.writeline(f"{ctype} {arr}[{self._trips() * self._rvec()}];")
                 self._row_cache[key] = arr
-                self.loads.writeline(f"{arr}[r0_cnt] = {line};")
-            return self.cse.generate(buf, f"{arr}[r0_cnt]", dtype=out_dtype)
+                self.loads.writeline(f"{arr}[r0_cnt * {self._rvec()} + spy_v] = {line};")
+            return self.cse.generate(buf, f"{arr}[r0_cnt * {self._rvec()} + spy_v]",
+                                     dtype=out_dtype)
         return self.cse.generate(buf, line, dtype=out_dtype)
 
     def _cacheable_row_load(self, index: sympy.Expr) -> bool:
@@ -643,7 +656,7 @@ class SpyreKernel(SIMDKernel):
             with self.body.indent():
                 self.body.splice(self.loads)
                 self.body.splice(self.compute)
-            self.body.writeline("}")
+            self.body.writeline("}}")
             self._rloop_open = False
             # values computed inside the loop die with it; reduction results
             # (made after the loop) stay available to later phases
