@@ -207,6 +207,34 @@ int sph_bmm_f16(int64_t batch, int64_t m, int64_t n, int64_t k,
                 const void* a, const void* b, void* d, sph_stream_t stream);
 
 /* ------------------------------------------------------------------ */
+/* Fused attention forward                                              */
+/* Replaces: the chain the reference runs for attention, spyre__bmm_    */
+/*   default (spyre_torch_ops.cpp:297-377) for the scores, the          */
+/*   generated add + _softmax (Metadata.yaml:275-277, base.jinja2:16-   */
+/*   241) and spyre__bmm_default again for P V: the same result without */
+/*   writing the [mq, sk] score matrix.  No single reference function   */
+/*   corresponds; the compile backend substitutes it for that chain.    */
+/* ------------------------------------------------------------------ */
+
+/* O[b] = softmax(scale * Q[b] K[b]^T + M[b]) V[b] for b < batch, with
+ * Q[b] [mq, head_dim] at q + b*stride_q (row i at + i*ldq), K[b], V[b]
+ * [sk, head_dim] likewise, O[b] [mq, head_dim].  M is optional (NULL):
+ * an additive [mq, sk] mask in natural-log units (-inf drops a key) at
+ * mask + b*stride_m (stride_m 0 shares one mask), row i at + i*ldm.
+ * causal_q > 0 additionally drops keys j > (i % causal_q) + causal_off
+ * for row i (query heads stacked along the rows keep their positions).
+ * dtype in {F16, BF16} for Q, K, V, M, O; fp32 scores and accumulation;
+ * head_dim must be 128, mq a multiple of 128, rows 16-byte aligned
+ * (mask rows 8-byte aligned).  A row with no visible key yields NaN, as
+ * softmax over all -inf does. */
+int sph_attention_fwd(sph_dtype dtype, int64_t batch, int64_t mq, int64_t sk,
+                      int64_t head_dim, const void* q, int64_t ldq, int64_t stride_q,
+                      const void* k, int64_t ldk, int64_t stride_k, const void* v,
+                      int64_t ldv, int64_t stride_v, const void* mask, int64_t ldm,
+                      int64_t stride_m, int64_t causal_q, int64_t causal_off, float scale,
+                      void* o, int64_t ldo, int64_t stride_o, sph_stream_t stream);
+
+/* ------------------------------------------------------------------ */
 /* Generic strided pointwise engine                                     */
 /* Replaces: the generated base/list_inp eager ops of Metadata.yaml     */
 /*   (add/sub/mul/div/exp/log/.../where/eq/ge, base.jinja2:16-241),     */

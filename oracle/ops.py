@@ -106,6 +106,21 @@ def gelu(x):
     return (0.5 * a * (1.0 + _erf(a / np.sqrt(2.0)))).astype(np.float32)
 
 
+def attention(q, k, v, scale, mask=None, causal_q_len=0, causal_offset=0):
+    """softmax(scale * q k^T + mask) v per leading batch index (fp32 scores
+    and probabilities, float64 row sums).  The chain the reference runs for
+    attention: spyre__bmm_default (codegen/inputs/spyre_torch_ops.cpp:
+    297-377) for the scores, the generated add and _softmax
+    (Metadata.yaml:275-277), bmm again for P v.  q [..., mq, d], k / v
+    [..., sk, d], mask broadcastable to [..., mq, sk]; causal as in
+    `softmax` (row r keeps columns c <= r % causal_q_len + causal_offset)."""
+    s = np.matmul(_f32(q), np.swapaxes(_f32(k), -1, -2)) * np.float32(scale)
+    if mask is not None:
+        s = s + _f32(mask)
+    p = softmax(s, axis=-1, causal_q_len=causal_q_len, causal_offset=causal_offset)
+    return np.matmul(p, _f32(v)).astype(np.float32)
+
+
 def gelu_affine_rowsum(x, s, b):
     """y = gelu(x * s + b) (s, b broadcast over rows), r = sum_c y (fp32 y).
     The fused chain of config 3 (gelu followed by ReduceSum,

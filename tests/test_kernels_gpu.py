@@ -6,6 +6,8 @@ Bars: bit-exact for layout / copy / gather / integer work; rtol = atol = 1e-2
 against the oracle's fp32 result rounded to the output dtype for fp16 / bf16
 floating point (fp32 outputs: 1e-4)."""
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -444,6 +446,78 @@ def test_bmm(batch, m, n, k, tb):
                m * k, _p(bd), ldb, k * n, 0.0, None, 0, 0, 0, _p(d), n, m * n, 0, _stream())
     _sync()
     assert_close_fp(d, O.gemm(A.numpy(), B.numpy()), what="bmm")
+
+
+# ---------------------------------------------------------------------------
+# fused attention
+# ---------------------------------------------------------------------------
+def _attention(q, k, v, scale, mask=None, causal_q=0, causal_off=0, dtype=torch.float16,
+               ld_pad=0):
+    """q [b, mq, 128], k / v [b, sk, 128] (device, contiguous); mask [mq, sk]
+    device or None.  Rows of q/k/v/o get ld_pad extra elements when set."""
+    b, mq, d = q.shape
+    sk = k.shape[1]
+
+    def padded(t):
+        if not ld_pad:
+            return t, t.shape[-1]
+        buf = torch.zeros(t.shape[0], t.shape[1], d + ld_pad, dtype=t.dtype, device=t.device)
+        buf[..., :d] = t
+        return buf, d + ld_pad
+
+    (qp, ldq), (kp, ldk), (vp_, ldv) = padded(q), padded(k), padded(v)
+    o = torch.empty(b, mq, d + ld_pad, dtype=dtype, device=DEV)
+    ldm = mask.stride(0) if mask is not None else 0
+    _capi.call("sph_attention_fwd", DT[dtype], b, mq, sk, d, _p(qp), ldq, qp[0].numel(), _p(kp),
+               ldk, kp[0].numel(), _p(vp_), ldv, vp_[0].numel(), _p(mask), ldm, 0, causal_q,
+               causal_off, scale, _p(o), d + ld_pad, o[0].numel(), _stream())
+    _sync()
+    return o[..., :d]
+
+
+@pytest.mark.parametrize("b,mq,sk,causal_q,masked,pad", [(2, 256, 256, 256, False, 0),
+                                                        (3, 512, 128, 128, False, 8),
+                                                        (2, 128, 200, 0, True, 0),
+                                                        (1, 384, 320, 96, True, 16),
+                                                        (2, 256, 64, 0, False, 0)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_attention_fused(b, mq, sk, causal_q, masked, pad, dtype):
+    # causal with stacked query heads (mq = heads * causal_q), additive masks
+    # with -inf entries and key counts off the 64-key block, padded rows
+    _log(f"attention b={b} mq={mq} sk={sk} causal_q={causal_q} mask={masked} pad={pad} {dtype}")
+    q = randn((b, mq, 128), k=41, dtype=dtype)
+    k = randn((b, sk, 128), k=42, dtype=dtype)
+    v = randn((b, sk, 128), k=43, dtype=dtype)
+    scale = 1 / math.sqrt(128)
+    mask = None
+    if masked:
+        m = randn((mq, sk), k=44)
+        m[m < -1.2] = float("-inf")
+        m[:, 0] = 0.0
+        mask = m.to(dtype)
+    off = sk - causal_q if causal_q else 0
+    got = _attention(q.to(DEV), k.to(DEV), v.to(DEV), scale,
+                     mask.to(DEV) if mask is not None else None, causal_q, off, dtype, pad)
+    want = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), scale,
+                       mask=None if mask is None else mask.float().numpy(),
+                       causal_q_len=causal_q, causal_offset=off)
+    tol = dict(rtol=1e-2, atol=1e-2) if dtype == torch.float16 else dict(rtol=2e-2, atol=2e-2)
+    assert_close_fp(got, want, out_dtype=dtype, what="fused attention", **tol)
+
+
+def test_attention_fused_c4_shape():
+    # the c4 layer's attention: 8 KV heads, 4 query heads stacked per KV
+    # head (mq = 4 * 2048), causal over 2048 keys; one batch element
+    # checked against the oracle, all 8 run
+    _log("attention c4 shape")
+    q = randn((8, 8192, 128), k=45)
+    k = randn((8, 2048, 128), k=46)
+    v = randn((8, 2048, 128), k=47)
+    got = _attention(q.to(DEV), k.to(DEV), v.to(DEV), 1 / math.sqrt(128), None, 2048, 0)
+    want = O.attention(q[:1].numpy(), k[:1].numpy(), v[:1].numpy(), 1 / math.sqrt(128),
+                       causal_q_len=2048)
+    assert_close_fp(got[:1], want, what="c4 attention")
+    assert torch.isfinite(got.float()).all()
 
 
 # ---------------------------------------------------------------------------

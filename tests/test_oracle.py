@@ -287,3 +287,27 @@ def test_rope_vs_torch_and_norm_preserved():
     pair = lambda z: z[..., :8] ** 2 + z[..., 8:] ** 2  # noqa: E731
     np.testing.assert_allclose(pair(got), pair(xf.numpy()), rtol=1e-4, atol=1e-5)
     np.testing.assert_allclose(O.rope(x.numpy(), np.zeros(6), 1e4), xf.numpy(), atol=0)
+
+
+def test_attention_vs_torch_sdpa():
+    # oracle.attention against torch's own fused attention routine on the CPU
+    # (fp32): causal with stacked query heads, an additive mask, and a
+    # transposed-operand mistake that must fail
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(3, 4 * 16, 32, generator=g)
+    k = torch.randn(3, 16, 32, generator=g)
+    v = torch.randn(3, 16, 32, generator=g)
+    scale = 1 / math.sqrt(32)
+    got = O.attention(q.numpy(), k.numpy(), v.numpy(), scale, causal_q_len=16)
+    # stacked heads: row r is query r % 16 of head r // 16
+    qh = q.view(3, 4, 16, 32)
+    want = F.scaled_dot_product_attention(qh, k[:, None], v[:, None], is_causal=True)
+    np.testing.assert_allclose(got, want.reshape(3, 64, 32).numpy(), rtol=1e-5, atol=1e-5)
+    mask = torch.randn(64, 16, generator=g)
+    mask[mask < -1] = float("-inf")
+    mask[:, 0] = 0.0  # every row keeps a key
+    got = O.attention(q.numpy(), k.numpy(), v.numpy(), scale, mask=mask.numpy())
+    want = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+    np.testing.assert_allclose(got, want.numpy(), rtol=1e-5, atol=1e-5)
+    bad = O.attention(q.numpy(), v.numpy(), k.numpy(), scale, mask=mask.numpy())
+    assert not np.allclose(bad, want.numpy(), rtol=1e-3, atol=1e-3)

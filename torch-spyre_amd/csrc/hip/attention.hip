@@ -1,0 +1,410 @@
+// Fused attention forward: O = softmax(scale * Q K^T + mask) V for fp16 /
+// bf16, head dim 128, without materialising the score matrix.
+//
+// Shapes: per batch b (one KV head with its stacked query heads), Q is
+// [mq, 128], K and V are [sk, 128], O is [mq, 128]; rows of every operand
+// are 16-byte aligned with arbitrary leading dims.  Masking: an additive
+// [mq, sk] mask (natural-log units, -inf to drop a key) and/or causal
+// positions (row r sits at position r % causal_q + causal_off and sees keys
+// <= that position).
+//
+// Design (gfx950, MFMA 32x32x16):
+//   * A workgroup of 4 waves takes 128 query rows (32 per wave) and walks
+//     the keys in blocks of 64.  K and V blocks move into LDS by direct
+//     global->LDS DMA (buffer_load_dwordx4 ... lds), two stages deep.
+//   * Scores are computed transposed, S^T = K Q^T (K fragments from LDS as
+//     the MFMA's first operand, the wave's Q fragments held in registers as
+//     the second): each lane then owns one query column and 32 of the
+//     block's scores for it, so the row max and sum are in-lane reductions
+//     plus one exchange with the lane 32 away.
+//   * The output is accumulated transposed too, O^T += V^T P^T: P^T is the
+//     score accumulator itself (converted to fp16), V^T fragments come from
+//     the N-contiguous V block through ds_read_b64_tr_b16.  The MFMA's 16 K
+//     slots are mapped to keys so that a lane's 8 P values are 8
+//     consecutive accumulator registers and its V values two 4-key
+//     transpose reads.  The online-softmax rescale of O is per lane (each
+//     lane's O^T registers belong to its query) - no shuffles.
+//   * exp is computed as exp2 with scale * log2(e) folded into the scores.
+//   * Causal: key blocks past the last position of the workgroup's rows are
+//     skipped (about half the work for a square causal problem).
+//   * LDS layouts chosen so every fragment read is a per-lane base plus a
+//     compile-time offset (fewer live address registers) and bank-conflict
+//     free: K rows are padded to 272 bytes (16 consecutive rows at one
+//     16-byte chunk start 68 banks apart); V is split by 32-wide head-dim
+//     slab, [dt][key][32 values], 64-byte rows, so a transpose read's 4 rows
+//     x 4 chunks are one contiguous 256-byte run.
+//   * Causal work per workgroup grows with its query position.  When the
+//     query rows are whole position blocks of stacked heads, the 1-D grid is
+//     ordered so that the first half runs longest-first and the second half
+//     shortest-first: the two workgroups a CU holds at once then pair a long
+//     block with a short one and every CU gets about the same work.
+#include "sph_common.h"
+
+namespace sph {
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+#define SPH_LDS __attribute__((address_space(3)))
+
+constexpr int AQ = 128;   // query rows per workgroup (32 per wave)
+constexpr int AK = 64;    // keys per block
+constexpr int AD = 128;   // head dim
+constexpr int KPITCH = AD * 2 + 16;       // padded K row (bytes)
+constexpr int KBLK = AK * KPITCH;         // 17408 bytes: 17 DMA lines of 1 KB
+constexpr int VBLK = AK * AD * 2;         // 16384 bytes: 16 lines
+constexpr int KLINES = KBLK / 1024, VLINES = VBLK / 1024;
+constexpr int STAGE = KBLK + VBLK;
+static_assert(KBLK % 1024 == 0 && VBLK % 1024 == 0, "whole DMA lines");
+
+struct AttnArgs {
+  int64_t mq, sk;
+  const void* q;
+  int64_t ldq, sq;
+  const void* k;
+  int64_t ldk, skb;
+  const void* v;
+  int64_t ldv, svb;
+  const void* mask;
+  int64_t ldm, smb;
+  int64_t causal_q, causal_off;
+  int64_t batch, nbq;   // batch, query blocks per batch element (mq / 128)
+  int64_t heads;        // > 0: causal rows are `heads` stacked runs of causal_q
+  float scale_log2;  // scale * log2(e)
+  void* o;
+  int64_t ldo, so;
+};
+
+template <typename T>
+__device__ inline f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (__is_same(T, half_t)) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+}
+
+template <typename T>
+__device__ inline uint32_t pack2(float lo, float hi) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, Num<T>::from_f(lo))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, Num<T>::from_f(hi))) << 16);
+}
+
+__device__ inline i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(static_cast<uint32_t>(a)));
+  r[1] = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(static_cast<uint32_t>(a >> 32) & 0xffffu));
+  r[2] = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(bytes));
+  r[3] = 0x00020000;
+  return r;
+}
+// 16 bytes per lane from rsrc[voff + soff] into LDS at lds_addr + 16 * lane
+// (inline asm: the compiler would otherwise wait for it before every LDS
+// read; completion is awaited explicitly).
+__device__ inline void dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory", "m0");
+}
+template <int N>
+__device__ inline void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <typename T, bool MASK, bool CAUSAL>
+__global__ void __launch_bounds__(256) attn_fwd_kernel(const AttnArgs p) {
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t wg = blockIdx.x;
+  int64_t b, r0;  // batch element, first query row of the workgroup
+  if (CAUSAL && p.heads > 0) {
+    const int64_t per = p.batch * p.heads, total = per * p.nbq, half = total / 2;
+    const int64_t j = wg < half ? wg : total - 1 - (wg - half);  // rank by work, largest first
+    const int64_t pb = p.nbq / p.heads - 1 - j / per, rem = j % per;
+    b = rem / p.heads;
+    r0 = (rem % p.heads) * p.causal_q + pb * AQ;
+  } else {
+    b = wg / p.nbq;
+    r0 = (wg % p.nbq) * AQ;
+  }
+  const int64_t qrow = r0 + wave * 32 + (lane & 31);         // this lane's query row
+  const int h = lane >> 5;
+
+  // Keys this workgroup can see.
+  int64_t kend = p.sk;
+  if constexpr (CAUSAL) {
+    const int64_t last = r0 + AQ - 1;
+    const int64_t pmax = (r0 / p.causal_q == last / p.causal_q) ? last % p.causal_q + p.causal_off
+                                                                : p.causal_q - 1 + p.causal_off;
+    kend = pmax + 1 < kend ? pmax + 1 : kend;
+  }
+  const int nblk = kend <= 0 ? 0 : static_cast<int>((kend + AK - 1) / AK);
+  const int64_t qpos = CAUSAL ? qrow % p.causal_q + p.causal_off : 0;
+
+  // Q fragments: query qrow, head dims 16 kk + 8 h .. + 7.
+  const uint16_t* Q = static_cast<const uint16_t*>(p.q) + b * p.sq + qrow * p.ldq;
+  u32x4 qf[AD / 16];
+#pragma unroll
+  for (int kk = 0; kk < AD / 16; ++kk) qf[kk] = *reinterpret_cast<const u32x4*>(Q + 16 * kk + 8 * h);
+
+  // DMA set-up.  K line L: 16-byte slot s = L*64 + lane of the padded
+  // block, row s / 17, chunk s % 17 (chunk 16 is the pad: it fetches
+  // nothing - its offset lies past the buffer range, which reads zeros).
+  // V line L: slab dt = L / 4, keys 16 (L % 4) .., lanes in runs of 4
+  // chunks per key.
+  // Each block gets buffer resources based at its first key and bounded by
+  // its last valid key, so rows past sk read zeros.
+  const uint16_t* Kb = static_cast<const uint16_t*>(p.k) + b * p.skb;
+  const uint16_t* Vb = static_cast<const uint16_t*>(p.v) + b * p.svb;
+  // lines handled by this wave: K lines wave, wave+4, ... (< 17), V lines 4 per wave
+  constexpr int KLW = (KLINES + 3) / 4, VLW = VLINES / 4;
+  uint32_t vk[KLW], vv[VLW];
+#pragma unroll
+  for (int i = 0; i < KLW; ++i) {
+    const int s = (wave + 4 * i) * 64 + lane;
+    const int r = s / 17, c = s % 17;
+    vk[i] = c < 16 ? static_cast<uint32_t>(r * p.ldk * 2 + c * 16) : 0xffffffffu;
+  }
+#pragma unroll
+  for (int i = 0; i < VLW; ++i) {
+    const int L = wave * VLW + i;
+    const int dt = L >> 2, key = (L & 3) * 16 + (lane >> 2), c = 4 * dt + (lane & 3);
+    vv[i] = static_cast<uint32_t>(key * p.ldv * 2 + c * 16);
+  }
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((SPH_LDS char*)(lds)));
+  auto issue = [&](int blk, int st) {
+    const uint32_t sbase = lds_base + st * STAGE;
+    const int64_t key0 = static_cast<int64_t>(blk) * AK;
+    const int64_t nk = p.sk - key0 < AK ? p.sk - key0 : AK;
+    const i32x4 rk = buffer_rsrc(Kb + key0 * p.ldk, static_cast<uint32_t>(((nk - 1) * p.ldk + AD) * 2));
+    const i32x4 rv = buffer_rsrc(Vb + key0 * p.ldv, static_cast<uint32_t>(((nk - 1) * p.ldv + AD) * 2));
+#pragma unroll
+    for (int i = 0; i < KLW; ++i)
+      if (wave + 4 * i < KLINES)
+        dma16(rk, __builtin_amdgcn_readfirstlane(sbase + (wave + 4 * i) * 1024), vk[i], 0u);
+#pragma unroll
+    for (int i = 0; i < VLW; ++i)
+      dma16(rv, __builtin_amdgcn_readfirstlane(sbase + KBLK + (wave * VLW + i) * 1024), vv[i], 0u);
+  };
+
+  // Fragment read bases of this lane (block-relative bytes): K row
+  // lane % 32, chunk h; V^T transpose pointer at key 4 (g >> 1) + e, column
+  // 16 (g & 1) + 4 q4 of slab 0.
+  const int g = lane >> 4, jj = lane & 15, e = jj >> 2, q4 = jj & 3;
+  const int kbase_lane = (lane & 31) * KPITCH + h * 16;
+  const int vbase_lane = (4 * (g >> 1) + e) * 64 + (16 * (g & 1) + 4 * q4) * 2;
+  f32x16 o[AD / 32];
+#pragma unroll
+  for (int t = 0; t < AD / 32; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  const uint16_t* Mrow =
+      MASK ? static_cast<const uint16_t*>(p.mask) + b * p.smb + qrow * p.ldm : nullptr;
+
+  if (nblk > 0) {
+    issue(0, 0);
+    if (nblk > 1) {
+      issue(1, 1);
+      wait_vmcnt<(KLINES + 3) / 4 + VLINES / 4>();
+    } else {
+      wait_vmcnt<0>();
+    }
+  }
+  __syncthreads();
+  for (int kb = 0; kb < nblk; ++kb) {
+    const int st = kb & 1;
+    const char* sK = lds + st * STAGE;
+    const char* sV = sK + KBLK;
+    // S^T for this block: two 32-key tiles.
+    f32x16 s[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < AD / 16; ++kk) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(sK + kbase_lane + t * 32 * KPITCH + kk * 32);
+        s[t] = mfma<T>(kf, qf[kk], s[t]);
+      }
+    }
+    // Scores in log2 units, masked; block max.
+    const int64_t k0 = static_cast<int64_t>(kb) * AK;
+    float mb = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int64_t kbase = k0 + t * 32 + 8 * rg + 4 * h;
+        float mk[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (MASK) {
+          if (kbase + 4 <= p.sk) {
+            const u32x2 mv = *reinterpret_cast<const u32x2*>(Mrow + kbase);
+            const T* me = reinterpret_cast<const T*>(&mv);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mk[i] = Num<T>::to_f(me[i]) * 1.4426950408889634f;
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              mk[i] = kbase + i < p.sk ? Num<T>::to_f(reinterpret_cast<const T*>(Mrow)[kbase + i]) *
+                                             1.4426950408889634f
+                                       : 0.f;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t key = kbase + i;
+          float x = s[t][4 * rg + i] * p.scale_log2 + mk[i];
+          bool keep = key < p.sk;
+          if constexpr (CAUSAL) keep = keep && key <= qpos;
+          x = keep ? x : -INFINITY;
+          s[t][4 * rg + i] = x;
+          mb = fmaxf(mb, x);
+        }
+      }
+    }
+    mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+    const float m_new = fmaxf(m_run, mb);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    float lb = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pr = __builtin_amdgcn_exp2f(s[t][r] - m_use);
+        s[t][r] = pr;
+        lb += pr;
+      }
+    lb += __shfl_xor(lb, 32, 64);
+    l_run = l_run * alpha + lb;
+    m_run = m_new;
+#pragma unroll
+    for (int dt = 0; dt < AD / 32; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    // O^T += V^T P^T over the block's 4 sixteen-key steps.
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int t = c >> 1, rb = 8 * (c & 1);
+      u32x4 pf;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pf[i] = pack2<T>(s[t][rb + 2 * i], s[t][rb + 2 * i + 1]);
+#pragma unroll
+      for (int dt = 0; dt < AD / 32; ++dt) {
+        // slab dt, key rows 16 c + 4 (g >> 1) + e (+ 8 for the second read)
+        const SPH_LDS char* p0 =
+            (const SPH_LDS char*)(sV) + vbase_lane + dt * (AK * 64) + 16 * c * 64;
+        const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((SPH_LDS s16x4*)(p0)));
+        const u32x2 hi = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((SPH_LDS s16x4*)(p0 + 8 * 64)));
+        const u32x4 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3);
+        o[dt] = mfma<T>(vf, pf, o[dt]);
+      }
+    }
+    // Block kb+1 landed (own DMA) and every wave is done with stage st.
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (kb + 2 < nblk) issue(kb + 2, st);
+  }
+  // O[qrow][d], d = 32 dt + 8 rg + 4 h + i, normalised by the row sum.
+  const float inv = 1.0f / l_run;
+  uint16_t* O = static_cast<uint16_t*>(p.o) + b * p.so + qrow * p.ldo;
+#pragma unroll
+  for (int dt = 0; dt < AD / 32; ++dt)
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      u32x2 w;
+      w[0] = pack2<T>(o[dt][4 * rg] * inv, o[dt][4 * rg + 1] * inv);
+      w[1] = pack2<T>(o[dt][4 * rg + 2] * inv, o[dt][4 * rg + 3] * inv);
+      *reinterpret_cast<u32x2*>(O + dt * 32 + 8 * rg + 4 * h) = w;
+    }
+}
+
+inline bool al16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+}  // namespace
+}  // namespace sph
+
+using namespace sph;
+
+extern "C" int sph_attention_fwd(sph_dtype dtype, int64_t batch, int64_t mq, int64_t sk,
+                                 int64_t head_dim, const void* q, int64_t ldq, int64_t stride_q,
+                                 const void* k, int64_t ldk, int64_t stride_k, const void* v,
+                                 int64_t ldv, int64_t stride_v, const void* mask, int64_t ldm,
+                                 int64_t stride_m, int64_t causal_q, int64_t causal_off,
+                                 float scale, void* o, int64_t ldo, int64_t stride_o,
+                                 sph_stream_t stream) {
+  SPH_REQUIRE(dtype == SPH_F16 || dtype == SPH_BF16, SPH_ERR_UNSUPPORTED,
+              "attention: dtype must be F16 or BF16");
+  SPH_REQUIRE(head_dim == AD, SPH_ERR_UNSUPPORTED, "attention: head_dim must be 128");
+  SPH_REQUIRE(batch >= 0 && mq >= 0 && sk >= 0, SPH_ERR_INVALID_ARG, "attention: negative size");
+  if (batch == 0 || mq == 0) return SPH_OK;
+  SPH_REQUIRE(sk > 0, SPH_ERR_INVALID_ARG, "attention: no keys");
+  SPH_REQUIRE(mq % AQ == 0, SPH_ERR_UNSUPPORTED, "attention: query rows must be a multiple of 128");
+  SPH_REQUIRE(batch * (mq / AQ) < (1LL << 31), SPH_ERR_TOO_LARGE, "attention: grid too large");
+  SPH_REQUIRE(causal_q >= 0, SPH_ERR_INVALID_ARG, "attention: causal_q < 0");
+  SPH_REQUIRE(ldq >= AD && ldk >= AD && ldv >= AD && ldo >= AD, SPH_ERR_INVALID_ARG,
+              "attention: leading dimension below head_dim");
+  SPH_REQUIRE(al16(q) && al16(k) && al16(v) && al16(o) && ldq % 8 == 0 && ldk % 8 == 0 &&
+                  ldv % 8 == 0 && ldo % 8 == 0 && (batch == 1 || (stride_q % 8 == 0 &&
+                  stride_k % 8 == 0 && stride_v % 8 == 0 && stride_o % 8 == 0)),
+              SPH_ERR_INVALID_ARG, "attention: rows must be 16-byte aligned");
+  SPH_REQUIRE(mask == nullptr || (ldm >= sk && ldm % 4 == 0 && (reinterpret_cast<uintptr_t>(mask) & 7u) == 0 &&
+                                  (batch == 1 || stride_m % 4 == 0)),
+              SPH_ERR_INVALID_ARG, "attention: mask rows must be 8-byte aligned, ldm >= sk");
+  // DMA buffer offsets are 32-bit.
+  SPH_REQUIRE(((sk - 1) * ldk + AD) * 2 < (1LL << 31) && ((sk - 1) * ldv + AD) * 2 < (1LL << 31),
+              SPH_ERR_TOO_LARGE, "attention: K/V too large for 32-bit offsets");
+  AttnArgs p{};
+  p.mq = mq;
+  p.sk = sk;
+  p.q = q;
+  p.ldq = ldq;
+  p.sq = stride_q;
+  p.k = k;
+  p.ldk = ldk;
+  p.skb = stride_k;
+  p.v = v;
+  p.ldv = ldv;
+  p.svb = stride_v;
+  p.mask = mask;
+  p.ldm = ldm;
+  p.smb = stride_m;
+  p.causal_q = causal_q;
+  p.causal_off = causal_off;
+  p.batch = batch;
+  p.nbq = mq / AQ;
+  p.heads = (causal_q > 0 && causal_q % AQ == 0 && mq % causal_q == 0) ? mq / causal_q : 0;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  p.o = o;
+  p.ldo = ldo;
+  p.so = stride_o;
+  hipStream_t st = as_stream(stream);
+  dim3 grid(static_cast<unsigned>(batch * (mq / AQ)));
+  const bool m = mask != nullptr, c = causal_q > 0;
+#define SPH_ATTN(T_)                                                                     \
+  do {                                                                                   \
+    if (m && c) attn_fwd_kernel<T_, true, true><<<grid, 256, 0, st>>>(p);                \
+    else if (m) attn_fwd_kernel<T_, true, false><<<grid, 256, 0, st>>>(p);               \
+    else if (c) attn_fwd_kernel<T_, false, true><<<grid, 256, 0, st>>>(p);               \
+    else attn_fwd_kernel<T_, false, false><<<grid, 256, 0, st>>>(p);                     \
+  } while (0)
+  if (dtype == SPH_F16)
+    SPH_ATTN(half_t);
+  else
+    SPH_ATTN(bf16_t);
+#undef SPH_ATTN
+  return check_launch("sph_attention_fwd");
+}
