@@ -226,13 +226,23 @@ int sph_bmm_f16(int64_t batch, int64_t m, int64_t n, int64_t k,
  * dtype in {F16, BF16} for Q, K, V, M, O; fp32 scores and accumulation;
  * head_dim must be 128, mq a multiple of 128, rows 16-byte aligned
  * (mask rows 8-byte aligned).  A row with no visible key yields NaN, as
- * softmax over all -inf does. */
+ * softmax over all -inf does.
+ * workspace (device memory, may be NULL) of at least
+ * sph_attention_workspace_bytes(batch, mq, sk, stride_m) bytes lets a mask
+ * call class the mask's 128 x 64 blocks first (all zero / mixed / all
+ * -inf; 16-byte aligned mask rows) and skip the all -inf ones: a causal
+ * mask then costs about half the work.  The workspace is written on
+ * `stream`; calls sharing one workspace must be ordered on a stream. */
 int sph_attention_fwd(sph_dtype dtype, int64_t batch, int64_t mq, int64_t sk,
                       int64_t head_dim, const void* q, int64_t ldq, int64_t stride_q,
                       const void* k, int64_t ldk, int64_t stride_k, const void* v,
                       int64_t ldv, int64_t stride_v, const void* mask, int64_t ldm,
                       int64_t stride_m, int64_t causal_q, int64_t causal_off, float scale,
-                      void* o, int64_t ldo, int64_t stride_o, sph_stream_t stream);
+                      void* o, int64_t ldo, int64_t stride_o, void* workspace,
+                      int64_t workspace_bytes, sph_stream_t stream);
+/* Bytes of mask-block classes sph_attention_fwd uses for this shape: one
+ * per (mask batch, 128-row block, 64-key block); 0 for an empty shape. */
+int64_t sph_attention_workspace_bytes(int64_t batch, int64_t mq, int64_t sk, int64_t stride_m);
 
 /* ------------------------------------------------------------------ */
 /* Generic strided pointwise engine                                     */

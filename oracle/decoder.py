@@ -14,7 +14,10 @@ output is an fp16 tensor: RoPE rounds x*cos, rot*sin and their sum; the
 scores round after the bmm and again after the scale; SiLU rounds before
 the gate product), True = compiled (Inductor keeps values in registers
 inside each fused kernel: RoPE and SiLU*up round once, the scale is applied
-to the fp16 bmm output without another rounding).
+to the fp16 bmm output without another rounding; where the compiled program
+runs attention as one fused kernel - prefill, head dim 128, the stacked
+query rows of a KV head a multiple of 128 - the scores are not rounded at
+all, only the probabilities before the second product).
 
 Pinned by tests/test_decoder.py against torch's CPU float32 ops with
 F.scaled_dot_product_attention (is_causal, enable_gqa) as an independent
@@ -65,9 +68,10 @@ def _rope(x, cos, sin, act, fused=False):
     return _r(_r(x * c, act) + _r(rot * s, act), act)
 
 
-def attention(q, k, v, q_pos, k_pos, act=None, fused=False):
+def attention(q, k, v, q_pos, k_pos, act=None, fused=False, scores_fp32=False):
     """q [B, Sq, Hq, D], k / v [B, Sk, Hkv, D]; causal on absolute
-    positions (key position <= query position).  Returns [B, Sq, Hq*D]."""
+    positions (key position <= query position).  Returns [B, Sq, Hq*D].
+    scores_fp32: the scores stay float32 (a fused attention kernel)."""
     B, Sq, Hq, D = q.shape
     Hkv = k.shape[2]
     g = Hq // Hkv
@@ -76,9 +80,11 @@ def attention(q, k, v, q_pos, k_pos, act=None, fused=False):
     for b in range(B):
         for h in range(Hq):
             kh = h // g
-            s = _r(q[b, :, h].astype(np.float32) @ k[b, :, kh].astype(np.float32).T, act)
+            s = q[b, :, h].astype(np.float32) @ k[b, :, kh].astype(np.float32).T
+            if not scores_fp32:
+                s = _r(s, act)
             s = s * np.float32(1.0 / np.sqrt(D))
-            if not fused:
+            if not fused and not scores_fp32:
                 s = _r(s, act)
             s = np.where(allowed, s, np.float32(-np.inf))
             p = _r(O.softmax(s, axis=-1), act)
@@ -103,7 +109,10 @@ def layer(h, w, cfg, positions, act=np.float16, kv_prefix=None, fused=False):
         k = np.concatenate([kv_prefix[0], k], axis=1)
         v = np.concatenate([kv_prefix[1], v], axis=1)
         k_pos = np.arange(k.shape[1])
-    a = attention(q, k, v, np.asarray(positions), k_pos, act, fused)
+    # the compiled program's prefill attention is one fused kernel when its
+    # shapes fit (head dim 128, stacked query rows per KV head % 128 == 0)
+    fused_attn = fused and kv_prefix is None and D == 128 and (S * (H // Hkv)) % 128 == 0
+    a = attention(q, k, v, np.asarray(positions), k_pos, act, fused, scores_fp32=fused_attn)
     h = _r(h + _linear(a, w["wo"], act), act)
     x = _rmsnorm(h, w["mlp_norm"], cfg.eps, act)
     gte = _linear(x, w["wg"], act)

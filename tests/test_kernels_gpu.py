@@ -452,9 +452,10 @@ def test_bmm(batch, m, n, k, tb):
 # fused attention
 # ---------------------------------------------------------------------------
 def _attention(q, k, v, scale, mask=None, causal_q=0, causal_off=0, dtype=torch.float16,
-               ld_pad=0):
+               ld_pad=0, workspace=True):
     """q [b, mq, 128], k / v [b, sk, 128] (device, contiguous); mask [mq, sk]
-    device or None.  Rows of q/k/v/o get ld_pad extra elements when set."""
+    or [b, mq, sk] on the device, or None.  Rows of q/k/v/o get ld_pad extra
+    elements when set; `workspace` passes room for the mask-block pre-pass."""
     b, mq, d = q.shape
     sk = k.shape[1]
 
@@ -467,10 +468,15 @@ def _attention(q, k, v, scale, mask=None, causal_q=0, causal_off=0, dtype=torch.
 
     (qp, ldq), (kp, ldk), (vp_, ldv) = padded(q), padded(k), padded(v)
     o = torch.empty(b, mq, d + ld_pad, dtype=dtype, device=DEV)
-    ldm = mask.stride(0) if mask is not None else 0
+    ldm = mask.stride(-2) if mask is not None else 0
+    sm = mask.stride(0) if mask is not None and mask.dim() == 3 else 0
+    ws, nws = None, 0
+    if workspace and mask is not None:
+        nws = _capi.lib().sph_attention_workspace_bytes(b, mq, sk, sm)
+        ws = torch.full((nws,), 0xAB, dtype=torch.uint8, device=DEV)  # stale contents
     _capi.call("sph_attention_fwd", DT[dtype], b, mq, sk, d, _p(qp), ldq, qp[0].numel(), _p(kp),
-               ldk, kp[0].numel(), _p(vp_), ldv, vp_[0].numel(), _p(mask), ldm, 0, causal_q,
-               causal_off, scale, _p(o), d + ld_pad, o[0].numel(), _stream())
+               ldk, kp[0].numel(), _p(vp_), ldv, vp_[0].numel(), _p(mask), ldm, sm, causal_q,
+               causal_off, scale, _p(o), d + ld_pad, o[0].numel(), _p(ws), nws, _stream())
     _sync()
     return o[..., :d]
 
@@ -503,6 +509,64 @@ def test_attention_fused(b, mq, sk, causal_q, masked, pad, dtype):
                        causal_q_len=causal_q, causal_offset=off)
     tol = dict(rtol=1e-2, atol=1e-2) if dtype == torch.float16 else dict(rtol=2e-2, atol=2e-2)
     assert_close_fp(got, want, out_dtype=dtype, what="fused attention", **tol)
+
+
+def _block_mask(kind, b, mq, sk, causal_q=0):
+    """Additive masks whose 128 x 64 blocks cover every class the pre-pass
+    tells apart (all zero, mixed, all -inf), as [mq, sk] or [b, mq, sk]."""
+    if kind == "causal":       # stacked heads, each a causal run of causal_q rows
+        r = torch.arange(mq)[:, None] % causal_q + (sk - causal_q)
+        return torch.where(torch.arange(sk)[None, :] <= r, 0.0, float("-inf"))
+    if kind == "window":       # keys (pos - 100, pos]: all -inf blocks at the front
+        pos = torch.arange(mq)[:, None] % sk
+        c = torch.arange(sk)[None, :]
+        return torch.where((c <= pos) & (c > pos - 100), 0.0, float("-inf"))
+    if kind == "holes":        # zero mask with all -inf key blocks in the middle, per batch
+        m = torch.zeros(b, mq, sk)
+        for i in range(b):
+            m[i, :, 64 * (i + 1):64 * (i + 2)] = float("-inf")
+        m[:, 5, 3] = -0.75     # one mixed block
+        return m
+    if kind == "zero":
+        return torch.zeros(mq, sk)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind,b,mq,sk,causal_q", [("causal", 2, 512, 256, 128),
+                                                    ("causal", 1, 256, 200, 200),
+                                                    ("window", 2, 384, 384, 0),
+                                                    ("holes", 3, 256, 320, 0),
+                                                    ("zero", 2, 128, 136, 0)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_attention_mask_blocks(kind, b, mq, sk, causal_q, dtype):
+    # the mask-block pre-pass: same result as without it (bit-exact: skipped
+    # blocks are all -inf, unloaded ones all zero) and as the oracle
+    _log(f"attention mask blocks {kind} b={b} mq={mq} sk={sk} {dtype}")
+    q = randn((b, mq, 128), k=51, dtype=dtype)
+    k = randn((b, sk, 128), k=52, dtype=dtype)
+    v = randn((b, sk, 128), k=53, dtype=dtype)
+    m = _block_mask(kind, b, mq, sk, causal_q).to(dtype)
+    args = (q.to(DEV), k.to(DEV), v.to(DEV), 1 / math.sqrt(128), m.to(DEV), 0, 0, dtype)
+    got = _attention(*args)
+    plain = _attention(*args, workspace=False)
+    assert torch.equal(got, plain), "mask-block pre-pass changed the result"
+    want = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), 1 / math.sqrt(128),
+                       mask=m.float().numpy())
+    tol = dict(rtol=1e-2, atol=1e-2) if dtype == torch.float16 else dict(rtol=2e-2, atol=2e-2)
+    assert_close_fp(got, want, out_dtype=dtype, what=f"attention {kind} mask", **tol)
+
+
+def test_attention_causal_mask_matches_causal_positions():
+    # c4's attention with its additive causal mask (stacked heads) takes
+    # the same blocks, in the same order, as the causal-position mode
+    _log("attention c4 causal mask vs positions")
+    q = randn((8, 8192, 128), k=55).to(DEV)
+    k = randn((8, 2048, 128), k=56).to(DEV)
+    v = randn((8, 2048, 128), k=57).to(DEV)
+    m = _block_mask("causal", 8, 8192, 2048, 2048).half().to(DEV)
+    by_mask = _attention(q, k, v, 1 / math.sqrt(128), m, 0, 0)
+    by_pos = _attention(q, k, v, 1 / math.sqrt(128), None, 2048, 0)
+    assert torch.equal(by_mask, by_pos)
 
 
 def test_attention_fused_c4_shape():

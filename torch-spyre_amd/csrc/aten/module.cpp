@@ -20,6 +20,10 @@ namespace spyre {
 int64_t load_kernel(const std::string& code_object, const std::string& name);
 void launch_kernel(int64_t handle, const std::vector<at::Tensor>& args, int64_t grid,
                    int64_t block, const std::vector<int64_t>& extents);
+// Fused attention (ops_attention.cpp).
+at::Tensor attention_fwd(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                         const c10::optional<at::Tensor>& mask, double scale, int64_t causal_q,
+                         int64_t causal_off);
 }  // namespace spyre
 
 PYBIND11_MODULE(_C, m) {
@@ -37,6 +41,10 @@ PYBIND11_MODULE(_C, m) {
         "Launches a loaded kernel on the spyre stream of the arguments' device; "
         "extents[i] >= 0 bounds the elements argument i may address.");
 
+  m.def("attention_fwd", &spyre::attention_fwd, py::arg("q"), py::arg("k"), py::arg("v"),
+        py::arg("mask"), py::arg("scale"), py::arg("causal_q") = 0, py::arg("causal_off") = 0,
+        "softmax(scale * q k^T + mask) v on the spyre stream (q [B, mq, 128], k / v "
+        "[B, sk, 128], mask [mq, sk] / [B or 1, mq, sk] or None; fp16 / bf16).");
   m.def("device_count", []() { return spyre::device_count(); });
   m.def("current_device", []() { return spyre::current_device(); });
   m.def("set_device", [](int d) { spyre::set_device(d); });

@@ -33,11 +33,16 @@
 //     16-byte chunk start 68 banks apart); V is split by 32-wide head-dim
 //     slab, [dt][key][32 values], 64-byte rows, so a transpose read's 4 rows
 //     x 4 chunks are one contiguous 256-byte run.
-//   * Causal work per workgroup grows with its query position.  When the
-//     query rows are whole position blocks of stacked heads, the 1-D grid is
-//     ordered so that the first half runs longest-first and the second half
-//     shortest-first: the two workgroups a CU holds at once then pair a long
-//     block with a short one and every CU gets about the same work.
+//   * Masks: a pre-pass classes every (128-row, 64-key) block of the mask as
+//     all zero, mixed or all -inf (one byte each).  A workgroup walks only
+//     the key range between its first and last block that is not all -inf,
+//     skips all -inf blocks inside it and loads mask values only for mixed
+//     blocks - a causal mask then costs what the causal-position mode costs.
+//   * Causal work per workgroup grows with its query position.  The 1-D grid
+//     runs row blocks last-first in its first half and first-first in its
+//     second half, so the two workgroups a CU holds at once are row blocks
+//     rb and nbq-1-rb: for causal rows (also with heads stacked along the
+//     rows) their key counts add up to about the same total on every CU.
 #include "sph_common.h"
 
 namespace sph {
@@ -73,7 +78,9 @@ struct AttnArgs {
   int64_t ldm, smb;
   int64_t causal_q, causal_off;
   int64_t batch, nbq;   // batch, query blocks per batch element (mq / 128)
-  int64_t heads;        // > 0: causal rows are `heads` stacked runs of causal_q
+  const uint8_t* mblk;  // mask block classes [mask batch][nbq][nkb] or null
+  int64_t mblk_b;       // row blocks per mask batch in mblk (0: one mask for all)
+  int64_t nkb;          // key blocks (ceil(sk / 64))
   float scale_log2;  // scale * log2(e)
   void* o;
   int64_t ldo, so;
@@ -119,27 +126,63 @@ __device__ inline void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Mask block classes (values of the pre-pass's bytes).
+constexpr uint8_t MB_ZERO = 0, MB_MIXED = 1, MB_NEGINF = 2;
+
+// One workgroup per (mask batch, row block, key block): class the block's
+// 128 x 64 mask values (keys past sk ignored).
+template <typename T>
+__global__ void __launch_bounds__(256) mask_blocks_kernel(const uint16_t* __restrict__ mask,
+                                                          int64_t ldm, int64_t smb, int64_t sk,
+                                                          int64_t nbq, int64_t nkb,
+                                                          uint8_t* __restrict__ out) {
+  const int64_t kb = blockIdx.x, rb = blockIdx.y, mb = blockIdx.z;
+  const int t = threadIdx.x;
+  const uint16_t* M = mask + mb * smb + (rb * AQ) * ldm + kb * AK;
+  const int64_t kn = sk - kb * AK;  // keys of this block (<= 64 counts)
+  bool nonzero = false, finite = false;
+  // 128 rows x 8 chunks of 8 keys: 4 chunks per thread
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = t + 256 * i, r = c >> 3, k8 = (c & 7) * 8;
+    if (k8 + 8 <= kn) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(M + r * ldm + k8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint16_t bits = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+        const float x = Num<T>::to_f(__builtin_bit_cast(T, bits));
+        nonzero |= x != 0.f;
+        finite |= x != -INFINITY;
+      }
+    } else {
+      for (int e = 0; e < 8 && k8 + e < kn; ++e) {
+        const float x = Num<T>::to_f(reinterpret_cast<const T*>(M + r * ldm)[k8 + e]);
+        nonzero |= x != 0.f;
+        finite |= x != -INFINITY;
+      }
+    }
+  }
+  const int anynz = __syncthreads_or(nonzero), anyfin = __syncthreads_or(finite);
+  if (t == 0) out[(mb * nbq + rb) * nkb + kb] = !anyfin ? MB_NEGINF : (anynz ? MB_MIXED : MB_ZERO);
+}
+
 template <typename T, bool MASK, bool CAUSAL>
-__global__ void __launch_bounds__(256) attn_fwd_kernel(const AttnArgs p) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+attn_fwd_kernel(const AttnArgs p) {
   __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t wg = blockIdx.x;
-  int64_t b, r0;  // batch element, first query row of the workgroup
-  if (CAUSAL && p.heads > 0) {
-    const int64_t per = p.batch * p.heads, total = per * p.nbq, half = total / 2;
-    const int64_t j = wg < half ? wg : total - 1 - (wg - half);  // rank by work, largest first
-    const int64_t pb = p.nbq / p.heads - 1 - j / per, rem = j % per;
-    b = rem / p.heads;
-    r0 = (rem % p.heads) * p.causal_q + pb * AQ;
-  } else {
-    b = wg / p.nbq;
-    r0 = (wg % p.nbq) * AQ;
-  }
+  // Workgroup order: first half row blocks descending, second half ascending
+  // (u = rank in a row-block-descending list), so workgroups wg and
+  // wg + half take row blocks rb and nbq-1-rb.
+  const int64_t wg = blockIdx.x, total = p.batch * p.nbq, half = total / 2;
+  const int64_t u = wg < half ? wg : total - 1 - (wg - half);
+  const int64_t rb = p.nbq - 1 - u / p.batch, b = u % p.batch;
+  const int64_t r0 = rb * AQ;                                 // first row of the workgroup
   const int64_t qrow = r0 + wave * 32 + (lane & 31);         // this lane's query row
   const int h = lane >> 5;
 
-  // Keys this workgroup can see.
+  // Key blocks this workgroup walks: [kb0, kb1).
   int64_t kend = p.sk;
   if constexpr (CAUSAL) {
     const int64_t last = r0 + AQ - 1;
@@ -147,7 +190,26 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(const AttnArgs p) {
                                                                 : p.causal_q - 1 + p.causal_off;
     kend = pmax + 1 < kend ? pmax + 1 : kend;
   }
-  const int nblk = kend <= 0 ? 0 : static_cast<int>((kend + AK - 1) / AK);
+  int kb0 = 0, kb1 = kend <= 0 ? 0 : static_cast<int>((kend + AK - 1) / AK);
+  const uint8_t* mcls = nullptr;
+  if (MASK && p.mblk != nullptr) {
+    // first and last key block not entirely -inf
+    mcls = p.mblk + (b * p.mblk_b + rb) * p.nkb;  // [mask batch][rb][kb]
+    int lo = 0x7fffffff, hi = -1;
+    for (int kb = lane; kb < kb1; kb += 64)
+      if (mcls[kb] != MB_NEGINF) {
+        lo = lo < kb ? lo : kb;
+        hi = kb;
+      }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+      const int ol = __shfl_xor(lo, d, 64), oh = __shfl_xor(hi, d, 64);
+      lo = lo < ol ? lo : ol;
+      hi = hi > oh ? hi : oh;
+    }
+    kb0 = __builtin_amdgcn_readfirstlane(hi < 0 ? 0 : lo);
+    kb1 = __builtin_amdgcn_readfirstlane(hi + 1);
+  }
   const int64_t qpos = CAUSAL ? qrow % p.causal_q + p.causal_off : 0;
 
   // Q fragments: query qrow, head dims 16 kk + 8 h .. + 7.
@@ -211,20 +273,23 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(const AttnArgs p) {
   const uint16_t* Mrow =
       MASK ? static_cast<const uint16_t*>(p.mask) + b * p.smb + qrow * p.ldm : nullptr;
 
-  if (nblk > 0) {
-    issue(0, 0);
-    if (nblk > 1) {
-      issue(1, 1);
+  if (kb0 < kb1) {
+    issue(kb0, 0);
+    if (kb0 + 1 < kb1) {
+      issue(kb0 + 1, 1);
       wait_vmcnt<(KLINES + 3) / 4 + VLINES / 4>();
     } else {
       wait_vmcnt<0>();
     }
   }
   __syncthreads();
-  for (int kb = 0; kb < nblk; ++kb) {
-    const int st = kb & 1;
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const int st = (kb - kb0) & 1;
     const char* sK = lds + st * STAGE;
     const char* sV = sK + KBLK;
+    // mask class of this block (all mixed without the pre-pass)
+    const uint8_t cls = MASK ? (mcls != nullptr ? mcls[kb] : MB_MIXED) : MB_ZERO;
+    if (cls != MB_NEGINF) {
     // S^T for this block: two 32-key tiles.
     f32x16 s[2];
 #pragma unroll
@@ -239,41 +304,53 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(const AttnArgs p) {
         s[t] = mfma<T>(kf, qf[kk], s[t]);
       }
     }
-    // Scores in log2 units, masked; block max.
+    // Scores in log2 units; keys past sk (and past the position) dropped.
     const int64_t k0 = static_cast<int64_t>(kb) * AK;
-    float mb = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        const int64_t kbase = k0 + t * 32 + 8 * rg + 4 * h;
-        float mk[4] = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (MASK) {
-          if (kbase + 4 <= p.sk) {
-            const u32x2 mv = *reinterpret_cast<const u32x2*>(Mrow + kbase);
-            const T* me = reinterpret_cast<const T*>(&mv);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) mk[i] = Num<T>::to_f(me[i]) * 1.4426950408889634f;
-          } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              mk[i] = kbase + i < p.sk ? Num<T>::to_f(reinterpret_cast<const T*>(Mrow)[kbase + i]) *
-                                             1.4426950408889634f
-                                       : 0.f;
-          }
-        }
+      for (int rg = 0; rg < 4; ++rg)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int64_t key = kbase + i;
-          float x = s[t][4 * rg + i] * p.scale_log2 + mk[i];
+          const int64_t key = k0 + t * 32 + 8 * rg + 4 * h + i;
           bool keep = key < p.sk;
           if constexpr (CAUSAL) keep = keep && key <= qpos;
-          x = keep ? x : -INFINITY;
-          s[t][4 * rg + i] = x;
-          mb = fmaxf(mb, x);
+          s[t][4 * rg + i] = keep ? s[t][4 * rg + i] * p.scale_log2 : -INFINITY;
         }
+    // Mixed mask blocks: add the mask (log2 units).  Lane's keys for (t, rg):
+    // k0 + 32 t + 8 rg + 4 h .. + 3, one 8-byte load each.
+    if (MASK && cls == MB_MIXED) {
+      const uint16_t* mp = Mrow + k0 + 4 * h;
+      if (k0 + AK <= p.sk) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int rg = 0; rg < 4; ++rg) {
+            const u32x2 mv = *reinterpret_cast<const u32x2*>(mp + 32 * t + 8 * rg);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const uint16_t bits = static_cast<uint16_t>(mv[i >> 1] >> (16 * (i & 1)));
+              s[t][4 * rg + i] = fmaf(Num<T>::to_f(__builtin_bit_cast(T, bits)), 1.4426950408889634f,
+                                      s[t][4 * rg + i]);
+            }
+          }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int rg = 0; rg < 4; ++rg)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (k0 + 32 * t + 8 * rg + 4 * h + i < p.sk)
+                s[t][4 * rg + i] = fmaf(Num<T>::to_f(reinterpret_cast<const T*>(mp)[32 * t + 8 * rg + i]),
+                                        1.4426950408889634f, s[t][4 * rg + i]);
       }
     }
+    float mb = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mb = fmaxf(mb, s[t][r]);
     mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
     const float m_new = fmaxf(m_run, mb);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
@@ -313,10 +390,11 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(const AttnArgs p) {
         o[dt] = mfma<T>(vf, pf, o[dt]);
       }
     }
+    }  // cls != MB_NEGINF
     // Block kb+1 landed (own DMA) and every wave is done with stage st.
     wait_vmcnt<0>();
     __syncthreads();
-    if (kb + 2 < nblk) issue(kb + 2, st);
+    if (kb + 2 < kb1) issue(kb + 2, st);
   }
   // O[qrow][d], d = 32 dt + 8 rg + 4 h + i, normalised by the row sum.
   const float inv = 1.0f / l_run;
@@ -339,13 +417,23 @@ inline bool al16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 1
 
 using namespace sph;
 
+namespace {
+int64_t mask_batches(int64_t batch, int64_t stride_m) { return (batch == 1 || stride_m == 0) ? 1 : batch; }
+}  // namespace
+
+extern "C" int64_t sph_attention_workspace_bytes(int64_t batch, int64_t mq, int64_t sk,
+                                                 int64_t stride_m) {
+  if (batch <= 0 || mq <= 0 || sk <= 0) return 0;
+  return mask_batches(batch, stride_m) * ((mq + AQ - 1) / AQ) * ((sk + AK - 1) / AK);
+}
+
 extern "C" int sph_attention_fwd(sph_dtype dtype, int64_t batch, int64_t mq, int64_t sk,
                                  int64_t head_dim, const void* q, int64_t ldq, int64_t stride_q,
                                  const void* k, int64_t ldk, int64_t stride_k, const void* v,
                                  int64_t ldv, int64_t stride_v, const void* mask, int64_t ldm,
                                  int64_t stride_m, int64_t causal_q, int64_t causal_off,
                                  float scale, void* o, int64_t ldo, int64_t stride_o,
-                                 sph_stream_t stream) {
+                                 void* workspace, int64_t workspace_bytes, sph_stream_t stream) {
   SPH_REQUIRE(dtype == SPH_F16 || dtype == SPH_BF16, SPH_ERR_UNSUPPORTED,
               "attention: dtype must be F16 or BF16");
   SPH_REQUIRE(head_dim == AD, SPH_ERR_UNSUPPORTED, "attention: head_dim must be 128");
@@ -364,9 +452,10 @@ extern "C" int sph_attention_fwd(sph_dtype dtype, int64_t batch, int64_t mq, int
   SPH_REQUIRE(mask == nullptr || (ldm >= sk && ldm % 4 == 0 && (reinterpret_cast<uintptr_t>(mask) & 7u) == 0 &&
                                   (batch == 1 || stride_m % 4 == 0)),
               SPH_ERR_INVALID_ARG, "attention: mask rows must be 8-byte aligned, ldm >= sk");
-  // DMA buffer offsets are 32-bit.
-  SPH_REQUIRE(((sk - 1) * ldk + AD) * 2 < (1LL << 31) && ((sk - 1) * ldv + AD) * 2 < (1LL << 31),
-              SPH_ERR_TOO_LARGE, "attention: K/V too large for 32-bit offsets");
+  // DMA offsets within one key block are 32-bit.
+  SPH_REQUIRE(AK * ldk * 2 < (1LL << 31) && AK * ldv * 2 < (1LL << 31), SPH_ERR_TOO_LARGE,
+              "attention: K/V rows too long for 32-bit block offsets");
+  SPH_REQUIRE(workspace_bytes >= 0, SPH_ERR_INVALID_ARG, "attention: negative workspace size");
   AttnArgs p{};
   p.mq = mq;
   p.sk = sk;
@@ -386,12 +475,31 @@ extern "C" int sph_attention_fwd(sph_dtype dtype, int64_t batch, int64_t mq, int
   p.causal_off = causal_off;
   p.batch = batch;
   p.nbq = mq / AQ;
-  p.heads = (causal_q > 0 && causal_q % AQ == 0 && mq % causal_q == 0) ? mq / causal_q : 0;
+  p.nkb = (sk + AK - 1) / AK;
   p.scale_log2 = scale * 1.4426950408889634f;
   p.o = o;
   p.ldo = ldo;
   p.so = stride_o;
   hipStream_t st = as_stream(stream);
+  // Mask block classes, when the caller gave room for them and the mask rows
+  // allow 16-byte reads.
+  const int64_t mbat = mask_batches(batch, stride_m);
+  if (mask != nullptr && workspace != nullptr &&
+      workspace_bytes >= sph_attention_workspace_bytes(batch, mq, sk, stride_m) &&
+      al16(mask) && ldm % 8 == 0 && (mbat == 1 || stride_m % 8 == 0)) {
+    SPH_REQUIRE(p.nkb < (1LL << 31) && mbat <= 65535 && p.nbq <= 65535, SPH_ERR_TOO_LARGE,
+                "attention: mask too large for the block pre-pass");
+    uint8_t* cls = static_cast<uint8_t*>(workspace);
+    dim3 g(static_cast<unsigned>(p.nkb), static_cast<unsigned>(p.nbq), static_cast<unsigned>(mbat));
+    if (dtype == SPH_F16)
+      mask_blocks_kernel<half_t><<<g, 256, 0, st>>>(static_cast<const uint16_t*>(mask), ldm,
+                                                    mbat == 1 ? 0 : stride_m, sk, p.nbq, p.nkb, cls);
+    else
+      mask_blocks_kernel<bf16_t><<<g, 256, 0, st>>>(static_cast<const uint16_t*>(mask), ldm,
+                                                    mbat == 1 ? 0 : stride_m, sk, p.nbq, p.nkb, cls);
+    p.mblk = cls;
+    p.mblk_b = mbat == 1 ? 0 : p.nbq;
+  }
   dim3 grid(static_cast<unsigned>(batch * (mq / AQ)));
   const bool m = mask != nullptr, c = causal_q > 0;
 #define SPH_ATTN(T_)                                                                     \

@@ -226,3 +226,34 @@ def _(x, mean, norm_mean, weight, bias):
     out = x.new_empty(x.size())
     out.spyre_dci = tensor_get_dci(x)
     return out
+
+
+# ---- fused attention --------------------------------------------------------
+
+@torch.library.custom_op("spyre::attention", mutates_args=())
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[torch.Tensor],
+              scale: float) -> torch.Tensor:
+    """softmax(scale * q k^T + mask, -1) v for q [B, mq, d], k / v [B, sk, d],
+    mask broadcastable to [B, mq, sk] or None; softmax in fp32, its result
+    rounded to the input dtype before the second product.  This is the
+    chain the reference runs as spyre__bmm_default
+    (codegen/inputs/spyre_torch_ops.cpp:297-377), add + _softmax
+    (codegen/inputs/Metadata.yaml:275-277) and bmm again; on other devices
+    it runs as that chain, on spyre as one fused kernel."""
+    s = torch.bmm(q, k.transpose(1, 2)) * scale
+    if mask is not None:
+        s = s + mask
+    p = torch.softmax(s.float(), dim=-1).to(q.dtype)
+    return torch.bmm(p, v)
+
+
+@attention.register_kernel("spyre")
+def _(q, k, v, mask, scale):
+    from torch_spyre import _C
+
+    return _C.attention_fwd(q, k, v, mask, float(scale))
+
+
+@attention.register_fake
+def _(q, k, v, mask, scale):
+    return q.new_empty((q.shape[0], q.shape[1], v.shape[2]))

@@ -7,7 +7,8 @@ global config.  Here the passes run through the per-device custom pass of
 `register_backend_for_device`, i.e. only on post-grad graphs that hold spyre
 tensors, and no conversion is removed: kernels upcast to fp32 internally, so
 the conversions Inductor sees are the ones the program asked for.  The list
-is empty by default; a pass is any callable taking the GraphModule.
+holds the attention fusion (bmm -> softmax -> bmm as one fused kernel,
+fuse_attention.py); a pass is any callable taking the GraphModule.
 """
 
 from __future__ import annotations
@@ -17,7 +18,9 @@ from typing import Any, Callable, List, Optional
 import torch
 from torch._inductor.custom_graph_pass import CustomGraphModulePass, get_hash_for_files
 
-custom_post_passes: List[Callable[[torch.fx.GraphModule], None]] = []
+from .fuse_attention import fuse_attention
+
+custom_post_passes: List[Callable[[torch.fx.GraphModule], None]] = [fuse_attention]
 
 
 class CustomPostPasses(CustomGraphModulePass):
@@ -31,4 +34,6 @@ class CustomPostPasses(CustomGraphModulePass):
             f = getattr(p, "file", None)
             if callable(f):
                 files.add(f())
-        return (get_hash_for_files(tuple(sorted(files))), tuple(repr(p) for p in custom_post_passes))
+        names = tuple(getattr(p, "__module__", "") + "." + getattr(p, "__qualname__", repr(p))
+                      for p in custom_post_passes)
+        return (get_hash_for_files(tuple(sorted(files))), names)
