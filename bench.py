@@ -254,6 +254,49 @@ def bench_spyre_paths(steps, warmup):
     return out
 
 
+def bench_host_copies(reps=5, mib=256):
+    """Host<->device copy throughput of spyre tensors (GB/s, median of
+    `reps`), pageable and pinned, next to torch-ROCm's own copies of the
+    same bytes as a yardstick.  Wall time from the call to the end of a
+    device synchronise."""
+    import statistics
+    import time
+
+    import torch
+
+    n = mib << 20
+    x = torch.randint(0, 256, (n,), dtype=torch.uint8, generator=_gen(7))
+    xp = x.pin_memory()
+    back = torch.empty_like(x)
+    backp = torch.empty_like(x).pin_memory()
+    d = torch.empty(n, dtype=torch.uint8, device="spyre")
+    c = torch.empty(n, dtype=torch.uint8, device="cuda")
+
+    def rate(fn, sync):
+        fn()
+        sync()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            sync()
+            ts.append(time.perf_counter() - t0)
+        return round(n / statistics.median(ts) / 1e9, 1)
+
+    ss, cs = torch.spyre.synchronize, torch.cuda.synchronize
+    out = {"bytes": n,
+           "spyre_h2d_pageable_GBs": rate(lambda: d.copy_(x), ss),
+           "spyre_h2d_pinned_nonblocking_GBs": rate(lambda: d.copy_(xp, non_blocking=True), ss),
+           "spyre_d2h_pageable_GBs": rate(lambda: back.copy_(d), ss),
+           "spyre_d2h_pinned_nonblocking_GBs": rate(lambda: backp.copy_(d, non_blocking=True), ss),
+           "torch_rocm_h2d_pageable_GBs": rate(lambda: c.copy_(x), cs),
+           "torch_rocm_h2d_pinned_nonblocking_GBs": rate(lambda: c.copy_(xp, non_blocking=True), cs),
+           "torch_rocm_d2h_pageable_GBs": rate(lambda: back.copy_(c), cs),
+           "torch_rocm_d2h_pinned_nonblocking_GBs": rate(lambda: backp.copy_(c, non_blocking=True), cs)}
+    assert torch.equal(back, x) and torch.equal(backp, x)
+    return out
+
+
 def bench_decoder(steps, warmup, c5_layers=40, decode_steps=128):
     """c4: one decoder layer (+ embedding) compiled, prefill of 2048 tokens;
     c5: the 40-layer model, compiled prefill of 4 x 1024 tokens into the KV
@@ -445,8 +488,10 @@ def main(argv=None):
     ap.add_argument("--no-decoder", action="store_true")
     ap.add_argument("--c5-layers", type=int, default=40)
     ap.add_argument("--decode-steps", type=int, default=128)
-    ap.add_argument("--kernel", choices=["all", "gemm", "copy", "decoder", "bmm"], default="all",
-                    help="gemm / copy / decoder / bmm: run only that part (for rocprofv3 passes)")
+    ap.add_argument("--kernel", choices=["all", "gemm", "copy", "decoder", "bmm", "h2d"],
+                    default="all",
+                    help="gemm / copy / decoder / bmm / h2d: run only that part (for rocprofv3 "
+                         "passes)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; runs on more than one GPU are not "
@@ -467,6 +512,9 @@ def main(argv=None):
     if args.kernel == "bmm":
         print(json.dumps({"kernel": "bmm", **bench_bmm(args.steps, args.warmup, stream, _capi)}))
         return 0
+    if args.kernel == "h2d":
+        print(json.dumps({"kernel": "h2d", **bench_host_copies()}))
+        return 0
     if args.kernel == "decoder":
         print(json.dumps({"kernel": "decoder",
                           **bench_decoder(5, 2, args.c5_layers, args.decode_steps)}))
@@ -483,6 +531,8 @@ def main(argv=None):
         extra["c2_mm_4096_spyre_device_eager"] = bench_eager_mm(max(10, args.steps), args.warmup)
         _log("spyre device paths (eager + torch.compile)")
         extra["spyre_device"] = bench_spyre_paths(max(10, args.steps), args.warmup)
+        _log("host<->device copies")
+        extra["host_device_copy"] = bench_host_copies()
         if not args.no_decoder:
             _log("decoder workloads (c4 layer, c5 model)")
             extra["decoder"] = bench_decoder(5, 2, args.c5_layers, args.decode_steps)

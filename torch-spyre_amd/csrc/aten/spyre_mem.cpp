@@ -7,7 +7,7 @@
 // Device tensors are plain strided tensors whose storage is MI355X HBM, so
 // every PyTorch view (transposes included) works; their storage is sized
 // with the reference's 128-byte stick rule.  Host<->device copies move the
-// bytes with hipMemcpyAsync on the device's spyre stream; any dtype
+// bytes on the device's spyre stream (spyre_copy.cpp); any dtype
 // conversion, broadcast or stride change happens either on the host side of
 // the copy (torch's own CPU copy) or on the device in the strided copy
 // kernel, so copies are bit-exact.  Differences from the reference, on
@@ -150,43 +150,51 @@ const at::Tensor& spyre_resize_(const at::Tensor& self, c10::IntArrayRef size,
 // ---------------------------------------------------------------------------
 namespace {
 
+// A CPU tensor whose bytes are exactly the image of `like` (same dtype,
+// sizes and strides, dense): `t` itself when it already is one.
+bool same_image(const at::Tensor& t, const at::Tensor& like) {
+  return t.scalar_type() == like.scalar_type() && t.sizes().equals(like.sizes()) &&
+         t.strides().equals(like.strides()) && t.is_non_overlapping_and_dense();
+}
+
 // dst (spyre) = src (CPU), any shapes broadcastable, any dtypes.
-void copy_h2d(const at::Tensor& src, const at::Tensor& dst) {
+void copy_h2d(const at::Tensor& src, const at::Tensor& dst, bool non_blocking) {
   c10::DeviceGuard guard(dst.device());
   const int dev = dst.get_device();
-  // Host image of dst's values in dst's dtype; dense, so one DMA moves it.
   const bool dense = dst.is_non_overlapping_and_dense();
-  at::Tensor host = dense ? at::empty_strided(dst.sizes(), dst.strides(),
-                                              dst.options().device(at::kCPU))
-                          : at::empty(dst.sizes(), dst.options().device(at::kCPU));
-  host.copy_(src);
   const size_t nbytes = static_cast<size_t>(dst.numel()) * dst.element_size();
-  hipStream_t s = stream(dev);
+  // Host image of dst's values in dst's dtype (the source itself when its
+  // bytes already are that image); dense, so it moves as one byte stream.
+  at::Tensor host;
+  if (dense && same_image(src, dst)) {
+    host = src;
+  } else {
+    host = dense ? at::empty_strided(dst.sizes(), dst.strides(), dst.options().device(at::kCPU))
+                 : at::empty(dst.sizes(), dst.options().device(at::kCPU));
+    host.copy_(src);
+  }
   if (dense) {
-    SPYRE_HIP_CHECK(hipMemcpyAsync(dst.data_ptr(), host.data_ptr(), nbytes,
-                                   hipMemcpyHostToDevice, s));
-    SPYRE_HIP_CHECK(hipStreamSynchronize(s));
+    h2d_bytes(dev, dst.data_ptr(), host, nbytes, non_blocking);
     return;
   }
   at::Tensor staging = empty_spyre(dst.sizes(), dst.scalar_type(), dst.device());
-  SPYRE_HIP_CHECK(hipMemcpyAsync(staging.data_ptr(), host.data_ptr(), nbytes,
-                                 hipMemcpyHostToDevice, s));
+  h2d_bytes(dev, staging.data_ptr(), host, nbytes, non_blocking && host.is_same(src));
   device_copy(dst, staging);
-  SPYRE_HIP_CHECK(hipStreamSynchronize(s));
 }
 
 // dst (CPU) = src (spyre).
-void copy_d2h(const at::Tensor& src, const at::Tensor& dst) {
+void copy_d2h(const at::Tensor& src, const at::Tensor& dst, bool non_blocking) {
   c10::DeviceGuard guard(src.device());
+  const int dev = src.get_device();
   at::Tensor dsrc = src.is_non_overlapping_and_dense() ? src : contiguous_on_device(src);
+  const size_t nbytes = static_cast<size_t>(dsrc.numel()) * dsrc.element_size();
+  if (same_image(dst, dsrc)) {
+    d2h_bytes(dev, dst, dsrc.data_ptr(), nbytes, non_blocking);
+    return;
+  }
   at::Tensor host = at::empty_strided(dsrc.sizes(), dsrc.strides(),
                                       dsrc.options().device(at::kCPU));
-  const size_t nbytes = static_cast<size_t>(dsrc.numel()) * dsrc.element_size();
-  hipStream_t s = stream(src.get_device());
-  if (nbytes > 0)
-    SPYRE_HIP_CHECK(hipMemcpyAsync(host.data_ptr(), dsrc.data_ptr(), nbytes,
-                                   hipMemcpyDeviceToHost, s));
-  SPYRE_HIP_CHECK(hipStreamSynchronize(s));
+  d2h_bytes(dev, host, dsrc.data_ptr(), nbytes, false);
   dst.copy_(host);
 }
 
@@ -222,18 +230,21 @@ void copy_d2d(const at::Tensor& src, const at::Tensor& dst) {
   }
   // dtype pair the kernels cannot convert (e.g. float8): convert on the host.
   at::Tensor host = src.to(at::kCPU).to(dst.scalar_type());
-  copy_h2d(host, dst);
+  copy_h2d(host, dst, false);
 }
 
 }  // namespace
 
+// non_blocking: a copy between a spyre tensor and pinned host memory
+// returns without waiting for the DMA (synchronise before touching the host
+// side); copies with pageable memory behave as if blocking, except that a
+// host-to-device copy returns once its data is staged.
 at::Tensor spyre_copy_from(const at::Tensor& self, const at::Tensor& dst, bool non_blocking) {
-  (void)non_blocking;  // copies are ordered on the spyre stream; host staging is synchronous
   if (dst.numel() == 0) return dst;
   if (self.is_cpu() && is_spyre(dst)) {
-    copy_h2d(self, dst);
+    copy_h2d(self, dst, non_blocking);
   } else if (is_spyre(self) && dst.is_cpu()) {
-    copy_d2h(self, dst);
+    copy_d2h(self, dst, non_blocking);
   } else if (is_spyre(self) && is_spyre(dst)) {
     copy_d2d(self, dst);
   } else {

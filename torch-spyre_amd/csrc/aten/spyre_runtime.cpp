@@ -86,10 +86,12 @@ hipStream_t stream(int device) {
 void synchronize(int device) {
   if (device >= 0) {
     if (g_streams[device]) SPYRE_HIP_CHECK(hipStreamSynchronize(g_streams[device]));
+    release_copy_keepalive(device);
     return;
   }
   for (int d = 0; d < device_count(); ++d)
     if (g_streams[d]) SPYRE_HIP_CHECK(hipStreamSynchronize(g_streams[d]));
+  release_copy_keepalive(-1);
 }
 
 bool has_sph(at::ScalarType t) {
@@ -337,7 +339,7 @@ class PinnedAllocator final : public c10::Allocator {
     SPYRE_HIP_CHECK(hipHostMalloc(&p, nbytes, hipHostMallocDefault));
     {
       std::lock_guard<std::mutex> lk(mu_);
-      live_.insert(p);
+      live_[reinterpret_cast<uintptr_t>(p)] = nbytes;
     }
     return {p, p, &free_pinned, cpu};
   }
@@ -345,9 +347,14 @@ class PinnedAllocator final : public c10::Allocator {
   void copy_data(void* dest, const void* src, std::size_t count) const override {
     std::memcpy(dest, src, count);
   }
+  // p inside a live block (views and offsets of pinned tensors count).
   bool owns(const void* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
     std::lock_guard<std::mutex> lk(mu_);
-    return live_.count(const_cast<void*>(p)) != 0;
+    auto it = live_.upper_bound(a);
+    if (it == live_.begin()) return false;
+    --it;
+    return a < it->first + it->second;
   }
   static PinnedAllocator& instance() {
     static PinnedAllocator* inst = new PinnedAllocator();
@@ -360,12 +367,12 @@ class PinnedAllocator final : public c10::Allocator {
     {
       auto& self = instance();
       std::lock_guard<std::mutex> lk(self.mu_);
-      self.live_.erase(p);
+      self.live_.erase(reinterpret_cast<uintptr_t>(p));
     }
     (void)hipHostFree(p);
   }
   std::mutex mu_;
-  std::unordered_set<void*> live_;
+  std::map<uintptr_t, size_t> live_;  // block base -> bytes
 };
 
 }  // namespace

@@ -59,7 +59,21 @@ bool has_sph(at::ScalarType t);
 c10::Allocator* device_allocator();
 // Pinned host memory (hipHostMalloc) for staging copies.
 c10::Allocator* pinned_allocator();
+// True for any address inside a block of pinned_allocator().
 bool is_pinned_ptr(const void* p);
+
+// Host<->device byte copies on the spyre stream of `dev` (spyre_copy.cpp).
+// `host` is a CPU tensor whose n bytes from data_ptr() are the host side.
+// Pageable host memory is staged through pinned buffers (h2d returns once
+// staged, d2h once the data is in `host`); pinned host memory is moved
+// directly and, with non_blocking, without waiting (the host storage is
+// kept alive until the copy completes).
+bool host_ptr_pinned(const void* p);
+void h2d_bytes(int dev, void* dst, const at::Tensor& host, size_t n, bool non_blocking);
+void d2h_bytes(int dev, const at::Tensor& host, const void* src, size_t n, bool non_blocking);
+// Releases the host storages held for completed non-blocking copies (-1:
+// every device); called by synchronize().
+void release_copy_keepalive(int dev);
 
 struct MemoryStats {
   int64_t allocated = 0;      // bytes in live blocks
