@@ -411,6 +411,36 @@ def test_gemm_small_m_weight_layout(m, n, k, dtype):
                     what=f"small-M {dtype}", **tol)
 
 
+@pytest.mark.parametrize("m,n,k", [(4, 25600, 4096), (4, 49155, 4096), (5, 16400, 2056),
+                                   (8, 4100, 8192), (2, 32770, 1024), (3, 4097, 8192),
+                                   (1, 4100, 8200)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_gemm_stream_decode_shapes(m, n, k, dtype):
+    # the persistent weight-stream kernel (batch 1, M <= 8, K >= 1024):
+    # K not a multiple of the 512-element lane sweep, N off the 16 waves of
+    # a workgroup, several rows per wave, K at the LDS staging limit (and
+    # just past it, on the small-M kernel)
+    _log(f"gemm stream {m}x{n}x{k} {dtype}")
+    X = uniform((m, k), k=21, dtype=dtype)
+    W = (uniform((n, k), k=22) * 0.05).to(dtype)
+    d = _gemm(X.to(DEV), W.to(DEV), trans_b=True, dtype=dtype)
+    tol = dict(rtol=1e-2, atol=1e-2) if dtype == torch.float16 else dict(rtol=2e-2, atol=2e-2)
+    assert_close_fp(d, O.gemm(X.float().numpy(), W.float().numpy().T), out_dtype=dtype,
+                    what=f"stream {dtype}", **tol)
+
+
+def test_gemm_stream_epilogue():
+    _log("gemm stream epilogue")
+    m, n, k = 4, 8192, 4096
+    X, W = uniform((m, k), k=23), uniform((n, k), k=24) * 0.02
+    bias = uniform((n,), k=25)
+    d = _gemm(X.to(DEV), W.to(DEV), trans_b=True, alpha=0.5, beta=1.5, c=bias.to(DEV), crow=0,
+              ccol=1, epi=3)
+    want = O.gemm(X.numpy(), W.numpy().T, alpha=0.5, beta=1.5, c=bias.numpy()[None, :],
+                  epilogue="silu")
+    assert_close_fp(d, want, what="stream silu epilogue")
+
+
 def test_gemm_small_m_epilogue_and_batch():
     _log("gemm small-M epilogue / batched")
     m, n, k = 4, 200, 264

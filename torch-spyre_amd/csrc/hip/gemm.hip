@@ -1144,6 +1144,145 @@ int launch_skinny(const GemmArgs& p, int64_t batch, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------------------
+// Decode-shaped products (M <= 8 activation rows against a weight matrix
+// W[N, K] read once; batch 1, K from 1024 to 8192): the weight stream is
+// the whole cost, so the kernel is built to keep as many weight bytes in
+// flight as the CU allows.
+//   * One 1024-thread workgroup per CU (persistent over the rows): the M x K
+//     activations are staged into LDS once and read from there (16-byte
+//     chunks, a wave's 64 lanes on 1 KB of consecutive bytes).
+//   * Each wave streams whole weight rows: lane l owns the 16-byte chunks
+//     l, l + 64, ... of the row, in segments of SEG chunks.  The wave walks
+//     a flat sequence of (row, segment) items and loads item i+1 into one
+//     register buffer while it computes item i from the other, so loads of
+//     the next row are in flight while a row's sums are reduced and stored.
+//   * Rows go round-robin over all waves of the grid; at the end of a row the
+//     64 lane sums per activation row are reduced by butterflies and one lane
+//     writes the M outputs (with the epilogue: alpha, beta*C, activation).
+// ---------------------------------------------------------------------------
+namespace gv {
+constexpr int WAVES = 16, THREADS = WAVES * 64, SEG = 8;
+}
+
+template <typename T, int MT, int KMAX>
+__global__ void __launch_bounds__(gv::THREADS) gemm_stream_kernel(const GemmArgs p) {
+  using namespace gv;
+  __shared__ __attribute__((aligned(16))) uint16_t As[MT * KMAX];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nc = static_cast<int>(p.k / 8);           // 16-byte chunks per row
+  const int mrows = static_cast<int>(p.m);
+  const uint16_t* A = static_cast<const uint16_t*>(p.a);
+  const uint16_t* B = static_cast<const uint16_t*>(p.b);
+  T* D = static_cast<T*>(p.d);
+  const int cpl = (nc + 63) / 64;                      // chunks per lane
+  const int nseg = (cpl + SEG - 1) / SEG;              // segments per row
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * WAVES;
+  int64_t n = static_cast<int64_t>(blockIdx.x) * WAVES + wave;
+  u32x4 wa[SEG], wb[SEG];
+  float acc[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) acc[m] = 0.f;
+
+// Weight chunks of (ROW_, SEG_) into register buffer W_ (chunks past the row
+// read a valid chunk that is not summed).
+#define SPH_GV_LOAD(W_, ROW_, SEG_)                                                         \
+  do {                                                                                      \
+    const uint16_t* rp_ = B + (ROW_) * p.ldb;                                               \
+    _Pragma("unroll") for (int j_ = 0; j_ < SEG; ++j_) {                                    \
+      int c_ = ((SEG_) * SEG + j_) * 64 + lane;                                             \
+      c_ = c_ < nc ? c_ : nc - 1;                                                           \
+      W_[j_] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rp_ + c_ * 8));    \
+    }                                                                                       \
+  } while (0)
+#define SPH_GV_COMPUTE(W_, SEG_)                                                            \
+  do {                                                                                      \
+    _Pragma("unroll") for (int j_ = 0; j_ < SEG; ++j_) {                                    \
+      const int c_ = ((SEG_) * SEG + j_) * 64 + lane;                                       \
+      if (c_ < nc) {                                                                        \
+        _Pragma("unroll") for (int m_ = 0; m_ < MT; ++m_) {                                 \
+          const u32x4 a_ = *reinterpret_cast<const u32x4*>(As + (m_ * nc + c_) * 8);        \
+          acc[m_] = dot8_acc<T>(a_, W_[j_], acc[m_]);                                       \
+        }                                                                                   \
+      }                                                                                     \
+    }                                                                                       \
+  } while (0)
+// End of row ROW_: butterflies, lane m < M writes output (m, ROW_).
+#define SPH_GV_FINISH(ROW_)                                                                 \
+  do {                                                                                      \
+    _Pragma("unroll") for (int m_ = 0; m_ < MT; ++m_) {                                     \
+      _Pragma("unroll") for (int o_ = 32; o_ > 0; o_ >>= 1) acc[m_] += __shfl_xor(acc[m_], o_, 64); \
+    }                                                                                       \
+    float v_ = acc[0];                                                                      \
+    _Pragma("unroll") for (int m_ = 1; m_ < MT; ++m_) v_ = lane == m_ ? acc[m_] : v_;       \
+    if (lane < MT && lane < mrows)                                                          \
+      D[lane * p.ldd + (ROW_)] = Num<T>::from_f(skinny_epilogue<T>(p, v_, 0, lane, (ROW_))); \
+    _Pragma("unroll") for (int m_ = 0; m_ < MT; ++m_) acc[m_] = 0.f;                        \
+  } while (0)
+
+  // The first weight loads go out before the activations are staged, so
+  // the two latencies overlap.
+  if (n < p.n) SPH_GV_LOAD(wa, n, 0);
+  // Stage the activations ([m][chunk], rows past M as zeros).
+  for (int i = threadIdx.x; i < MT * nc; i += THREADS) {
+    const int m = i / nc, c = i - m * nc;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (m < mrows) v = *reinterpret_cast<const u32x4*>(A + m * p.lda + c * 8);
+    *reinterpret_cast<u32x4*>(As + (m * nc + c) * 8) = v;
+  }
+  __syncthreads();
+  if (n >= p.n) return;  // no barrier follows
+  // Items (row, segment) in order; item i+1 loads while item i computes.
+  int s = 0;
+  while (true) {
+    int64_t n2 = s + 1 == nseg ? n + stride : n;
+    int s2 = s + 1 == nseg ? 0 : s + 1;
+    const bool more = n2 < p.n;
+    if (more) SPH_GV_LOAD(wb, n2, s2);
+    SPH_GV_COMPUTE(wa, s);
+    if (s == nseg - 1) SPH_GV_FINISH(n);
+    if (!more) break;
+    n = n2;
+    s = s2;
+    n2 = s + 1 == nseg ? n + stride : n;
+    s2 = s + 1 == nseg ? 0 : s + 1;
+    const bool more2 = n2 < p.n;
+    if (more2) SPH_GV_LOAD(wa, n2, s2);
+    SPH_GV_COMPUTE(wb, s);
+    if (s == nseg - 1) SPH_GV_FINISH(n);
+    if (!more2) break;
+    n = n2;
+    s = s2;
+  }
+#undef SPH_GV_LOAD
+#undef SPH_GV_COMPUTE
+#undef SPH_GV_FINISH
+}
+
+// Streaming kernel fit: batch 1, M <= 8, K-contiguous 16-byte aligned rows,
+// K % 8 == 0 within the LDS staging size, and at least 32 M weights
+// (64 MB of fp16).  Measured on MI355X with cold weights, x[4, 4096]: W
+// [25600, 4096] 43.6 -> 37.9 us, [49155, 4096] 68.3 -> 65.0 us against the
+// small-M kernel; at 32-50 MB of weights both are set by fixed latency and
+// within noise of each other, so those stay on the small-M kernel.
+inline bool stream_fits(const GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont) {
+  return batch == 1 && p.m >= 1 && p.m <= 8 && a_kcont && b_kcont && p.vec_a && p.vec_b &&
+         p.k >= 1024 && p.k % 8 == 0 && p.k <= 8192 && p.n >= 1024 &&
+         p.n < (1LL << 40) && p.n * p.k >= (32LL << 20);
+}
+
+template <typename T>
+int launch_stream(const GemmArgs& p, hipStream_t st) {
+  constexpr int64_t kCUs = 256;  // one workgroup per MI355X compute unit
+  const int64_t wgs = ceil_div(p.n, gv::WAVES);
+  const unsigned grid = static_cast<unsigned>(wgs < kCUs ? wgs : kCUs);
+  if (p.m <= 4)
+    gemm_stream_kernel<T, 4, 8192><<<grid, dim3(gv::THREADS), 0, st>>>(p);
+  else
+    gemm_stream_kernel<T, 8, 8192><<<grid, dim3(gv::THREADS), 0, st>>>(p);
+  return check_launch("sph_gemm (stream)");
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 template <typename T, int BM, int BN, int WM, int WN, bool FULL>
@@ -1225,6 +1364,8 @@ inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) 
 template <typename T>
 int gemm_dispatch(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
                   hipStream_t st) {
+  if (stream_fits(p, batch, a_kcont, b_kcont))
+    return launch_stream<T>(p, st);
   if (p.m <= 16 && a_kcont && b_kcont && p.vec_a && p.vec_b && p.k > 0 && p.k % 8 == 0 &&
       ceil_div(p.n, 2) < (1LL << 40))
     return launch_skinny<T>(p, batch, st);
