@@ -200,6 +200,20 @@ int sph_gemm_strided_batched(sph_dtype dtype, int trans_a, int trans_b,
                              int64_t stride_d, int epilogue,
                              sph_stream_t stream);
 
+/* D[m, j] = silu(sum_k A[m, k] W[j, k]) * (sum_k A[m, k] W[n + j, k]) for
+ * j < n: the gate and up projections of a SwiGLU MLP from one weight
+ * matrix W [2n, k] (gate rows first), both K-contiguous, and the
+ * activation product, in one GEMM (fp32 sums, one rounding to dtype).
+ * Replaces: spyre__mm_default (spyre_torch_ops.cpp:214-293) for x W^T
+ * followed by the generated silu and mul ops (Metadata.yaml base ops,
+ * base.jinja2:16-241); no single reference function corresponds (the
+ * reference does not fuse).  Needs m % 256 == 0, n % 128 == 0,
+ * k % 64 == 0 and 16-byte aligned rows; other shapes return
+ * SPH_ERR_UNSUPPORTED (compute the three steps instead). */
+int sph_gemm_swiglu(sph_dtype dtype, int64_t m, int64_t n, int64_t k, const void* a,
+                    int64_t lda, const void* w, int64_t ldw, void* d, int64_t ldd,
+                    sph_stream_t stream);
+
 /* fp16 shorthands: contiguous row-major, no transpose, no C. */
 int sph_gemm_f16(int64_t m, int64_t n, int64_t k, const void* a,
                  const void* b, void* d, sph_stream_t stream);

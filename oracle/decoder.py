@@ -17,7 +17,10 @@ inside each fused kernel: RoPE and SiLU*up round once, the scale is applied
 to the fp16 bmm output without another rounding; where the compiled program
 runs attention as one fused kernel - prefill, head dim 128, the stacked
 query rows of a KV head a multiple of 128 - the scores are not rounded at
-all, only the probabilities before the second product).
+all, only the probabilities before the second product; where it runs the
+gate / up projection and silu(gate) * up as one GEMM - prefill, rows
+% 256 == 0, intermediate % 128 == 0, hidden % 64 == 0 - gate and up are not
+rounded either).
 
 Pinned by tests/test_decoder.py against torch's CPU float32 ops with
 F.scaled_dot_product_attention (is_causal, enable_gqa) as an independent
@@ -115,8 +118,12 @@ def layer(h, w, cfg, positions, act=np.float16, kv_prefix=None, fused=False):
     a = attention(q, k, v, np.asarray(positions), k_pos, act, fused, scores_fp32=fused_attn)
     h = _r(h + _linear(a, w["wo"], act), act)
     x = _rmsnorm(h, w["mlp_norm"], cfg.eps, act)
-    gte = _linear(x, w["wg"], act)
-    up = _linear(x, w["wu"], act)
+    # the compiled prefill's fused SwiGLU GEMM keeps gate / up in fp32
+    fused_mlp = (fused and kv_prefix is None and (B * S) % 256 == 0 and
+                 cfg.intermediate % 128 == 0 and cfg.hidden % 64 == 0)
+    lin_act = None if fused_mlp else act
+    gte = _linear(x, w["wg"], lin_act)
+    up = _linear(x, w["wu"], lin_act)
     m = _r((O.silu(gte) if fused else _r(O.silu(gte), act)) * up, act)
     return _r(h + _linear(m, w["wd"], act), act), (k, v)
 

@@ -441,6 +441,40 @@ def test_gemm_stream_epilogue():
     assert_close_fp(d, want, what="stream silu epilogue")
 
 
+@pytest.mark.parametrize("m,n,k,pad", [(256, 128, 64, 0), (512, 384, 256, 8), (1024, 1280, 4096, 0),
+                                       (768, 256, 1024, 16)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_gemm_swiglu(m, n, k, pad, dtype):
+    # silu(x Wg^T) * (x Wu^T) from one [2n, k] weight (gate rows first),
+    # padded leading dims on every operand
+    _log(f"gemm swiglu {m}x{n}x{k} pad={pad} {dtype}")
+    X = uniform((m, k), k=31, dtype=dtype)
+    W = (uniform((2 * n, k), k=32) * 0.05).to(dtype)
+    xd = torch.zeros(m, k + pad, dtype=dtype, device=DEV)
+    xd[:, :k] = X.to(DEV)
+    wd = torch.zeros(2 * n, k + pad, dtype=dtype, device=DEV)
+    wd[:, :k] = W.to(DEV)
+    d = torch.full((m, n + pad), 7.0, dtype=dtype, device=DEV)
+    _capi.call("sph_gemm_swiglu", DT[dtype], m, n, k, _p(xd), k + pad, _p(wd), k + pad, _p(d),
+               n + pad, _stream())
+    _sync()
+    xf, wf = X.float().numpy(), W.float().numpy()
+    want = O.silu(O.gemm(xf, wf[:n].T)) * O.gemm(xf, wf[n:].T)
+    tol = dict(rtol=1e-2, atol=1e-2) if dtype == torch.float16 else dict(rtol=2e-2, atol=2e-2)
+    assert_close_fp(d[:, :n], want, out_dtype=dtype, what=f"swiglu {dtype}", **tol)
+    if pad:
+        assert bool((d[:, n:] == 7.0).all()), "padding columns written"
+
+
+def test_gemm_swiglu_rejects_unfit_shapes():
+    x = torch.zeros(200, 64, dtype=torch.float16, device=DEV)
+    w = torch.zeros(256, 64, dtype=torch.float16, device=DEV)
+    d = torch.zeros(200, 128, dtype=torch.float16, device=DEV)
+    rc = _capi.lib().sph_gemm_swiglu(_capi.F16, 200, 128, 64, _p(x), 64, _p(w), 64, _p(d), 128,
+                                     _stream())
+    assert rc == 1002  # SPH_ERR_UNSUPPORTED: m % 256 != 0
+
+
 def test_gemm_small_m_epilogue_and_batch():
     _log("gemm small-M epilogue / batched")
     m, n, k = 4, 200, 264

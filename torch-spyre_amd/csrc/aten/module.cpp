@@ -20,6 +20,8 @@ namespace spyre {
 int64_t load_kernel(const std::string& code_object, const std::string& name);
 void launch_kernel(int64_t handle, const std::vector<at::Tensor>& args, int64_t grid,
                    int64_t block, const std::vector<int64_t>& extents);
+// Fused SwiGLU projection (ops_gemm.cpp).
+at::Tensor gemm_swiglu(const at::Tensor& x, const at::Tensor& w);
 // Fused attention (ops_attention.cpp).
 at::Tensor attention_fwd(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                          const c10::optional<at::Tensor>& mask, double scale, int64_t causal_q,
@@ -45,6 +47,8 @@ PYBIND11_MODULE(_C, m) {
         py::arg("mask"), py::arg("scale"), py::arg("causal_q") = 0, py::arg("causal_off") = 0,
         "softmax(scale * q k^T + mask) v on the spyre stream (q [B, mq, 128], k / v "
         "[B, sk, 128], mask [mq, sk] / [B or 1, mq, sk] or None; fp16 / bf16).");
+  m.def("gemm_swiglu", &spyre::gemm_swiglu, py::arg("x"), py::arg("w"),
+        "silu(x w[:n]^T) * (x w[n:]^T) on the spyre stream (x [M, K], w [2n, K]).");
   m.def("device_count", []() { return spyre::device_count(); });
   m.def("current_device", []() { return spyre::current_device(); });
   m.def("set_device", [](int d) { spyre::set_device(d); });

@@ -188,6 +188,40 @@ at::Tensor& baddbmm_out(const at::Tensor& self, const at::Tensor& b1, const at::
 
 }  // namespace
 
+// silu(x w[:n]^T) * (x w[n:]^T) for x [M, K], w [2n, K] on spyre: one fused
+// GEMM (sph_gemm_swiglu) when the shape fits it, else the three device ops
+// (mm, silu, mul) with the rounding the unfused program has.
+at::Tensor gemm_swiglu(const at::Tensor& x_in, const at::Tensor& w_in) {
+  TORCH_CHECK(is_spyre(x_in) && is_spyre(w_in), "spyre swiglu_mm: spyre tensors expected");
+  TORCH_CHECK(x_in.dim() == 2 && w_in.dim() == 2 && x_in.size(1) == w_in.size(1) &&
+                  w_in.size(0) % 2 == 0,
+              "spyre swiglu_mm: x [M, K] and w [2n, K] expected");
+  check_gemm_dtype(x_in, w_in, "swiglu_mm");
+  const int64_t m = x_in.size(0), k = x_in.size(1), n = w_in.size(0) / 2;
+  at::Tensor out = empty_spyre({m, n}, x_in.scalar_type(), x_in.device());
+  if (out.numel() == 0) return out;
+  at::Tensor x = x_in.stride(1) == 1 ? x_in : contiguous_on_device(x_in);
+  at::Tensor w = w_in.stride(1) == 1 ? w_in : contiguous_on_device(w_in);
+  c10::DeviceGuard guard(out.device());
+  const bool fits = m % 256 == 0 && n % 128 == 0 && k % 64 == 0 && k > 0 &&
+                    x.stride(0) % 8 == 0 && w.stride(0) % 8 == 0 &&
+                    reinterpret_cast<uintptr_t>(x.data_ptr()) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(w.data_ptr()) % 16 == 0;
+  if (fits) {
+    check_matrix_extent(x, x.data_ptr(), m, k, x.stride(0), 0, 1, 0, "swiglu_mm x");
+    check_matrix_extent(w, w.data_ptr(), 2 * n, k, w.stride(0), 0, 1, 0, "swiglu_mm w");
+    const int rc = sph_gemm_swiglu(to_sph(out.scalar_type()), m, n, k, x.data_ptr(), x.stride(0),
+                                   w.data_ptr(), w.stride(0), out.data_ptr(), n,
+                                   stream(out.get_device()));
+    if (rc == 0) return out;
+    TORCH_CHECK(rc == SPH_ERR_UNSUPPORTED || rc == SPH_ERR_TOO_LARGE, "spyre: sph_gemm_swiglu failed (status ",
+                rc, "): ", sph_last_error());
+  }
+  at::Tensor gu = at::mm(x, w.t());
+  out.copy_(at::silu(gu.narrow(1, 0, n)) * gu.narrow(1, n, n));
+  return out;
+}
+
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("mm.out", TORCH_FN(mm_out));
   m.impl("bmm.out", TORCH_FN(bmm_out));

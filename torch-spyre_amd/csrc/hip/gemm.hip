@@ -591,10 +591,18 @@ struct Cfg {
 };
 }  // namespace dl
 
-template <typename T, bool B_KCONT, int BN_>
+// SWIGLU: B holds the gate rows [0, n) and the up rows [n, 2n) of one
+// weight matrix (K-contiguous) and D[m, j] = silu(A B_gate[j]) * (A B_up[j]).
+// A 256-wide tile then covers 128 output columns: in the 64 columns of wave
+// wn, MFMA tile 0 takes gate rows j0 + 32 wn .. + 31 and tile 1 the up rows
+// of the same columns, so each lane's two accumulators hold the gate and up
+// sums of the same output element and the epilogue combines them in
+// registers.
+template <typename T, bool B_KCONT, int BN_, bool SWIGLU = false>
 __global__ void __launch_bounds__(dl::Cfg<BN_>::NT) gemm_dl_kernel(const GemmArgs p) {
   using namespace dl;
   using DC = Cfg<BN_>;
+  static_assert(!SWIGLU || (B_KCONT && BN_ == 256), "SwiGLU tiles: K-contiguous B, 256 wide");
   constexpr int BN = DC::BN, WN = DC::WN, STAGE = DC::STAGE, LPA = DC::LPA, LPB = DC::LPB;
   constexpr int NBR = B_KCONT ? 1 : 2;           // LDS reads per B fragment
   constexpr int NDS = TM + TN * NBR;             // LDS reads per sub-step
@@ -604,7 +612,8 @@ __global__ void __launch_bounds__(dl::Cfg<BN_>::NT) gemm_dl_kernel(const GemmArg
   int tm, tn;
   tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
   const int64_t batch = blockIdx.y;
-  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+  // first output column (SwiGLU: 128 output columns per tile)
+  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * (SWIGLU ? BN / 2 : BN);
   const uint16_t* A = static_cast<const uint16_t*>(p.a) + batch * p.stride_a;
   const uint16_t* B = static_cast<const uint16_t*>(p.b) + batch * p.stride_b;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -614,7 +623,10 @@ __global__ void __launch_bounds__(dl::Cfg<BN_>::NT) gemm_dl_kernel(const GemmArg
 
   // Buffer ranges: exactly the bytes this tile's rows (columns) span.
   const i32x4 ra = buffer_rsrc(A + m0 * lda, static_cast<uint32_t>(((BM - 1) * static_cast<int64_t>(lda) + p.k) * 2));
-  const i32x4 rb = B_KCONT
+  // (SwiGLU: from gate row n0 to up row n + n0 + 127)
+  const i32x4 rb = SWIGLU
+      ? buffer_rsrc(B + n0 * ldb, static_cast<uint32_t>(((p.n + BN / 2 - 1) * static_cast<int64_t>(ldb) + p.k) * 2))
+      : B_KCONT
       ? buffer_rsrc(B + n0 * ldb, static_cast<uint32_t>(((BN - 1) * static_cast<int64_t>(ldb) + p.k) * 2))
       : buffer_rsrc(B + n0, static_cast<uint32_t>(((p.k - 1) * ldb + BN) * 2));
   // Per-lane global byte offsets of this wave's DMA lines (K tile 0).
@@ -628,7 +640,13 @@ __global__ void __launch_bounds__(dl::Cfg<BN_>::NT) gemm_dl_kernel(const GemmArg
 #pragma unroll
   for (int i = 0; i < LPB; ++i) {
     const int s = (wave * LPB + i) * 64 + lane;
-    if constexpr (B_KCONT) {
+    if constexpr (SWIGLU) {
+      // LDS row r (tile column) -> weight row: gate j0 + 32 (r / 64) + r % 32
+      // for r % 64 < 32, else the matching up row (+ n)
+      const int r = s / CPR, c = (s % CPR) ^ ((r >> 1) & 7);
+      const int64_t wr = 32 * (r >> 6) + (r & 31) + ((r & 32) ? p.n : 0);
+      vb[i] = static_cast<uint32_t>(wr * ldb * 2 + c * 16);
+    } else if constexpr (B_KCONT) {
       const int r = s / CPR, c = (s % CPR) ^ ((r >> 1) & 7);
       vb[i] = static_cast<uint32_t>(r * ldb * 2 + c * 16);
     } else {
@@ -765,18 +783,35 @@ __global__ void __launch_bounds__(dl::Cfg<BN_>::NT) gemm_dl_kernel(const GemmArg
   const T* C = p.c ? static_cast<const T*>(p.c) + batch * p.stride_c : nullptr;
   float* slab = reinterpret_cast<float*>(lds) + wave * (32 * EPITCH);
   const int64_t row0 = m0 + wm * WTM;
-  const int64_t colw = n0 + wn * WTN;
+  if constexpr (SWIGLU) {
+    // silu(gate) * up per element, 32 output columns per wave
+    static_assert(TN == 2, "gate / up tile pair");
+    constexpr int SP = 32 + 8;
+    const int64_t colw = n0 + wn * 32;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
+    for (int i = 0; i < TM; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        slab[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * EPITCH + j * 32 + (lane & 31)] =
-            acc[i][j][r];
-    __syncthreads();
-    store_slab<T, WTN, EPITCH>(p, slab, D, C, row0 + i * 32, colw, lane);
-    __syncthreads();
+        slab[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * SP + (lane & 31)] =
+            silu(acc[i][0][r]) * acc[i][1][r];
+      __syncthreads();
+      store_slab<T, 32, SP>(p, slab, D, C, row0 + i * 32, colw, lane);
+      __syncthreads();
+    }
+  } else {
+    const int64_t colw = n0 + wn * WTN;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          slab[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * EPITCH + j * 32 + (lane & 31)] =
+              acc[i][j][r];
+      __syncthreads();
+      store_slab<T, WTN, EPITCH>(p, slab, D, C, row0 + i * 32, colw, lane);
+      __syncthreads();
+    }
   }
 }
 
@@ -1477,6 +1512,47 @@ extern "C" int sph_gemm(sph_dtype dtype, int trans_a, int trans_b, int64_t m,
   return sph_gemm_strided_batched(dtype, trans_a, trans_b, 1, m, n, k, alpha, a,
                                   lda, 0, b, ldb, 0, beta, c, ldc_row, ldc_col,
                                   0, d, ldd, 0, epilogue, stream);
+}
+
+extern "C" int sph_gemm_swiglu(sph_dtype dtype, int64_t m, int64_t n, int64_t k, const void* a,
+                               int64_t lda, const void* w, int64_t ldw, void* d, int64_t ldd,
+                               sph_stream_t stream) {
+  SPH_REQUIRE(m >= 0 && n >= 0 && k >= 0, SPH_ERR_INVALID_ARG, "gemm_swiglu: negative size");
+  SPH_REQUIRE(dtype == SPH_F16 || dtype == SPH_BF16, SPH_ERR_UNSUPPORTED,
+              "gemm_swiglu: dtype must be F16 or BF16");
+  if (m == 0 || n == 0) return SPH_OK;
+  SPH_REQUIRE(m % dl::BM == 0 && n % 128 == 0 && k > 0 && k % dl::BKD == 0, SPH_ERR_UNSUPPORTED,
+              "gemm_swiglu: needs m % 256 == 0, n % 128 == 0, k % 64 == 0");
+  SPH_REQUIRE(lda >= k && ldw >= k && ldd >= n, SPH_ERR_INVALID_ARG,
+              "gemm_swiglu: leading dimension too small");
+  SPH_REQUIRE(al16(a) && al16(w) && al16(d) && lda % 8 == 0 && ldw % 8 == 0 && ldd % 8 == 0,
+              SPH_ERR_UNSUPPORTED, "gemm_swiglu: rows must be 16-byte aligned");
+  constexpr int64_t kLim = 1LL << 31;
+  SPH_REQUIRE(((dl::BM - 1) * lda + k) * 2 < kLim && ((n + 127) * ldw + k) * 2 < kLim &&
+                  (m / dl::BM) * (n / 128) < kLim,
+              SPH_ERR_TOO_LARGE, "gemm_swiglu: operands too large for 32-bit tile offsets");
+  GemmArgs p{};
+  p.m = m;
+  p.n = n;
+  p.k = k;
+  p.a = a;
+  p.lda = lda;
+  p.b = w;
+  p.ldb = ldw;
+  p.d = d;
+  p.ldd = ldd;
+  p.alpha = 1.f;
+  p.epilogue = SPH_EPI_NONE;
+  p.vec_a = p.vec_b = p.vec_d = 1;
+  p.tiles_m = static_cast<int>(m / dl::BM);
+  p.tiles_n = static_cast<int>(n / 128);
+  const dim3 grid(static_cast<unsigned>(p.tiles_m) * p.tiles_n);
+  hipStream_t st = as_stream(stream);
+  if (dtype == SPH_F16)
+    gemm_dl_kernel<half_t, true, 256, true><<<grid, dim3(dl::Cfg<256>::NT), 0, st>>>(p);
+  else
+    gemm_dl_kernel<bf16_t, true, 256, true><<<grid, dim3(dl::Cfg<256>::NT), 0, st>>>(p);
+  return check_launch("sph_gemm_swiglu");
 }
 
 extern "C" int sph_gemm_f16(int64_t m, int64_t n, int64_t k, const void* a,

@@ -257,3 +257,30 @@ def _(q, k, v, mask, scale):
 @attention.register_fake
 def _(q, k, v, mask, scale):
     return q.new_empty((q.shape[0], q.shape[1], v.shape[2]))
+
+
+# ---- fused SwiGLU projection ------------------------------------------------
+
+@torch.library.custom_op("spyre::swiglu_mm", mutates_args=())
+def swiglu_mm(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """silu(x w[:n]^T) * (x w[n:]^T) for x [M, K] and the stacked gate / up
+    weight w [2n, K]: the gate and up projections of a SwiGLU MLP with the
+    activation product.  On other devices it runs as the unfused chain the
+    reference would run (spyre__mm_default, spyre_torch_ops.cpp:214-293, then
+    the generated silu and mul ops); on spyre as one GEMM whose epilogue
+    forms silu(gate) * up from the fp32 sums."""
+    n = w.shape[0] // 2
+    gu = torch.mm(x, w.t())
+    return torch.nn.functional.silu(gu[:, :n]) * gu[:, n:]
+
+
+@swiglu_mm.register_kernel("spyre")
+def _(x, w):
+    from torch_spyre import _C
+
+    return _C.gemm_swiglu(x, w)
+
+
+@swiglu_mm.register_fake
+def _(x, w):
+    return x.new_empty((x.shape[0], w.shape[0] // 2))
