@@ -159,6 +159,50 @@ def bench_extra(steps, warmup, stream, capi):
     return out
 
 
+def bench_attention(steps, warmup, stream, capi):
+    """c4's attention as one fused kernel (sph_attention_fwd): 8 KV heads x
+    4 stacked query heads x 2048 positions, head dim 128, fp16, with c4's
+    additive causal mask (block pre-pass included) and without a mask.
+    MFMA-bound: 4 mq sk d FLOP per batch element dense; the causal figure
+    counts the visible (lower-triangle) share."""
+    import math
+
+    import torch
+
+    s = stream.cuda_stream
+    lib = capi.lib()
+    B, MQ, SK, D = 8, 8192, 2048, 128
+    q = torch.randn(B, MQ, D, generator=_gen(40)).half().cuda()
+    k = torch.randn(B, SK, D, generator=_gen(41)).half().cuda()
+    v = torch.randn(B, SK, D, generator=_gen(42)).half().cuda()
+    o = torch.empty_like(q)
+    mask = torch.full((SK, SK), float("-inf")).triu(1).repeat(MQ // SK, 1).half().cuda()
+    nws = lib.sph_attention_workspace_bytes(B, MQ, SK, 0)
+    ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
+    sc = 1 / math.sqrt(D)
+    timer = Timer(stream)
+
+    def run(mp, w):
+        capi.check(lib.sph_attention_fwd(capi.F16, B, MQ, SK, D, q.data_ptr(), D, MQ * D,
+                                         k.data_ptr(), D, SK * D, v.data_ptr(), D, SK * D, mp,
+                                         SK if mp else 0, 0, 0, 0, sc, o.data_ptr(), D, MQ * D,
+                                         w, nws if w else 0, s), "sph_attention_fwd")
+
+    dense = 4.0 * B * MQ * SK * D
+    visible = dense * (SK + 1) / (2 * SK)
+    out = {}
+    ms, _ = timer.run(lambda: run(mask.data_ptr(), ws.data_ptr()), steps, warmup)
+    out["c4_attention_causal_mask"] = {
+        "us_per_launch": round(ms * 1e3, 2), "visible_flop": visible,
+        "TFLOP/s": round(visible / ms / 1e9, 1),
+        "roofline_frac": round(visible / ms / 1e9 / PEAK_FP16_TFLOPS, 4), "bound": "mfma"}
+    ms, _ = timer.run(lambda: run(None, None), steps, warmup)
+    out["c4_attention_no_mask"] = {
+        "us_per_launch": round(ms * 1e3, 2), "flop": dense, "TFLOP/s": round(dense / ms / 1e9, 1),
+        "roofline_frac": round(dense / ms / 1e9 / PEAK_FP16_TFLOPS, 4), "bound": "mfma"}
+    return out
+
+
 def bench_bmm(steps, warmup, stream, capi):
     """c2 bmm 32 x [2048,128] x [128,2048]: HBM-bound (AI 113.8 < ridge 314.6)."""
     import torch
@@ -447,6 +491,69 @@ def bench_eager_mm(steps, warmup):
     return {"ms_per_call": round(ms, 4), "TFLOP/s": round(2 * 4096 ** 3 / (ms * 1e-3) / 1e12, 1)}
 
 
+def cpu_per_config():
+    """The CPU side of every config, timed on this host in the same run:
+    the oracle's numpy restatements for c1 (softmax) and c3 (norms, GELU
+    chain) on the full or a row-sliced input, and the decoder's own torch
+    code run eagerly on CPU tensors (the reference's compare-with-CPU path)
+    for c4 and c5 on a bounded sample.  Figures are in the unit of the
+    config, with the sample stated; ~20 s in total."""
+    import numpy as np
+    import torch
+
+    from oracle import ops as O
+    from torch_spyre.examples import decoder as D
+
+    def timed(fn, min_s=1.0, min_reps=3):
+        fn()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= min_s and reps >= min_reps:
+                return el / reps, reps
+
+    out = {"threads": torch.get_num_threads()}
+    g = np.random.default_rng(SEED)
+    x = (g.standard_normal((512, 4096), dtype=np.float32) * 4).astype(np.float16)
+    t, n = timed(lambda: O.softmax(x))
+    out["c1_softmax_512x4096"] = {"GB/s": round(2 * x.size * 2 / t / 1e9, 2), "reps": n,
+                                  "sample": "full input, oracle.ops.softmax (numpy)"}
+    rows, C = 1024, 4096
+    xr = g.standard_normal((rows, C), dtype=np.float32).astype(np.float16)
+    rr = g.standard_normal((rows, C), dtype=np.float32).astype(np.float16)
+    w = (1 + 0.02 * g.standard_normal(C, dtype=np.float32)).astype(np.float16)
+    bb = (0.02 * g.standard_normal(C, dtype=np.float32)).astype(np.float16)
+    nb = 4 * rows * C * 2
+    t, n = timed(lambda: O.rmsnorm(xr, w, residual=rr))
+    out["c3_add_rmsnorm"] = {"GB/s": round(nb / t / 1e9, 2), "reps": n,
+                             "sample": f"rows 0..{rows} of 8192, oracle.ops.rmsnorm"}
+    t, n = timed(lambda: O.layernorm(xr, w, bb, residual=rr))
+    out["c3_add_layernorm"] = {"GB/s": round(nb / t / 1e9, 2), "reps": n,
+                               "sample": f"rows 0..{rows} of 8192, oracle.ops.layernorm"}
+    t, n = timed(lambda: O.gelu_affine_rowsum(xr, w, bb))
+    out["c3_gelu_rowsum"] = {"GB/s": round(2 * rows * C * 2 / t / 1e9, 2), "reps": n,
+                             "sample": f"rows 0..{rows} of 8192, oracle.ops.gelu_affine_rowsum"}
+    # c4 / c5: the decoder code itself on CPU tensors (fp32: torch's fp16
+    # CPU matmul is far slower, so this is the faster CPU figure)
+    cfg = D.C4
+    S = 256
+    params = D.init_params(cfg, "cpu", dtype=torch.float32, pool_elems=1 << 24)
+    cos, sin = D.rope_tables(cfg, S, "cpu", torch.float32)
+    mask = D.causal_mask(cfg, S, "cpu", torch.float32)
+    tok = torch.randint(0, cfg.vocab, (1, S), generator=torch.Generator().manual_seed(SEED))
+    with torch.no_grad():
+        t, n = timed(lambda: D.block_forward(tok, params, cos, sin, mask, cfg), min_s=3.0)
+    out["c4_layer_prefill"] = {"tok/s": round(S / t, 1), "reps": n,
+                               "sample": f"c4 layer (embedding + 1 layer) at seq {S} of 2048, "
+                                         "torch eager fp32 on CPU (decoder.block_forward)"}
+    out["c5_prefill_estimate"] = {
+        "tok/s": round(S / t / 40, 1),
+        "sample": "the c4 layer rate divided by c5's 40 layers (LM head not included)"}
+    return out
+
+
 def cpu_baseline_gemm(a, b):
     """Oracle GEMM (numpy fp32) on a bounded row slice of the same problem,
     timed on this host's cores."""
@@ -488,10 +595,11 @@ def main(argv=None):
     ap.add_argument("--no-decoder", action="store_true")
     ap.add_argument("--c5-layers", type=int, default=40)
     ap.add_argument("--decode-steps", type=int, default=128)
-    ap.add_argument("--kernel", choices=["all", "gemm", "copy", "decoder", "bmm", "h2d"],
+    ap.add_argument("--kernel", choices=["all", "gemm", "copy", "decoder", "bmm", "h2d",
+                                         "attention"],
                     default="all",
-                    help="gemm / copy / decoder / bmm / h2d: run only that part (for rocprofv3 "
-                         "passes)")
+                    help="gemm / copy / decoder / bmm / h2d / attention: run only that part "
+                         "(for rocprofv3 passes)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; runs on more than one GPU are not "
@@ -512,6 +620,10 @@ def main(argv=None):
     if args.kernel == "bmm":
         print(json.dumps({"kernel": "bmm", **bench_bmm(args.steps, args.warmup, stream, _capi)}))
         return 0
+    if args.kernel == "attention":
+        print(json.dumps({"kernel": "attention",
+                          **bench_attention(args.steps, args.warmup, stream, _capi)}))
+        return 0
     if args.kernel == "h2d":
         print(json.dumps({"kernel": "h2d", **bench_host_copies()}))
         return 0
@@ -531,6 +643,8 @@ def main(argv=None):
         extra["c2_mm_4096_spyre_device_eager"] = bench_eager_mm(max(10, args.steps), args.warmup)
         _log("spyre device paths (eager + torch.compile)")
         extra["spyre_device"] = bench_spyre_paths(max(10, args.steps), args.warmup)
+        _log("fused attention (c4 shape)")
+        extra.update(bench_attention(max(10, args.steps), args.warmup, stream, _capi))
         _log("host<->device copies")
         extra["host_device_copy"] = bench_host_copies()
         if not args.no_decoder:
@@ -540,6 +654,9 @@ def main(argv=None):
     if not args.no_cpu:
         _log("cpu baseline")
         cpu = cpu_baseline_gemm(g["a"], g["b"])
+        if not args.no_extra:
+            _log("cpu side of every config")
+            extra["cpu_per_config"] = cpu_per_config()
     tflops = g["tflops"]
     line = {
         "metric": "fp16 GEMM TFLOP/s (M=N=K=4096, fp32 accumulate)",
