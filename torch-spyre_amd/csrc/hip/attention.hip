@@ -38,11 +38,15 @@
 //     the key range between its first and last block that is not all -inf,
 //     skips all -inf blocks inside it and loads mask values only for mixed
 //     blocks - a causal mask then costs what the causal-position mode costs.
-//   * Causal work per workgroup grows with its query position.  The 1-D grid
-//     runs row blocks last-first in its first half and first-first in its
-//     second half, so the two workgroups a CU holds at once are row blocks
-//     rb and nbq-1-rb: for causal rows (also with heads stacked along the
-//     rows) their key counts add up to about the same total on every CU.
+//   * A workgroup is 8 waves in two groups of 4 on the same 128 query rows:
+//     group g takes the key blocks kb with kb % 2 == g, each group with its
+//     own two-stage LDS ring, and the two partial softmax states merge
+//     through LDS at the end.  One workgroup fills a CU (two waves per
+//     SIMD), so the grid is longer than the CU count and its order matters:
+//     jobs run longest first (causal positions: by position block; masks:
+//     by the number of key blocks the mask leaves, counted and sorted on the
+//     device from the block classes), so short jobs fill in behind long
+//     ones.
 #include "sph_common.h"
 
 namespace sph {
@@ -64,6 +68,7 @@ constexpr int KBLK = AK * KPITCH;         // 17408 bytes: 17 DMA lines of 1 KB
 constexpr int VBLK = AK * AD * 2;         // 16384 bytes: 16 lines
 constexpr int KLINES = KBLK / 1024, VLINES = VBLK / 1024;
 constexpr int STAGE = KBLK + VBLK;
+constexpr int kMaxOrderBins = 4097;  // key blocks + 1 the job sort handles
 static_assert(KBLK % 1024 == 0 && VBLK % 1024 == 0, "whole DMA lines");
 
 struct AttnArgs {
@@ -78,10 +83,13 @@ struct AttnArgs {
   int64_t ldm, smb;
   int64_t causal_q, causal_off;
   int64_t batch, nbq;   // batch, query blocks per batch element (mq / 128)
+  int64_t heads;        // > 0: causal rows are `heads` stacked runs of causal_q
+  const int32_t* order; // job order (b * nbq + rb), longest first, or null
   const uint8_t* mblk;  // mask block classes [mask batch][nbq][nkb] or null
   int64_t mblk_b;       // row blocks per mask batch in mblk (0: one mask for all)
   int64_t nkb;          // key blocks (ceil(sk / 64))
-  float scale_log2;  // scale * log2(e)
+  float scale_log2;  // scale * log2(e) (scale > 0)
+  float inv_scale;   // 1 / scale: masks join the raw scores as mask / scale
   void* o;
   int64_t ldo, so;
 };
@@ -166,20 +174,78 @@ __global__ void __launch_bounds__(256) mask_blocks_kernel(const uint16_t* __rest
   if (t == 0) out[(mb * nbq + rb) * nkb + kb] = !anyfin ? MB_NEGINF : (anynz ? MB_MIXED : MB_ZERO);
 }
 
+// One workgroup: the jobs (b * nbq + rb) counting-sorted by the number of
+// key blocks their mask leaves (first to last block not all -inf), longest
+// first, into order[].  The classes of every job (jobs * nkb bytes, at most
+// kMaxOrderBytes) are staged in LDS with 16-byte loads first.  Ties keep no
+// particular order.
+constexpr int kMaxOrderBytes = 48 * 1024;
+__global__ void __launch_bounds__(1024) attn_order_kernel(const uint8_t* __restrict__ mblk,
+                                                          int64_t mblk_b, int nkb, int nbq,
+                                                          int jobs, int32_t* __restrict__ order) {
+  __shared__ __attribute__((aligned(16))) uint8_t cls[kMaxOrderBytes];
+  __shared__ int cnt[kMaxOrderBins];
+  // the class rows are contiguous per mask batch: [mask batch][rb][kb]
+  const int per_mb = nbq * nkb, nmb = mblk_b == 0 ? 1 : jobs / nbq;
+  const int total = nmb * per_mb;
+  for (int i = threadIdx.x * 16; i < total; i += 1024 * 16) {
+    if (i + 16 <= total && ((reinterpret_cast<uintptr_t>(mblk) + i) & 15) == 0)
+      *reinterpret_cast<u32x4*>(cls + i) = *reinterpret_cast<const u32x4*>(mblk + i);
+    else
+      for (int e = i; e < i + 16 && e < total; ++e) cls[e] = mblk[e];
+  }
+  for (int i = threadIdx.x; i <= nkb; i += 1024) cnt[i] = 0;
+  __syncthreads();
+  auto work = [&](int job) {
+    const uint8_t* c = cls + ((mblk_b == 0 ? 0 : job / nbq) * nbq + job % nbq) * nkb;
+    int lo = -1, hi = -1;
+    for (int kb = 0; kb < nkb; ++kb)
+      if (c[kb] != MB_NEGINF) {
+        lo = lo < 0 ? kb : lo;
+        hi = kb;
+      }
+    return hi < 0 ? 0 : hi - lo + 1;
+  };
+  for (int jb = threadIdx.x; jb < jobs; jb += 1024) atomicAdd(&cnt[work(jb)], 1);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int off = 0;
+    for (int w = nkb; w >= 0; --w) {
+      const int c = cnt[w];
+      cnt[w] = off;
+      off += c;
+    }
+  }
+  __syncthreads();
+  for (int jb = threadIdx.x; jb < jobs; jb += 1024) order[atomicAdd(&cnt[work(jb)], 1)] = jb;
+}
+
 template <typename T, bool MASK, bool CAUSAL>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
 attn_fwd_kernel(const AttnArgs p) {
-  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds[4 * STAGE];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // Workgroup order: first half row blocks descending, second half ascending
-  // (u = rank in a row-block-descending list), so workgroups wg and
-  // wg + half take row blocks rb and nbq-1-rb.
-  const int64_t wg = blockIdx.x, total = p.batch * p.nbq, half = total / 2;
-  const int64_t u = wg < half ? wg : total - 1 - (wg - half);
-  const int64_t rb = p.nbq - 1 - u / p.batch, b = u % p.batch;
+  const int grp = wave >> 2, wq = wave & 3;  // key-block group, wave within it (its rows)
+  // The job: batch element b, row block rb.
+  int64_t b, rb;
+  const int64_t wg = blockIdx.x;
+  if (p.order != nullptr) {
+    const int64_t job = p.order[wg];
+    b = job / p.nbq;
+    rb = job % p.nbq;
+  } else if (CAUSAL && p.heads > 0) {
+    // longest first: position block descending, then batch and head
+    const int64_t per = p.batch * p.heads, nbh = p.nbq / p.heads;
+    const int64_t pb = nbh - 1 - wg / per, rem = wg % per;
+    b = rem / p.heads;
+    rb = (rem % p.heads) * nbh + pb;
+  } else {
+    b = wg / p.nbq;
+    rb = wg % p.nbq;
+  }
   const int64_t r0 = rb * AQ;                                 // first row of the workgroup
-  const int64_t qrow = r0 + wave * 32 + (lane & 31);         // this lane's query row
+  const int64_t qrow = r0 + wq * 32 + (lane & 31);           // this lane's query row
   const int h = lane >> 5;
 
   // Key blocks this workgroup walks: [kb0, kb1).
@@ -210,7 +276,16 @@ attn_fwd_kernel(const AttnArgs p) {
     kb0 = __builtin_amdgcn_readfirstlane(hi < 0 ? 0 : lo);
     kb1 = __builtin_amdgcn_readfirstlane(hi + 1);
   }
-  const int64_t qpos = CAUSAL ? qrow % p.causal_q + p.causal_off : 0;
+  // causal position of this lane's row and the smallest over the wave's 32
+  // rows (blocks wholly at or below it need no per-key position check)
+  const int qpos = CAUSAL ? static_cast<int>(qrow % p.causal_q + p.causal_off) : 0;
+  int qpos_min = qpos;
+  if constexpr (CAUSAL) {
+#pragma unroll
+    for (int d = 16; d >= 1; d >>= 1) qpos_min = min(qpos_min, __shfl_xor(qpos_min, d, 64));
+    qpos_min = __builtin_amdgcn_readfirstlane(qpos_min);
+  }
+  const int sk32 = static_cast<int>(p.sk);
 
   // Q fragments: query qrow, head dims 16 kk + 8 h .. + 7.
   const uint16_t* Q = static_cast<const uint16_t*>(p.q) + b * p.sq + qrow * p.ldq;
@@ -227,35 +302,36 @@ attn_fwd_kernel(const AttnArgs p) {
   // its last valid key, so rows past sk read zeros.
   const uint16_t* Kb = static_cast<const uint16_t*>(p.k) + b * p.skb;
   const uint16_t* Vb = static_cast<const uint16_t*>(p.v) + b * p.svb;
-  // lines handled by this wave: K lines wave, wave+4, ... (< 17), V lines 4 per wave
+  // lines handled by this wave of its group: K lines wq, wq+4, ... (< 17),
+  // V lines 4 per wave
   constexpr int KLW = (KLINES + 3) / 4, VLW = VLINES / 4;
   uint32_t vk[KLW], vv[VLW];
 #pragma unroll
   for (int i = 0; i < KLW; ++i) {
-    const int s = (wave + 4 * i) * 64 + lane;
+    const int s = (wq + 4 * i) * 64 + lane;
     const int r = s / 17, c = s % 17;
     vk[i] = c < 16 ? static_cast<uint32_t>(r * p.ldk * 2 + c * 16) : 0xffffffffu;
   }
 #pragma unroll
   for (int i = 0; i < VLW; ++i) {
-    const int L = wave * VLW + i;
+    const int L = wq * VLW + i;
     const int dt = L >> 2, key = (L & 3) * 16 + (lane >> 2), c = 4 * dt + (lane & 3);
     vv[i] = static_cast<uint32_t>(key * p.ldv * 2 + c * 16);
   }
   const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((SPH_LDS char*)(lds)));
-  auto issue = [&](int blk, int st) {
-    const uint32_t sbase = lds_base + st * STAGE;
+  auto issue = [&](int blk, int slot) {  // this group's ring slot
+    const uint32_t sbase = lds_base + (grp * 2 + slot) * STAGE;
     const int64_t key0 = static_cast<int64_t>(blk) * AK;
     const int64_t nk = p.sk - key0 < AK ? p.sk - key0 : AK;
     const i32x4 rk = buffer_rsrc(Kb + key0 * p.ldk, static_cast<uint32_t>(((nk - 1) * p.ldk + AD) * 2));
     const i32x4 rv = buffer_rsrc(Vb + key0 * p.ldv, static_cast<uint32_t>(((nk - 1) * p.ldv + AD) * 2));
 #pragma unroll
     for (int i = 0; i < KLW; ++i)
-      if (wave + 4 * i < KLINES)
-        dma16(rk, __builtin_amdgcn_readfirstlane(sbase + (wave + 4 * i) * 1024), vk[i], 0u);
+      if (wq + 4 * i < KLINES)
+        dma16(rk, __builtin_amdgcn_readfirstlane(sbase + (wq + 4 * i) * 1024), vk[i], 0u);
 #pragma unroll
     for (int i = 0; i < VLW; ++i)
-      dma16(rv, __builtin_amdgcn_readfirstlane(sbase + KBLK + (wave * VLW + i) * 1024), vv[i], 0u);
+      dma16(rv, __builtin_amdgcn_readfirstlane(sbase + KBLK + (wq * VLW + i) * 1024), vv[i], 0u);
   };
 
   // Fragment read bases of this lane (block-relative bytes): K row
@@ -269,26 +345,46 @@ attn_fwd_kernel(const AttnArgs p) {
   for (int t = 0; t < AD / 32; ++t)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+  // Online softmax state per row, in log2 units: O and l are relative to
+  // 2^m_ref; m_ref follows the running max lazily (moved only when a row's
+  // max passes it by more than 8, so exp2 arguments stay <= 8 and most
+  // blocks skip the rescale of O).
+  float m_ref = -INFINITY, l_run = 0.f;
   const uint16_t* Mrow =
       MASK ? static_cast<const uint16_t*>(p.mask) + b * p.smb + qrow * p.ldm : nullptr;
 
-  if (kb0 < kb1) {
-    issue(kb0, 0);
-    if (kb0 + 1 < kb1) {
-      issue(kb0 + 1, 1);
-      wait_vmcnt<(KLINES + 3) / 4 + VLINES / 4>();
+  // Group g takes key blocks base + 2 it + g, it = 0 .. nit-1 (those in
+  // [kb0, kb1)); base is kb0 rounded down to even, so which group a block
+  // goes to does not depend on kb0.
+  const int base = kb0 & ~1;
+  const int nit = kb1 > base ? (kb1 - base + 1) / 2 : 0;
+  auto blk_of = [&](int it) { return base + 2 * it + grp; };
+  auto valid = [&](int kb) { return kb >= kb0 && kb < kb1; };
+  auto cls_of = [&](int kb) -> uint8_t {  // (all mixed without the pre-pass)
+    return !valid(kb) ? MB_NEGINF : MASK ? (mcls != nullptr ? mcls[kb] : MB_MIXED) : MB_ZERO;
+  };
+
+  {
+    const bool v0 = nit > 0 && valid(blk_of(0)), v1 = nit > 1 && valid(blk_of(1));
+    if (v0) issue(blk_of(0), 0);
+    if (v1) issue(blk_of(1), 1);
+    // block 0 landed: wave wq issued KLW (wq == 0) or KLW - 1 K lines and
+    // VLW V lines per block
+    if (v0 && v1) {
+      if (wq == 0)
+        wait_vmcnt<KLW + VLW>();
+      else
+        wait_vmcnt<KLW - 1 + VLW>();
     } else {
       wait_vmcnt<0>();
     }
   }
   __syncthreads();
-  for (int kb = kb0; kb < kb1; ++kb) {
-    const int st = (kb - kb0) & 1;
-    const char* sK = lds + st * STAGE;
+  for (int it = 0; it < nit; ++it) {
+    const int kb = blk_of(it), slot = it & 1;
+    const char* sK = lds + (grp * 2 + slot) * STAGE;
     const char* sV = sK + KBLK;
-    // mask class of this block (all mixed without the pre-pass)
-    const uint8_t cls = MASK ? (mcls != nullptr ? mcls[kb] : MB_MIXED) : MB_ZERO;
+    const uint8_t cls = cls_of(kb);
     if (cls != MB_NEGINF) {
     // S^T for this block: two 32-key tiles.
     f32x16 s[2];
@@ -304,20 +400,23 @@ attn_fwd_kernel(const AttnArgs p) {
         s[t] = mfma<T>(kf, qf[kk], s[t]);
       }
     }
-    // Scores in log2 units; keys past sk (and past the position) dropped.
-    const int64_t k0 = static_cast<int64_t>(kb) * AK;
+    // Raw scores (the scale joins in the exponent); keys past sk and past a
+    // row's position dropped, checked only in blocks that reach them.
+    const int k0 = kb * AK;
+    if (k0 + AK > sk32 || (CAUSAL && k0 + AK - 1 > qpos_min)) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int rg = 0; rg < 4; ++rg)
+        for (int rg = 0; rg < 4; ++rg)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int64_t key = k0 + t * 32 + 8 * rg + 4 * h + i;
-          bool keep = key < p.sk;
-          if constexpr (CAUSAL) keep = keep && key <= qpos;
-          s[t][4 * rg + i] = keep ? s[t][4 * rg + i] * p.scale_log2 : -INFINITY;
-        }
-    // Mixed mask blocks: add the mask (log2 units).  Lane's keys for (t, rg):
+          for (int i = 0; i < 4; ++i) {
+            const int key = k0 + t * 32 + 8 * rg + 4 * h + i;
+            bool keep = key < sk32;
+            if constexpr (CAUSAL) keep = keep && key <= qpos;
+            s[t][4 * rg + i] = keep ? s[t][4 * rg + i] : -INFINITY;
+          }
+    }
+    // Mixed mask blocks: add mask / scale.  Lane's keys for (t, rg):
     // k0 + 32 t + 8 rg + 4 h .. + 3, one 8-byte load each.
     if (MASK && cls == MB_MIXED) {
       const uint16_t* mp = Mrow + k0 + 4 * h;
@@ -330,7 +429,7 @@ attn_fwd_kernel(const AttnArgs p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const uint16_t bits = static_cast<uint16_t>(mv[i >> 1] >> (16 * (i & 1)));
-              s[t][4 * rg + i] = fmaf(Num<T>::to_f(__builtin_bit_cast(T, bits)), 1.4426950408889634f,
+              s[t][4 * rg + i] = fmaf(Num<T>::to_f(__builtin_bit_cast(T, bits)), p.inv_scale,
                                       s[t][4 * rg + i]);
             }
           }
@@ -341,9 +440,9 @@ attn_fwd_kernel(const AttnArgs p) {
           for (int rg = 0; rg < 4; ++rg)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              if (k0 + 32 * t + 8 * rg + 4 * h + i < p.sk)
+              if (k0 + 32 * t + 8 * rg + 4 * h + i < sk32)
                 s[t][4 * rg + i] = fmaf(Num<T>::to_f(reinterpret_cast<const T*>(mp)[32 * t + 8 * rg + i]),
-                                        1.4426950408889634f, s[t][4 * rg + i]);
+                                        p.inv_scale, s[t][4 * rg + i]);
       }
     }
     float mb = -INFINITY;
@@ -352,25 +451,31 @@ attn_fwd_kernel(const AttnArgs p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) mb = fmaxf(mb, s[t][r]);
     mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
-    const float m_new = fmaxf(m_run, mb);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    const float c = p.scale_log2;
+    const float mbc = mb * c;  // block max, log2 units (-inf: nothing visible)
+    const bool grow = mbc > m_ref + 8.f;
+    if (__ballot(grow) != 0) {  // wave-uniform: some row moves its reference
+      const float m_new = grow ? mbc : m_ref;
+      const float alpha = grow ? __builtin_amdgcn_exp2f(m_ref - m_new) : 1.f;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < AD / 32; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+      m_ref = m_new;
+    }
+    const float neg = m_ref == -INFINITY ? 0.f : -m_ref;
     float lb = 0.f;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float pr = __builtin_amdgcn_exp2f(s[t][r] - m_use);
+        const float pr = __builtin_amdgcn_exp2f(fmaf(s[t][r], c, neg));
         s[t][r] = pr;
         lb += pr;
       }
     lb += __shfl_xor(lb, 32, 64);
-    l_run = l_run * alpha + lb;
-    m_run = m_new;
-#pragma unroll
-    for (int dt = 0; dt < AD / 32; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    l_run += lb;
     // O^T += V^T P^T over the block's 4 sixteen-key steps.
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -391,10 +496,35 @@ attn_fwd_kernel(const AttnArgs p) {
       }
     }
     }  // cls != MB_NEGINF
-    // Block kb+1 landed (own DMA) and every wave is done with stage st.
+    // The group's next block landed (own DMA) and every wave is done with
+    // this slot.
     wait_vmcnt<0>();
     __syncthreads();
-    if (kb + 2 < kb1) issue(kb + 2, st);
+    if (it + 2 < nit && valid(blk_of(it + 2))) issue(blk_of(it + 2), slot);
+  }
+  // Merge: group 1 hands (m_ref, l, O) to the group-0 lane of the same row
+  // through LDS (all DMA has landed: the loop ends with a wait + barrier).
+  float* mg = reinterpret_cast<float*>(lds) + wq * (66 * 64) + lane;
+  if (grp == 1) {
+    mg[0] = m_ref;
+    mg[64] = l_run;
+#pragma unroll
+    for (int dt = 0; dt < AD / 32; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mg[(2 + dt * 16 + r) * 64] = o[dt][r];
+  }
+  __syncthreads();
+  if (grp == 1) return;
+  {
+    const float m1 = mg[0], l1 = mg[64];
+    const float m = fmaxf(m_ref, m1);
+    const float a0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_ref - m);
+    const float a1 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
+    l_run = l_run * a0 + l1 * a1;
+#pragma unroll
+    for (int dt = 0; dt < AD / 32; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * a0 + mg[(2 + dt * 16 + r) * 64] * a1;
   }
   // O[qrow][d], d = 32 dt + 8 rg + 4 h + i, normalised by the row sum.
   const float inv = 1.0f / l_run;
@@ -424,7 +554,9 @@ int64_t mask_batches(int64_t batch, int64_t stride_m) { return (batch == 1 || st
 extern "C" int64_t sph_attention_workspace_bytes(int64_t batch, int64_t mq, int64_t sk,
                                                  int64_t stride_m) {
   if (batch <= 0 || mq <= 0 || sk <= 0) return 0;
-  return mask_batches(batch, stride_m) * ((mq + AQ - 1) / AQ) * ((sk + AK - 1) / AK);
+  // mask block classes, then (256-byte aligned) the job order
+  const int64_t cls = mask_batches(batch, stride_m) * ((mq + AQ - 1) / AQ) * ((sk + AK - 1) / AK);
+  return (cls + 255) / 256 * 256 + 4 * batch * ((mq + AQ - 1) / AQ);
 }
 
 extern "C" int sph_attention_fwd(sph_dtype dtype, int64_t batch, int64_t mq, int64_t sk,
@@ -443,6 +575,11 @@ extern "C" int sph_attention_fwd(sph_dtype dtype, int64_t batch, int64_t mq, int
   SPH_REQUIRE(mq % AQ == 0, SPH_ERR_UNSUPPORTED, "attention: query rows must be a multiple of 128");
   SPH_REQUIRE(batch * (mq / AQ) < (1LL << 31), SPH_ERR_TOO_LARGE, "attention: grid too large");
   SPH_REQUIRE(causal_q >= 0, SPH_ERR_INVALID_ARG, "attention: causal_q < 0");
+  SPH_REQUIRE(scale > 0.f && scale < INFINITY, SPH_ERR_INVALID_ARG,
+              "attention: scale must be positive and finite");
+  SPH_REQUIRE(sk < (1LL << 30) && causal_q < (1LL << 30) && causal_off > -(1LL << 30) &&
+                  causal_off < (1LL << 30),
+              SPH_ERR_TOO_LARGE, "attention: positions must fit 30 bits");
   SPH_REQUIRE(ldq >= AD && ldk >= AD && ldv >= AD && ldo >= AD, SPH_ERR_INVALID_ARG,
               "attention: leading dimension below head_dim");
   SPH_REQUIRE(al16(q) && al16(k) && al16(v) && al16(o) && ldq % 8 == 0 && ldk % 8 == 0 &&
@@ -475,8 +612,10 @@ extern "C" int sph_attention_fwd(sph_dtype dtype, int64_t batch, int64_t mq, int
   p.causal_off = causal_off;
   p.batch = batch;
   p.nbq = mq / AQ;
+  p.heads = (causal_q > 0 && causal_q % AQ == 0 && mq % causal_q == 0) ? mq / causal_q : 0;
   p.nkb = (sk + AK - 1) / AK;
   p.scale_log2 = scale * 1.4426950408889634f;
+  p.inv_scale = 1.0f / scale;
   p.o = o;
   p.ldo = ldo;
   p.so = stride_o;
@@ -499,15 +638,25 @@ extern "C" int sph_attention_fwd(sph_dtype dtype, int64_t batch, int64_t mq, int
                                                     mbat == 1 ? 0 : stride_m, sk, p.nbq, p.nkb, cls);
     p.mblk = cls;
     p.mblk_b = mbat == 1 ? 0 : p.nbq;
+    // Longest-first job order from the classes (masks without causal
+    // positions, small enough for one sorting workgroup).
+    const int64_t jobs = batch * p.nbq;
+    const int64_t cls_bytes = mbat * p.nbq * p.nkb;
+    if (causal_q == 0 && p.nkb < kMaxOrderBins && cls_bytes <= kMaxOrderBytes) {
+      int32_t* ord = reinterpret_cast<int32_t*>(cls + (cls_bytes + 255) / 256 * 256);
+      attn_order_kernel<<<1, 1024, 0, st>>>(cls, p.mblk_b, static_cast<int>(p.nkb),
+                                            static_cast<int>(p.nbq), static_cast<int>(jobs), ord);
+      p.order = ord;
+    }
   }
   dim3 grid(static_cast<unsigned>(batch * (mq / AQ)));
   const bool m = mask != nullptr, c = causal_q > 0;
 #define SPH_ATTN(T_)                                                                     \
   do {                                                                                   \
-    if (m && c) attn_fwd_kernel<T_, true, true><<<grid, 256, 0, st>>>(p);                \
-    else if (m) attn_fwd_kernel<T_, true, false><<<grid, 256, 0, st>>>(p);               \
-    else if (c) attn_fwd_kernel<T_, false, true><<<grid, 256, 0, st>>>(p);               \
-    else attn_fwd_kernel<T_, false, false><<<grid, 256, 0, st>>>(p);                     \
+    if (m && c) attn_fwd_kernel<T_, true, true><<<grid, 512, 0, st>>>(p);                \
+    else if (m) attn_fwd_kernel<T_, true, false><<<grid, 512, 0, st>>>(p);               \
+    else if (c) attn_fwd_kernel<T_, false, true><<<grid, 512, 0, st>>>(p);               \
+    else attn_fwd_kernel<T_, false, false><<<grid, 512, 0, st>>>(p);                     \
   } while (0)
   if (dtype == SPH_F16)
     SPH_ATTN(half_t);
