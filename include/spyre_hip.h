@@ -207,9 +207,10 @@ int sph_gemm_strided_batched(sph_dtype dtype, int trans_a, int trans_b,
  * Replaces: spyre__mm_default (spyre_torch_ops.cpp:214-293) for x W^T
  * followed by the generated silu and mul ops (Metadata.yaml base ops,
  * base.jinja2:16-241); no single reference function corresponds (the
- * reference does not fuse).  Needs m % 256 == 0, n % 128 == 0,
- * k % 64 == 0 and 16-byte aligned rows; other shapes return
- * SPH_ERR_UNSUPPORTED (compute the three steps instead). */
+ * reference does not fuse).  Takes m <= 8 (decode: 64 <= k <= 8192,
+ * k % 8 == 0) or m % 256 == 0 with n % 128 == 0 and k % 64 == 0, and
+ * 16-byte aligned rows; other shapes return SPH_ERR_UNSUPPORTED (compute
+ * the three steps instead). */
 int sph_gemm_swiglu(sph_dtype dtype, int64_t m, int64_t n, int64_t k, const void* a,
                     int64_t lda, const void* w, int64_t ldw, void* d, int64_t ldd,
                     sph_stream_t stream);

@@ -18,9 +18,9 @@ to the fp16 bmm output without another rounding; where the compiled program
 runs attention as one fused kernel - prefill, head dim 128, the stacked
 query rows of a KV head a multiple of 128 - the scores are not rounded at
 all, only the probabilities before the second product; where it runs the
-gate / up projection and silu(gate) * up as one GEMM - prefill, rows
-% 256 == 0, intermediate % 128 == 0, hidden % 64 == 0 - gate and up are not
-rounded either).
+gate / up projection and silu(gate) * up as one kernel - rows % 256 == 0,
+intermediate % 128 == 0, hidden % 64 == 0, or at most 8 rows with
+64 <= hidden <= 8192 - gate and up are not rounded either).
 
 Pinned by tests/test_decoder.py against torch's CPU float32 ops with
 F.scaled_dot_product_attention (is_causal, enable_gqa) as an independent
@@ -118,9 +118,11 @@ def layer(h, w, cfg, positions, act=np.float16, kv_prefix=None, fused=False):
     a = attention(q, k, v, np.asarray(positions), k_pos, act, fused, scores_fp32=fused_attn)
     h = _r(h + _linear(a, w["wo"], act), act)
     x = _rmsnorm(h, w["mlp_norm"], cfg.eps, act)
-    # the compiled prefill's fused SwiGLU GEMM keeps gate / up in fp32
-    fused_mlp = (fused and kv_prefix is None and (B * S) % 256 == 0 and
-                 cfg.intermediate % 128 == 0 and cfg.hidden % 64 == 0)
+    # the compiled program's fused SwiGLU kernels keep gate / up in fp32
+    # (tiled GEMM for whole 256-row blocks, weight stream for <= 8 rows)
+    fused_mlp = fused and (((B * S) % 256 == 0 and cfg.intermediate % 128 == 0 and
+                            cfg.hidden % 64 == 0) or
+                           (B * S <= 8 and cfg.hidden % 8 == 0 and 64 <= cfg.hidden <= 8192))
     lin_act = None if fused_mlp else act
     gte = _linear(x, w["wg"], lin_act)
     up = _linear(x, w["wu"], lin_act)

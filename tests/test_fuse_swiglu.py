@@ -47,11 +47,12 @@ def _swiglu(x, w, order="gu"):
     return F.silu(g) * u if order == "gu" else u * F.silu(g)
 
 
-@pytest.mark.parametrize("variant", ["2d", "3d", "swapped", "bf16"])
+@pytest.mark.parametrize("variant", ["2d", "3d", "swapped", "bf16", "decode"])
 def test_swiglu_is_fused_and_unchanged(variant):
     dtype = torch.bfloat16 if variant == "bf16" else torch.float16
     lead = (1,) if variant == "3d" else ()
-    x, w = _inputs(256, 128, 64, dtype, lead)
+    m, n = (4, 200) if variant == "decode" else (256, 128)  # decode: weight-stream shape
+    x, w = _inputs(m, n, 64, dtype, lead)
     order = "ug" if variant == "swapped" else "gu"
     out, n = _run(lambda x, w: _swiglu(x, w, order), x, w)
     assert n == 1
@@ -62,7 +63,7 @@ def test_swiglu_is_fused_and_unchanged(variant):
 def test_unfit_swiglu_stays_unfused(case):
     m, n, k, dtype = 256, 128, 64, torch.float16
     if case == "rows":
-        m = 200
+        m = 200  # neither whole 256-row tiles nor a decode shape
     elif case == "cols":
         n = 96
     elif case == "k":

@@ -442,11 +442,13 @@ def test_gemm_stream_epilogue():
 
 
 @pytest.mark.parametrize("m,n,k,pad", [(256, 128, 64, 0), (512, 384, 256, 8), (1024, 1280, 4096, 0),
-                                       (768, 256, 1024, 16)])
+                                       (768, 256, 1024, 16), (4, 12800, 4096, 0), (1, 300, 64, 8),
+                                       (8, 1000, 2056, 0), (5, 4100, 8192, 16)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_gemm_swiglu(m, n, k, pad, dtype):
     # silu(x Wg^T) * (x Wu^T) from one [2n, k] weight (gate rows first),
-    # padded leading dims on every operand
+    # padded leading dims on every operand; whole 256-row tiles (direct-load
+    # GEMM) and decode rows (m <= 8, weight-stream kernel)
     _log(f"gemm swiglu {m}x{n}x{k} pad={pad} {dtype}")
     X = uniform((m, k), k=31, dtype=dtype)
     W = (uniform((2 * n, k), k=32) * 0.05).to(dtype)

@@ -203,7 +203,8 @@ at::Tensor gemm_swiglu(const at::Tensor& x_in, const at::Tensor& w_in) {
   at::Tensor x = x_in.stride(1) == 1 ? x_in : contiguous_on_device(x_in);
   at::Tensor w = w_in.stride(1) == 1 ? w_in : contiguous_on_device(w_in);
   c10::DeviceGuard guard(out.device());
-  const bool fits = m % 256 == 0 && n % 128 == 0 && k % 64 == 0 && k > 0 &&
+  const bool fits = ((m % 256 == 0 && n % 128 == 0 && k % 64 == 0) ||
+                     (m <= 8 && k >= 64 && k % 8 == 0 && k <= 8192)) && k > 0 &&
                     x.stride(0) % 8 == 0 && w.stride(0) % 8 == 0 &&
                     reinterpret_cast<uintptr_t>(x.data_ptr()) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(w.data_ptr()) % 16 == 0;

@@ -1199,9 +1199,14 @@ namespace gv {
 constexpr int WAVES = 16, THREADS = WAVES * 64, SEG = 8;
 }
 
-template <typename T, int MT, int KMAX>
+// SWIGLU: W holds the gate rows [0, n) and the up rows [n, 2n); output j
+// is silu(x W[j]) * (x W[n + j]).  A wave's item then loads SEG / 2 chunks
+// of both rows (the same register footprint) and the end of the row
+// combines the two sums.
+template <typename T, int MT, int KMAX, bool SWIGLU = false>
 __global__ void __launch_bounds__(gv::THREADS) gemm_stream_kernel(const GemmArgs p) {
   using namespace gv;
+  constexpr int NR = SWIGLU ? 2 : 1, SEGK = SEG / NR;  // rows per item, chunks per row
   __shared__ __attribute__((aligned(16))) uint16_t As[MT * KMAX];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nc = static_cast<int>(p.k / 8);           // 16-byte chunks per row
@@ -1210,33 +1215,40 @@ __global__ void __launch_bounds__(gv::THREADS) gemm_stream_kernel(const GemmArgs
   const uint16_t* B = static_cast<const uint16_t*>(p.b);
   T* D = static_cast<T*>(p.d);
   const int cpl = (nc + 63) / 64;                      // chunks per lane
-  const int nseg = (cpl + SEG - 1) / SEG;              // segments per row
+  const int nseg = (cpl + SEGK - 1) / SEGK;            // segments per row
   const int64_t stride = static_cast<int64_t>(gridDim.x) * WAVES;
   int64_t n = static_cast<int64_t>(blockIdx.x) * WAVES + wave;
   u32x4 wa[SEG], wb[SEG];
-  float acc[MT];
+  float acc[NR][MT];
 #pragma unroll
-  for (int m = 0; m < MT; ++m) acc[m] = 0.f;
+  for (int r = 0; r < NR; ++r)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
 
-// Weight chunks of (ROW_, SEG_) into register buffer W_ (chunks past the row
-// read a valid chunk that is not summed).
+// Weight chunks of (ROW_, SEG_) into register buffer W_ (row r of the item
+// in entries r * SEGK ..; chunks past the row read a valid chunk that is
+// not summed).
 #define SPH_GV_LOAD(W_, ROW_, SEG_)                                                         \
   do {                                                                                      \
-    const uint16_t* rp_ = B + (ROW_) * p.ldb;                                               \
-    _Pragma("unroll") for (int j_ = 0; j_ < SEG; ++j_) {                                    \
-      int c_ = ((SEG_) * SEG + j_) * 64 + lane;                                             \
-      c_ = c_ < nc ? c_ : nc - 1;                                                           \
-      W_[j_] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rp_ + c_ * 8));    \
+    _Pragma("unroll") for (int r_ = 0; r_ < NR; ++r_) {                                     \
+      const uint16_t* rp_ = B + ((ROW_) + r_ * p.n) * p.ldb;                                \
+      _Pragma("unroll") for (int j_ = 0; j_ < SEGK; ++j_) {                                 \
+        int c_ = ((SEG_) * SEGK + j_) * 64 + lane;                                          \
+        c_ = c_ < nc ? c_ : nc - 1;                                                         \
+        W_[r_ * SEGK + j_] =                                                                \
+            __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rp_ + c_ * 8));       \
+      }                                                                                     \
     }                                                                                       \
   } while (0)
 #define SPH_GV_COMPUTE(W_, SEG_)                                                            \
   do {                                                                                      \
-    _Pragma("unroll") for (int j_ = 0; j_ < SEG; ++j_) {                                    \
-      const int c_ = ((SEG_) * SEG + j_) * 64 + lane;                                       \
+    _Pragma("unroll") for (int j_ = 0; j_ < SEGK; ++j_) {                                   \
+      const int c_ = ((SEG_) * SEGK + j_) * 64 + lane;                                      \
       if (c_ < nc) {                                                                        \
         _Pragma("unroll") for (int m_ = 0; m_ < MT; ++m_) {                                 \
           const u32x4 a_ = *reinterpret_cast<const u32x4*>(As + (m_ * nc + c_) * 8);        \
-          acc[m_] = dot8_acc<T>(a_, W_[j_], acc[m_]);                                       \
+          _Pragma("unroll") for (int r_ = 0; r_ < NR; ++r_)                                 \
+              acc[r_][m_] = dot8_acc<T>(a_, W_[r_ * SEGK + j_], acc[r_][m_]);               \
         }                                                                                   \
       }                                                                                     \
     }                                                                                       \
@@ -1244,14 +1256,21 @@ __global__ void __launch_bounds__(gv::THREADS) gemm_stream_kernel(const GemmArgs
 // End of row ROW_: butterflies, lane m < M writes output (m, ROW_).
 #define SPH_GV_FINISH(ROW_)                                                                 \
   do {                                                                                      \
+    _Pragma("unroll") for (int r_ = 0; r_ < NR; ++r_)                                       \
+      _Pragma("unroll") for (int m_ = 0; m_ < MT; ++m_)                                     \
+        _Pragma("unroll") for (int o_ = 32; o_ > 0; o_ >>= 1)                               \
+            acc[r_][m_] += __shfl_xor(acc[r_][m_], o_, 64);                                 \
+    float v_ = 0.f;                                                                         \
     _Pragma("unroll") for (int m_ = 0; m_ < MT; ++m_) {                                     \
-      _Pragma("unroll") for (int o_ = 32; o_ > 0; o_ >>= 1) acc[m_] += __shfl_xor(acc[m_], o_, 64); \
+      const float g_ = acc[0][m_];                                                          \
+      const float x_ = SWIGLU ? silu(g_) * acc[NR - 1][m_] : g_;                            \
+      v_ = lane == m_ ? x_ : v_;                                                            \
     }                                                                                       \
-    float v_ = acc[0];                                                                      \
-    _Pragma("unroll") for (int m_ = 1; m_ < MT; ++m_) v_ = lane == m_ ? acc[m_] : v_;       \
     if (lane < MT && lane < mrows)                                                          \
-      D[lane * p.ldd + (ROW_)] = Num<T>::from_f(skinny_epilogue<T>(p, v_, 0, lane, (ROW_))); \
-    _Pragma("unroll") for (int m_ = 0; m_ < MT; ++m_) acc[m_] = 0.f;                        \
+      D[lane * p.ldd + (ROW_)] = Num<T>::from_f(                                            \
+          SWIGLU ? v_ : skinny_epilogue<T>(p, v_, 0, lane, (ROW_)));                        \
+    _Pragma("unroll") for (int r_ = 0; r_ < NR; ++r_)                                       \
+      _Pragma("unroll") for (int m_ = 0; m_ < MT; ++m_) acc[r_][m_] = 0.f;                  \
   } while (0)
 
   // The first weight loads go out before the activations are staged, so
@@ -1521,12 +1540,47 @@ extern "C" int sph_gemm_swiglu(sph_dtype dtype, int64_t m, int64_t n, int64_t k,
   SPH_REQUIRE(dtype == SPH_F16 || dtype == SPH_BF16, SPH_ERR_UNSUPPORTED,
               "gemm_swiglu: dtype must be F16 or BF16");
   if (m == 0 || n == 0) return SPH_OK;
-  SPH_REQUIRE(m % dl::BM == 0 && n % 128 == 0 && k > 0 && k % dl::BKD == 0, SPH_ERR_UNSUPPORTED,
-              "gemm_swiglu: needs m % 256 == 0, n % 128 == 0, k % 64 == 0");
   SPH_REQUIRE(lda >= k && ldw >= k && ldd >= n, SPH_ERR_INVALID_ARG,
               "gemm_swiglu: leading dimension too small");
-  SPH_REQUIRE(al16(a) && al16(w) && al16(d) && lda % 8 == 0 && ldw % 8 == 0 && ldd % 8 == 0,
-              SPH_ERR_UNSUPPORTED, "gemm_swiglu: rows must be 16-byte aligned");
+  SPH_REQUIRE(al16(a) && al16(w) && lda % 8 == 0 && ldw % 8 == 0, SPH_ERR_UNSUPPORTED,
+              "gemm_swiglu: rows of x and w must be 16-byte aligned");
+  if (m <= 8) {
+    // decode shapes: the weight-stream kernel, gate and up rows per wave
+    SPH_REQUIRE(k >= 64 && k % 8 == 0 && k <= 8192 && n < (1LL << 40), SPH_ERR_UNSUPPORTED,
+                "gemm_swiglu: small m needs 64 <= k <= 8192, k % 8 == 0");
+    GemmArgs q{};
+    q.m = m;
+    q.n = n;
+    q.k = k;
+    q.a = a;
+    q.lda = lda;
+    q.b = w;
+    q.ldb = ldw;
+    q.d = d;
+    q.ldd = ldd;
+    q.alpha = 1.f;
+    constexpr int64_t kCUs = 256;
+    const int64_t wgs = ceil_div(n, gv::WAVES);
+    const unsigned grid = static_cast<unsigned>(wgs < kCUs ? wgs : kCUs);
+    hipStream_t st = as_stream(stream);
+#define SPH_SW_STREAM(T_)                                                                       \
+  do {                                                                                          \
+    if (m <= 4)                                                                                 \
+      gemm_stream_kernel<T_, 4, 8192, true><<<grid, dim3(gv::THREADS), 0, st>>>(q);             \
+    else                                                                                        \
+      gemm_stream_kernel<T_, 8, 8192, true><<<grid, dim3(gv::THREADS), 0, st>>>(q);             \
+  } while (0)
+    if (dtype == SPH_F16)
+      SPH_SW_STREAM(half_t);
+    else
+      SPH_SW_STREAM(bf16_t);
+#undef SPH_SW_STREAM
+    return check_launch("sph_gemm_swiglu (stream)");
+  }
+  SPH_REQUIRE(m % dl::BM == 0 && n % 128 == 0 && k > 0 && k % dl::BKD == 0, SPH_ERR_UNSUPPORTED,
+              "gemm_swiglu: needs m <= 8, or m % 256 == 0, n % 128 == 0, k % 64 == 0");
+  SPH_REQUIRE(al16(d) && ldd % 8 == 0, SPH_ERR_UNSUPPORTED,
+              "gemm_swiglu: rows of d must be 16-byte aligned");
   constexpr int64_t kLim = 1LL << 31;
   SPH_REQUIRE(((dl::BM - 1) * lda + k) * 2 < kLim && ((n + 127) * ldw + k) * 2 < kLim &&
                   (m / dl::BM) * (n / 128) < kLim,

@@ -12,10 +12,11 @@ Here, on spyre graphs, the chain
     s  = convert(mul(g, sigmoid(g)), f16)   # silu, as Inductor decomposes it
     y  = mul(s, slice(v, -1, n, 2n))        # either operand order
 
-is replaced by swiglu_mm(x, w) (reshaped like y) when the fused GEMM takes
-the shape (fp16 / bf16, M % 256 == 0, n % 128 == 0, K % 64 == 0) and no
-intermediate is used elsewhere: the [M, 2n] projection is then never
-written to HBM.
+is replaced by swiglu_mm(x, w) (reshaped like y) when a fused kernel takes
+the shape (fp16 / bf16; M % 256 == 0, n % 128 == 0, K % 64 == 0 for the
+tiled GEMM of prefill, or M <= 8 with K % 8 == 0 and 64 <= K <= 8192 for
+the weight-stream kernel of decode) and no intermediate is used elsewhere:
+the [M, 2n] projection is then never written to HBM.
 """
 
 from __future__ import annotations
@@ -29,7 +30,8 @@ from .fuse_attention import _is, _only_users, _val
 aten = torch.ops.aten
 prims = torch.ops.prims
 
-ROW_BLOCK, COL_BLOCK, K_BLOCK = 256, 128, 64
+ROW_BLOCK, COL_BLOCK, K_BLOCK = 256, 128, 64  # tiled GEMM (prefill)
+STREAM_ROWS, STREAM_K = 8, 8192               # weight-stream kernel (decode)
 _BIG = 2 ** 62
 
 
@@ -102,7 +104,9 @@ def _match(y: torch.fx.Node) -> Optional[tuple]:
         M, K = xv.shape
         if not all(isinstance(t, int) for t in (M, K)) or tuple(wv.shape) != (2 * n, K):
             continue
-        if M % ROW_BLOCK or n % COL_BLOCK or K % K_BLOCK:
+        tiles = M % ROW_BLOCK == 0 and n % COL_BLOCK == 0 and K % K_BLOCK == 0
+        stream = M <= STREAM_ROWS and K % 8 == 0 and 64 <= K <= STREAM_K
+        if not (tiles or stream):
             continue
         return x, w, chain
     return None
