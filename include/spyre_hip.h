@@ -210,10 +210,30 @@ int sph_gemm_strided_batched(sph_dtype dtype, int trans_a, int trans_b,
  * reference does not fuse).  Takes m <= 8 (decode: 64 <= k <= 8192,
  * k % 8 == 0) or m % 256 == 0 with n % 128 == 0 and k % 64 == 0, and
  * 16-byte aligned rows; other shapes return SPH_ERR_UNSUPPORTED (compute
- * the three steps instead). */
+ * the three steps instead).  workspace (may be NULL) of
+ * sph_gemm_swiglu_workspace_bytes(m, n, k) bytes lets a tiled call split
+ * its last, partial round of tiles along K. */
 int sph_gemm_swiglu(sph_dtype dtype, int64_t m, int64_t n, int64_t k, const void* a,
                     int64_t lda, const void* w, int64_t ldw, void* d, int64_t ldd,
-                    sph_stream_t stream);
+                    void* workspace, int64_t workspace_bytes, sph_stream_t stream);
+int64_t sph_gemm_swiglu_workspace_bytes(int64_t m, int64_t n, int64_t k);
+
+/* sph_gemm_strided_batched with a workspace (device memory, may be NULL):
+ * with at least sph_gemm_workspace_bytes(batch, m, n, k) bytes, a product
+ * on whole 256 x 256 tiles whose tile count leaves a partial last round on
+ * the 256 CUs splits that round's tiles along K into fp32 partial tiles
+ * (summed and finished with the epilogue by a second kernel) instead of
+ * running it on a few CUs.  Same results up to fp32 summation order.  No
+ * counterpart in the reference (its GEMM is one device call,
+ * spyre_torch_ops.cpp:214-293); calls sharing a workspace must be ordered
+ * on a stream. */
+int sph_gemm_ex(sph_dtype dtype, int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n,
+                int64_t k, float alpha, const void* a, int64_t lda, int64_t stride_a,
+                const void* b, int64_t ldb, int64_t stride_b, float beta, const void* c,
+                int64_t ldc_row, int64_t ldc_col, int64_t stride_c, void* d, int64_t ldd,
+                int64_t stride_d, int epilogue, void* workspace, int64_t workspace_bytes,
+                sph_stream_t stream);
+int64_t sph_gemm_workspace_bytes(int64_t batch, int64_t m, int64_t n, int64_t k);
 
 /* fp16 shorthands: contiguous row-major, no transpose, no C. */
 int sph_gemm_f16(int64_t m, int64_t n, int64_t k, const void* a,

@@ -442,7 +442,8 @@ def test_gemm_stream_epilogue():
 
 
 @pytest.mark.parametrize("m,n,k,pad", [(256, 128, 64, 0), (512, 384, 256, 8), (1024, 1280, 4096, 0),
-                                       (768, 256, 1024, 16), (4, 12800, 4096, 0), (1, 300, 64, 8),
+                                       (768, 256, 1024, 16), (256, 1280, 2048, 8),
+                                       (4, 12800, 4096, 0), (1, 300, 64, 8),
                                        (8, 1000, 2056, 0), (5, 4100, 8192, 16)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_gemm_swiglu(m, n, k, pad, dtype):
@@ -457,8 +458,10 @@ def test_gemm_swiglu(m, n, k, pad, dtype):
     wd = torch.zeros(2 * n, k + pad, dtype=dtype, device=DEV)
     wd[:, :k] = W.to(DEV)
     d = torch.full((m, n + pad), 7.0, dtype=dtype, device=DEV)
+    nws = _capi.lib().sph_gemm_swiglu_workspace_bytes(m, n, k)
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=DEV)
     _capi.call("sph_gemm_swiglu", DT[dtype], m, n, k, _p(xd), k + pad, _p(wd), k + pad, _p(d),
-               n + pad, _stream())
+               n + pad, _p(ws), nws, _stream())
     _sync()
     xf, wf = X.float().numpy(), W.float().numpy()
     want = O.silu(O.gemm(xf, wf[:n].T)) * O.gemm(xf, wf[n:].T)
@@ -468,12 +471,41 @@ def test_gemm_swiglu(m, n, k, pad, dtype):
         assert bool((d[:, n:] == 7.0).all()), "padding columns written"
 
 
+@pytest.mark.parametrize("m,n,k,tb,epi", [(2048, 4096, 4096, True, 0), (768, 512, 2048, False, 2),
+                                           (512, 1024, 12800, True, 0), (256, 256, 2048, True, 3)])
+def test_gemm_splitk_tail(m, n, k, tb, epi):
+    # sph_gemm_ex with a workspace: the partial last round of 256 x 256
+    # tiles runs as K slices plus a reduce (alpha, beta*C with a bias row,
+    # activation applied there); against the oracle and the unsplit call
+    _log(f"gemm split-K tail {m}x{n}x{k} tb={tb} epi={epi}")
+    lib = _capi.lib()
+    nws = lib.sph_gemm_workspace_bytes(1, m, n, k)
+    assert nws > 0, "shape should take a split"
+    X = uniform((m, k), k=61)
+    W = uniform((n, k) if tb else (k, n), k=62) * 0.05
+    bias = uniform((n,), k=63)
+    xd, wd, bd = X.to(DEV), W.to(DEV), bias.to(DEV)
+    ws = torch.empty(nws, dtype=torch.uint8, device=DEV)
+    outs = []
+    for w_ptr, w_n in ((_p(ws), nws), (None, 0)):
+        d = torch.empty(m, n, dtype=torch.float16, device=DEV)
+        _capi.call("sph_gemm_ex", _capi.F16, 0, int(tb), 1, m, n, k, 0.75, _p(xd), k, 0, _p(wd),
+                   k if tb else n, 0, 0.5, _p(bd), 0, 1, 0, _p(d), n, 0, epi, w_ptr, w_n, _stream())
+        _sync()
+        outs.append(d)
+    b_ = W.numpy().T if tb else W.numpy()
+    want = O.gemm(X.numpy(), b_, alpha=0.75, beta=0.5, c=bias.numpy()[None, :],
+                  epilogue={0: "none", 2: "gelu", 3: "silu"}[epi])
+    assert_close_fp(outs[0], want, what="split-K tail")
+    torch.testing.assert_close(outs[0].float(), outs[1].float(), rtol=2e-3, atol=2e-3)
+
+
 def test_gemm_swiglu_rejects_unfit_shapes():
     x = torch.zeros(200, 64, dtype=torch.float16, device=DEV)
     w = torch.zeros(256, 64, dtype=torch.float16, device=DEV)
     d = torch.zeros(200, 128, dtype=torch.float16, device=DEV)
     rc = _capi.lib().sph_gemm_swiglu(_capi.F16, 200, 128, 64, _p(x), 64, _p(w), 64, _p(d), 128,
-                                     _stream())
+                                     None, 0, _stream())
     assert rc == 1002  # SPH_ERR_UNSUPPORTED: m % 256 != 0
 
 

@@ -90,10 +90,14 @@ void gemm2d(const at::Tensor& a, const at::Tensor& b, const at::Tensor& d, float
     check_extent(ce, cp, 2, cs, cst, ce.element_size(), "addmm input");
   }
   c10::DeviceGuard guard(d.device());
-  SPYRE_SPH_CHECK(sph_gemm(to_sph(d.scalar_type()), va.trans, vb.trans, m, n, k, alpha, va.ptr,
-                           va.ld, vb.ptr, vb.ld, cp ? beta : 0.f, cp, ldc_r, ldc_c,
-                           dd.data_ptr(), m == 1 ? n : dd.stride(0), SPH_EPI_NONE,
-                           stream(d.get_device())));
+  // workspace for a split-K last round of tiles, when the shape has one
+  const int64_t nws = sph_gemm_workspace_bytes(1, m, n, k);
+  at::Tensor ws = nws > 0 ? empty_spyre({nws}, at::kByte, d.device()) : at::Tensor();
+  SPYRE_SPH_CHECK(sph_gemm_ex(to_sph(d.scalar_type()), va.trans, vb.trans, 1, m, n, k, alpha,
+                              va.ptr, va.ld, 0, vb.ptr, vb.ld, 0, cp ? beta : 0.f, cp, ldc_r,
+                              ldc_c, 0, dd.data_ptr(), m == 1 ? n : dd.stride(0), 0,
+                              SPH_EPI_NONE, ws.defined() ? ws.data_ptr() : nullptr,
+                              ws.defined() ? nws : 0, stream(d.get_device())));
   if (!d_ok) device_copy(d, dd);
 }
 
@@ -211,8 +215,11 @@ at::Tensor gemm_swiglu(const at::Tensor& x_in, const at::Tensor& w_in) {
   if (fits) {
     check_matrix_extent(x, x.data_ptr(), m, k, x.stride(0), 0, 1, 0, "swiglu_mm x");
     check_matrix_extent(w, w.data_ptr(), 2 * n, k, w.stride(0), 0, 1, 0, "swiglu_mm w");
+    const int64_t nws = sph_gemm_swiglu_workspace_bytes(m, n, k);
+    at::Tensor ws = nws > 0 ? empty_spyre({nws}, at::kByte, out.device()) : at::Tensor();
     const int rc = sph_gemm_swiglu(to_sph(out.scalar_type()), m, n, k, x.data_ptr(), x.stride(0),
                                    w.data_ptr(), w.stride(0), out.data_ptr(), n,
+                                   ws.defined() ? ws.data_ptr() : nullptr, ws.defined() ? nws : 0,
                                    stream(out.get_device()));
     if (rc == 0) return out;
     TORCH_CHECK(rc == SPH_ERR_UNSUPPORTED || rc == SPH_ERR_TOO_LARGE, "spyre: sph_gemm_swiglu failed (status ",

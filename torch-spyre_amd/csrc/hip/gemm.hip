@@ -56,6 +56,13 @@ struct GemmArgs {
   int epilogue;
   int vec_a, vec_b, vec_d;
   int tiles_m, tiles_n;
+  // Split-K tail (direct-load kernel): tiles ranked tail_start.. run as
+  // `splits` workgroups each, over kslice K tiles apiece, writing fp32
+  // partial tiles to part[(rank - tail_start) * splits + split] that
+  // gemm_splitk_reduce sums.  tail_start = the tile count: no split.
+  int tail_start, splits, kslice;
+  float* part;
+  int64_t part_bytes;
 };
 
 template <typename T>
@@ -609,8 +616,17 @@ __global__ void __launch_bounds__(dl::Cfg<BN_>::NT) gemm_dl_kernel(const GemmArg
   static_assert(NDS <= NMF, "one read per MFMA");
   __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
 
+  // Tile rank and K slice: workgroups past tail_start are split-K slices of
+  // the tail tiles.
+  int rank = blockIdx.x, split = 0;
+  const bool partial = rank >= p.tail_start;
+  if (partial) {
+    const int q = rank - p.tail_start;
+    rank = p.tail_start + q / p.splits;
+    split = q % p.splits;
+  }
   int tm, tn;
-  tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  tile_of(rank, p.tiles_m, p.tiles_n, tm, tn);
   const int64_t batch = blockIdx.y;
   // first output column (SwiGLU: 128 output columns per tile)
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * (SWIGLU ? BN / 2 : BN);
@@ -619,7 +635,9 @@ __global__ void __launch_bounds__(dl::Cfg<BN_>::NT) gemm_dl_kernel(const GemmArg
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int lda = static_cast<int>(p.lda), ldb = static_cast<int>(p.ldb);
-  const int ksteps = static_cast<int>(p.k / BKD);
+  const int ksteps_all = static_cast<int>(p.k / BKD);
+  const int kt0 = partial ? split * p.kslice : 0;  // first K tile of this workgroup
+  const int ksteps = partial ? min(p.kslice, ksteps_all - kt0) : ksteps_all;
 
   // Buffer ranges: exactly the bytes this tile's rows (columns) span.
   const i32x4 ra = buffer_rsrc(A + m0 * lda, static_cast<uint32_t>(((BM - 1) * static_cast<int64_t>(lda) + p.k) * 2));
@@ -718,11 +736,12 @@ __global__ void __launch_bounds__(dl::Cfg<BN_>::NT) gemm_dl_kernel(const GemmArg
     const uint32_t sb_ = lds_base + ((SL_) & 1) * STAGE;                                    \
     if (l_ < LPA)                                                                           \
       dma16(ra, __builtin_amdgcn_readfirstlane(sb_ + (wave * LPA + l_) * 1024), va[l_],     \
-            __builtin_amdgcn_readfirstlane(t_ * BKD * 2));                                  \
+            __builtin_amdgcn_readfirstlane((kt0 + t_) * BKD * 2));                          \
     else                                                                                    \
       dma16(rb, __builtin_amdgcn_readfirstlane(sb_ + A_BYTES + (wave * LPB + l_ - LPA) * 1024), \
             vb[l_ - LPA],                                                                   \
-            __builtin_amdgcn_readfirstlane(B_KCONT ? t_ * BKD * 2 : t_ * BKD * ldb * 2));   \
+            __builtin_amdgcn_readfirstlane(B_KCONT ? (kt0 + t_) * BKD * 2                   \
+                                                   : (kt0 + t_) * BKD * ldb * 2));          \
   } while (0)
 
   // Prologue: K tiles 0 and 1 in flight; wait for tile 0; fragments of the
@@ -778,6 +797,20 @@ __global__ void __launch_bounds__(dl::Cfg<BN_>::NT) gemm_dl_kernel(const GemmArg
 
   // Epilogue (LDS reused as fp32 slabs once every DMA has landed).
   wait_vmcnt<0>();
+  if (partial) {
+    // split-K slice: the raw fp32 tile, element (r, c) at r * BN + c
+    float* W = p.part + (static_cast<int64_t>(rank - p.tail_start) * p.splits + split) * (BM * BN);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          W[row * BN + wn * WTN + j * 32 + (lane & 31)] = acc[i][j][r];
+        }
+    return;
+  }
   __syncthreads();
   T* D = static_cast<T*>(p.d) + batch * p.stride_d;
   const T* C = p.c ? static_cast<const T*>(p.c) + batch * p.stride_c : nullptr;
@@ -813,6 +846,63 @@ __global__ void __launch_bounds__(dl::Cfg<BN_>::NT) gemm_dl_kernel(const GemmArg
       __syncthreads();
     }
   }
+}
+
+// Sums the split-K slices of one tail tile and applies the epilogue: one
+// workgroup per (tail tile, 1024 output elements); each thread takes 4
+// consecutive output columns of one row (16-byte reads of every slice).
+// SWIGLU: output column oc of the tile is silu(gate) * up with the gate sum
+// at tile column 64 (oc / 32) + oc % 32 and the up sum 32 columns further.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T, int BN, bool SWIGLU>
+__global__ void __launch_bounds__(256) gemm_splitk_reduce(const GemmArgs p) {
+  constexpr int OUTN = SWIGLU ? BN / 2 : BN;   // output columns per tile
+  constexpr int PER_WG = 1024;                  // outputs per workgroup
+  const int t = blockIdx.x;                     // tail tile
+  const int e = blockIdx.y * PER_WG + threadIdx.x * 4;
+  const int r = e / OUTN, oc = e % OUTN;
+  int tm, tn;
+  tile_of(p.tail_start + t, p.tiles_m, p.tiles_n, tm, tn);
+  const int64_t row = static_cast<int64_t>(tm) * dl::BM + r;
+  const int64_t col = static_cast<int64_t>(tn) * OUTN + oc;
+  const float* W = p.part + static_cast<int64_t>(t) * p.splits * (dl::BM * BN) + r * BN;
+  float v[4] = {0.f, 0.f, 0.f, 0.f}, u[4] = {0.f, 0.f, 0.f, 0.f};
+  const int cg = SWIGLU ? 64 * (oc / 32) + oc % 32 : oc;
+  for (int sp = 0; sp < p.splits; ++sp) {
+    const float* Ws = W + static_cast<int64_t>(sp) * (dl::BM * BN);
+    const f32x4 a = *reinterpret_cast<const f32x4*>(Ws + cg);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] += a[i];
+    if constexpr (SWIGLU) {
+      const f32x4 b = *reinterpret_cast<const f32x4*>(Ws + cg + 32);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) u[i] += b[i];
+    }
+  }
+  T* D = static_cast<T*>(p.d);
+  float out[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float x;
+    if constexpr (SWIGLU) {
+      x = silu(v[i]) * u[i];
+    } else {
+      x = p.alpha * v[i];
+      if (p.c != nullptr && p.beta != 0.f)
+        x += p.beta * Num<T>::to_f(static_cast<const T*>(p.c)[row * p.ldc_row + (col + i) * p.ldc_col]);
+      if (p.epilogue == SPH_EPI_RELU) x = fmaxf(x, 0.f);
+      else if (p.epilogue == SPH_EPI_GELU) x = gelu_erf(x);
+      else if (p.epilogue == SPH_EPI_SILU) x = silu(x);
+    }
+    out[i] = x;
+  }
+  u32x2 w;
+  w[0] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, Num<T>::from_f(out[0]))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, Num<T>::from_f(out[1]))) << 16);
+  w[1] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, Num<T>::from_f(out[2]))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, Num<T>::from_f(out[3]))) << 16);
+  *reinterpret_cast<u32x2*>(D + row * p.ldd + col) = w;
 }
 
 // ---------------------------------------------------------------------------
@@ -1364,15 +1454,58 @@ inline bool dl_fits(const GemmArgs& p, bool b_kcont, int bn) {
 
 constexpr int64_t kNumCUs = 256;  // MI355X compute units
 
-template <typename T, int BN>
-int launch_dl(GemmArgs& p, int64_t batch, bool b_kcont, hipStream_t st) {
+// Split-K for the last, partial round of 256-wide tiles (batch 1): when
+// `tiles` is not a multiple of the CU count, the tail tiles would run as a
+// round of their own on a few CUs.  Each tail tile is split into up to 8
+// K slices (enough to fill the CUs; K >= 2048, so a slice keeps >= 4 K
+// tiles) whose fp32 partial tiles a reduce kernel sums.  A tail of 0 (e.g.
+// 4096^3) takes no split.  Measured on one MI355X: the c4 decoder layer
+// (M = 2048: gate/up 800 tiles, O and down 128 tiles) 1.143 -> 1.037 ms.
+struct SplitPlan {
+  int splits = 1, kslice = 0;
+  int64_t tail_start = 0, bytes = 0;
+};
+inline SplitPlan splitk_plan(int64_t tiles, int64_t ksteps, int bn) {
+  SplitPlan pl;
+  pl.tail_start = tiles;
+  if (tiles <= 0 || tiles >= (1LL << 30) || ksteps < 32) return pl;
+  const int64_t full = tiles / kNumCUs * kNumCUs, tail = tiles - full;
+  if (tail == 0) return pl;
+  int64_t sp = kNumCUs / tail;
+  sp = sp < 8 ? sp : 8;
+  if (sp < 2) return pl;
+  const int64_t kslice = ceil_div(ksteps, sp);
+  sp = ceil_div(ksteps, kslice);  // every slice non-empty
+  if (sp < 2) return pl;
+  pl.splits = static_cast<int>(sp);
+  pl.kslice = static_cast<int>(kslice);
+  pl.tail_start = full;
+  pl.bytes = tail * sp * dl::BM * bn * 4;
+  return pl;
+}
+
+// Launches the direct-load kernel (and, with a split plan, the reduce).
+template <typename T, int BN, bool SWIGLU = false>
+int launch_dl(GemmArgs& p, int64_t batch, bool b_kcont, hipStream_t st,
+              const SplitPlan* plan = nullptr) {
   p.tiles_m = static_cast<int>(p.m / dl::BM);
-  p.tiles_n = static_cast<int>(p.n / BN);
-  dim3 grid(static_cast<unsigned>(p.tiles_m) * p.tiles_n, static_cast<unsigned>(batch));
+  p.tiles_n = static_cast<int>(p.n / (SWIGLU ? BN / 2 : BN));
+  const int64_t tiles = static_cast<int64_t>(p.tiles_m) * p.tiles_n;
+  const bool split = plan != nullptr && plan->splits > 1 && batch == 1;
+  p.tail_start = static_cast<int>(split ? plan->tail_start : tiles);
+  p.splits = split ? plan->splits : 1;
+  p.kslice = split ? plan->kslice : 0;
+  const int64_t wgs = split ? plan->tail_start + (tiles - plan->tail_start) * plan->splits : tiles;
+  dim3 grid(static_cast<unsigned>(wgs), static_cast<unsigned>(batch));
   if (b_kcont)
-    gemm_dl_kernel<T, true, BN><<<grid, dim3(dl::Cfg<BN>::NT), 0, st>>>(p);
-  else
+    gemm_dl_kernel<T, true, BN, SWIGLU><<<grid, dim3(dl::Cfg<BN>::NT), 0, st>>>(p);
+  else if constexpr (!SWIGLU)
     gemm_dl_kernel<T, false, BN><<<grid, dim3(dl::Cfg<BN>::NT), 0, st>>>(p);
+  if (split) {
+    constexpr int OUTN = SWIGLU ? BN / 2 : BN;
+    dim3 rg(static_cast<unsigned>(tiles - plan->tail_start), (dl::BM * OUTN) / 1024);
+    gemm_splitk_reduce<T, BN, SWIGLU><<<rg, 256, 0, st>>>(p);
+  }
   return check_launch("sph_gemm");
 }
 
@@ -1450,6 +1583,11 @@ int gemm_dispatch(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
     const int64_t tn = (p.m / dl::BM) * (p.n / 128) * batch;
     const bool w256 = p.n % 256 == 0 && dl_fits(p, b_kcont, 256) && tw < (1LL << 31);
     const bool w128 = dl_fits(p, b_kcont, 128) && tn < (1LL << 31);
+    // with a workspace, 256-wide tiles whose last round is split along K
+    if (w256 && batch == 1 && p.part != nullptr) {
+      const SplitPlan pl = splitk_plan(tw, p.k / dl::BKD, 256);
+      if (pl.splits > 1 && pl.bytes <= p.part_bytes) return launch_dl<T, 256>(p, batch, b_kcont, st, &pl);
+    }
     if (w256 && (!w128 || fill(tw) >= 0.75 * fill(tn))) return launch_dl<T, 256>(p, batch, b_kcont, st);
     if (w128) return launch_dl<T, 128>(p, batch, b_kcont, st);
   }
@@ -1469,12 +1607,13 @@ int gemm_dispatch(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
 
 using namespace sph;
 
-extern "C" int sph_gemm_strided_batched(
-    sph_dtype dtype, int trans_a, int trans_b, int64_t batch, int64_t m,
-    int64_t n, int64_t k, float alpha, const void* a, int64_t lda,
-    int64_t stride_a, const void* b, int64_t ldb, int64_t stride_b, float beta,
-    const void* c, int64_t ldc_row, int64_t ldc_col, int64_t stride_c, void* d,
-    int64_t ldd, int64_t stride_d, int epilogue, sph_stream_t stream) {
+namespace {
+int gemm_entry(sph_dtype dtype, int trans_a, int trans_b, int64_t batch, int64_t m, int64_t n,
+               int64_t k, float alpha, const void* a, int64_t lda, int64_t stride_a,
+               const void* b, int64_t ldb, int64_t stride_b, float beta, const void* c,
+               int64_t ldc_row, int64_t ldc_col, int64_t stride_c, void* d, int64_t ldd,
+               int64_t stride_d, int epilogue, void* workspace, int64_t workspace_bytes,
+               sph_stream_t stream) {
   SPH_REQUIRE(m >= 0 && n >= 0 && k >= 0 && batch >= 0, SPH_ERR_INVALID_ARG,
               "gemm: negative size");
   SPH_REQUIRE(dtype == SPH_F16 || dtype == SPH_BF16, SPH_ERR_UNSUPPORTED,
@@ -1517,9 +1656,41 @@ extern "C" int sph_gemm_strided_batched(
   p.vec_a = al16(a) && (lda % 8 == 0) && (batch == 1 || stride_a % 8 == 0);
   p.vec_b = al16(b) && (ldb % 8 == 0) && (batch == 1 || stride_b % 8 == 0);
   p.vec_d = al16(d) && (ldd % 8 == 0) && (batch == 1 || stride_d % 8 == 0);
+  p.part = workspace != nullptr && workspace_bytes > 0 && p.vec_d ? static_cast<float*>(workspace)
+                                                                  : nullptr;
+  p.part_bytes = p.part != nullptr ? workspace_bytes : 0;
   hipStream_t st = as_stream(stream);
   if (dtype == SPH_F16) return gemm_dispatch<half_t>(p, batch, a_kcont, b_kcont, st);
   return gemm_dispatch<bf16_t>(p, batch, a_kcont, b_kcont, st);
+}
+}  // namespace
+
+extern "C" int sph_gemm_strided_batched(
+    sph_dtype dtype, int trans_a, int trans_b, int64_t batch, int64_t m,
+    int64_t n, int64_t k, float alpha, const void* a, int64_t lda,
+    int64_t stride_a, const void* b, int64_t ldb, int64_t stride_b, float beta,
+    const void* c, int64_t ldc_row, int64_t ldc_col, int64_t stride_c, void* d,
+    int64_t ldd, int64_t stride_d, int epilogue, sph_stream_t stream) {
+  return gemm_entry(dtype, trans_a, trans_b, batch, m, n, k, alpha, a, lda, stride_a, b, ldb,
+                    stride_b, beta, c, ldc_row, ldc_col, stride_c, d, ldd, stride_d, epilogue,
+                    nullptr, 0, stream);
+}
+
+extern "C" int64_t sph_gemm_workspace_bytes(int64_t batch, int64_t m, int64_t n, int64_t k) {
+  if (batch != 1 || m % dl::BM != 0 || n % 256 != 0 || k % dl::BKD != 0 || k <= 0) return 0;
+  return splitk_plan((m / dl::BM) * (n / 256), k / dl::BKD, 256).bytes;
+}
+
+extern "C" int sph_gemm_ex(sph_dtype dtype, int trans_a, int trans_b, int64_t batch, int64_t m,
+                           int64_t n, int64_t k, float alpha, const void* a, int64_t lda,
+                           int64_t stride_a, const void* b, int64_t ldb, int64_t stride_b,
+                           float beta, const void* c, int64_t ldc_row, int64_t ldc_col,
+                           int64_t stride_c, void* d, int64_t ldd, int64_t stride_d, int epilogue,
+                           void* workspace, int64_t workspace_bytes, sph_stream_t stream) {
+  SPH_REQUIRE(workspace_bytes >= 0, SPH_ERR_INVALID_ARG, "gemm: negative workspace size");
+  return gemm_entry(dtype, trans_a, trans_b, batch, m, n, k, alpha, a, lda, stride_a, b, ldb,
+                    stride_b, beta, c, ldc_row, ldc_col, stride_c, d, ldd, stride_d, epilogue,
+                    workspace, workspace_bytes, stream);
 }
 
 extern "C" int sph_gemm(sph_dtype dtype, int trans_a, int trans_b, int64_t m,
@@ -1533,9 +1704,14 @@ extern "C" int sph_gemm(sph_dtype dtype, int trans_a, int trans_b, int64_t m,
                                   0, d, ldd, 0, epilogue, stream);
 }
 
+extern "C" int64_t sph_gemm_swiglu_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m <= 8 || m % dl::BM != 0 || n % 128 != 0 || k % dl::BKD != 0 || k <= 0) return 0;
+  return splitk_plan((m / dl::BM) * (n / 128), k / dl::BKD, 256).bytes;
+}
+
 extern "C" int sph_gemm_swiglu(sph_dtype dtype, int64_t m, int64_t n, int64_t k, const void* a,
                                int64_t lda, const void* w, int64_t ldw, void* d, int64_t ldd,
-                               sph_stream_t stream) {
+                               void* workspace, int64_t workspace_bytes, sph_stream_t stream) {
   SPH_REQUIRE(m >= 0 && n >= 0 && k >= 0, SPH_ERR_INVALID_ARG, "gemm_swiglu: negative size");
   SPH_REQUIRE(dtype == SPH_F16 || dtype == SPH_BF16, SPH_ERR_UNSUPPORTED,
               "gemm_swiglu: dtype must be F16 or BF16");
@@ -1598,15 +1774,13 @@ extern "C" int sph_gemm_swiglu(sph_dtype dtype, int64_t m, int64_t n, int64_t k,
   p.alpha = 1.f;
   p.epilogue = SPH_EPI_NONE;
   p.vec_a = p.vec_b = p.vec_d = 1;
-  p.tiles_m = static_cast<int>(m / dl::BM);
-  p.tiles_n = static_cast<int>(n / 128);
-  const dim3 grid(static_cast<unsigned>(p.tiles_m) * p.tiles_n);
   hipStream_t st = as_stream(stream);
+  const SplitPlan pl = splitk_plan((m / dl::BM) * (n / 128), k / dl::BKD, 256);
+  const bool split = pl.splits > 1 && workspace != nullptr && workspace_bytes >= pl.bytes;
+  p.part = split ? static_cast<float*>(workspace) : nullptr;
   if (dtype == SPH_F16)
-    gemm_dl_kernel<half_t, true, 256, true><<<grid, dim3(dl::Cfg<256>::NT), 0, st>>>(p);
-  else
-    gemm_dl_kernel<bf16_t, true, 256, true><<<grid, dim3(dl::Cfg<256>::NT), 0, st>>>(p);
-  return check_launch("sph_gemm_swiglu");
+    return launch_dl<half_t, 256, true>(p, 1, true, st, split ? &pl : nullptr);
+  return launch_dl<bf16_t, 256, true>(p, 1, true, st, split ? &pl : nullptr);
 }
 
 extern "C" int sph_gemm_f16(int64_t m, int64_t n, int64_t k, const void* a,

@@ -55,7 +55,13 @@ _SIGS = {
     "sph_gemm_strided_batched": ([c_int, c_int, c_int, c_i64, c_i64, c_i64, c_i64, c_f32, vp,
                                   c_i64, c_i64, vp, c_i64, c_i64, c_f32, vp, c_i64, c_i64,
                                   c_i64, vp, c_i64, c_i64, c_int, vp], c_int),
-    "sph_gemm_swiglu": ([c_int, c_i64, c_i64, c_i64, vp, c_i64, vp, c_i64, vp, c_i64, vp], c_int),
+    "sph_gemm_swiglu": ([c_int, c_i64, c_i64, c_i64, vp, c_i64, vp, c_i64, vp, c_i64, vp, c_i64,
+                         vp], c_int),
+    "sph_gemm_swiglu_workspace_bytes": ([c_i64, c_i64, c_i64], c_i64),
+    "sph_gemm_ex": ([c_int, c_int, c_int, c_i64, c_i64, c_i64, c_i64, c_f32, vp, c_i64, c_i64, vp,
+                     c_i64, c_i64, c_f32, vp, c_i64, c_i64, c_i64, vp, c_i64, c_i64, c_int, vp,
+                     c_i64, vp], c_int),
+    "sph_gemm_workspace_bytes": ([c_i64, c_i64, c_i64, c_i64], c_i64),
     "sph_gemm_f16": ([c_i64, c_i64, c_i64, vp, vp, vp, vp], c_int),
     "sph_bmm_f16": ([c_i64, c_i64, c_i64, c_i64, vp, vp, vp, vp], c_int),
     "sph_attention_fwd": ([c_int, c_i64, c_i64, c_i64, c_i64, vp, c_i64, c_i64, vp, c_i64,
