@@ -596,9 +596,10 @@ def main(argv=None):
     ap.add_argument("--c5-layers", type=int, default=40)
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--kernel", choices=["all", "gemm", "copy", "decoder", "bmm", "h2d",
-                                         "attention"],
+                                         "attention", "spyre"],
                     default="all",
-                    help="gemm / copy / decoder / bmm / h2d / attention: run only that part "
+                    help="gemm / copy / decoder / bmm / h2d / attention / spyre (the eager and "
+                         "compiled paths on spyre tensors): run only that part "
                          "(for rocprofv3 passes)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -626,6 +627,9 @@ def main(argv=None):
         return 0
     if args.kernel == "h2d":
         print(json.dumps({"kernel": "h2d", **bench_host_copies()}))
+        return 0
+    if args.kernel == "spyre":
+        print(json.dumps({"kernel": "spyre", **bench_spyre_paths(args.steps, args.warmup)}))
         return 0
     if args.kernel == "decoder":
         print(json.dumps({"kernel": "decoder",

@@ -85,10 +85,35 @@ def test_layernorm_gelu_rmsnorm_fuse(fake_device):
     assert len(_kernels(code)) == 1 and "block_welford" in code
     code = _compile(lambda x, s, b: (lambda y: (y, y.sum(-1)))(F.gelu(x * s + b)),
                     [((64, 4096), torch.float16), ((4096,), torch.float16), ((4096,), torch.float16)])
-    assert len(_kernels(code)) == 1 and "erf_fast" in code
+    assert len(_kernels(code)) == 1 and "spy::gelu_erf(" in code
     code = _compile(lambda x, r, w: (lambda h: (h, torch.rms_norm(h, [4096], w, 1e-5)))(x + r),
                     [((64, 4096), torch.float16), ((64, 4096), torch.float16), ((4096,), torch.float16)])
     assert len(_kernels(code)) == 1
+
+
+def _source(code):
+    src = re.search(r"source='(.*?)',\n", code, re.S).group(1)
+    return src.encode().decode("unicode_escape")
+
+
+def test_row_phases_reuse_stored_values(fake_device):
+    # add + LayerNorm: the residual sum is stored once and the normalise
+    # phase takes it from registers, not by reading the output back
+    code = _compile(lambda x, r, w, b: (lambda h: (h, F.layer_norm(h, [4096], w, b, 1e-5)))(x + r),
+                    [((64, 4096), torch.float16)] * 2 + [((4096,), torch.float16)] * 2)
+    src = _source(code)
+    out = re.search(r"(out_ptr\d+)\[r0_1 \+ 4096LL\*x0\] = ", src).group(1)
+    assert src.count(f"{out}[") == 1, src  # the store only
+    assert "welford_acc_add" in src and "welford_finish" in src and "welford_add(" not in src
+
+
+def test_gelu_peephole_only_on_the_erf_form(fake_device):
+    specs = [((64, 4096), torch.float16)]
+    # the tanh form and a near miss (a different scale inside erf) keep the generic code
+    for fn in (lambda x: F.gelu(x, approximate="tanh"),
+               lambda x: x * 0.5 * (1 + torch.erf(x * 0.7))):
+        assert "gelu_erf" not in _compile(fn, specs)
+    assert "spy::gelu_erf(" in _compile(lambda x: x * 0.5 * (1 + torch.erf(x * 0.7071067811865476)), specs)
 
 
 def test_matmul_is_extern_mfma_call(fake_device):

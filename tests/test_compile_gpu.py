@@ -82,6 +82,28 @@ def test_c3_norms_and_gelu_chain_compiled_vs_oracle():
     np.testing.assert_allclose(rs.cpu().float().numpy(), ers, rtol=2e-2, atol=0.5)
 
 
+def test_compiled_variance_and_gelu_edges():
+    # LayerNorm's per-thread variance is summed around a data point, so a
+    # large mean with a small spread keeps its precision (fp32 in and out,
+    # against float64 on the CPU); the looped form (rows longer than the
+    # register-held ones) goes the same way
+    for cols in (4096, 40960):
+        _log(f"compiled layer_norm fp32, mean 100, std 0.1, [32,{cols}]")
+        g = torch.Generator().manual_seed(11)
+        x = 100 + 0.1 * torch.randn(32, cols, generator=g)
+        y = torch.compile(lambda a: F.layer_norm(a, [cols], eps=1e-5), dynamic=False)(x.to(DEV))
+        ref = F.layer_norm(x.double(), [cols], eps=1e-5).float()
+        torch.testing.assert_close(y.cpu(), ref, rtol=0, atol=2e-4)
+    # the erf form of GELU (one call in the generated code) over its
+    # breakpoints and special values, against torch's CPU gelu (fp32)
+    _log("compiled gelu special values")
+    v = [-float("inf"), -30.0, -5.6, -5.5, -5.4, -3.0, -0.5, -1e-3, 0.0, 1e-3, 0.5, 3.0, 5.4,
+         5.5, 5.6, 30.0, float("nan"), float("inf")]
+    x = torch.tensor(v + torch.linspace(-8, 8, 4096 - len(v)).tolist()).reshape(2, 2048)
+    y = torch.compile(lambda a: F.gelu(a), dynamic=False)(x.to(DEV)).cpu()
+    torch.testing.assert_close(y, F.gelu(x), rtol=0, atol=1e-6, equal_nan=True)
+
+
 def test_c2_matmul_and_bmm_compiled():
     _log("compiled mm / bmm")
     A, B = uniform((1024, 2048), k=0), uniform((2048, 512), k=1)

@@ -128,6 +128,26 @@ __device__ inline float erf_fast(float x) {
   return a < 0.5f ? small : large;
 }
 
+// GELU, erf form: x Phi(x) = max(x, 0) - |x| h(|x|) with h(a) = erfc(a/sqrt 2)/2
+// the Gaussian tail.  log2 h on [0, 5.5] is the degree-7 least-squares
+// polynomial (fit in float64 on 200001 points in the Chebyshev basis,
+// converted to monomials); past 5.5, h < 1.9e-8 and is taken as 0.
+// Absolute error below 5.3e-7 for every finite x (float32, against float64
+// erfc); +-inf and NaN give NaN.
+__device__ inline float gelu_erf(float x) {
+  const float ax = fabsf(x);
+  const float a = fminf(ax, 5.5f);
+  float p = fmaf(-1.9959244095426196e-06f, a, 6.483463872904686e-05f);
+  p = fmaf(p, a, -0.0009561956288912488f);
+  p = fmaf(p, a, 0.00860984128475729f);
+  p = fmaf(p, a, -0.054171898352491525f);
+  p = fmaf(p, a, -0.45824610324983095f);
+  p = fmaf(p, a, -1.1513446909430594f);
+  p = fmaf(p, a, -0.9999850572286579f);
+  const float h = ax < 5.5f ? __builtin_amdgcn_exp2f(p) : 0.f;
+  return fmaf(-ax, h, fmaxf(x, 0.f));
+}
+
 // Integer index helpers used by printed index expressions.
 __device__ inline int64_t floordiv_i(int64_t a, int64_t b) {
   int64_t q = a / b;
@@ -249,30 +269,81 @@ __device__ inline Welford welford_add(Welford a, float x) {
   return welford_combine(a, b);
 }
 
+// One thread's share of a row, accumulated without a division per element:
+// sums of x - c and (x - c)^2 around the thread's first element c (the
+// shifted-data algorithm; Chan, Golub & LeVeque, "Algorithms for computing
+// the sample variance", 1983, section 3).  c lies within the data, so the
+// sums carry no cancellation beyond that of the data's own spread.
+// welford_finish turns it into a Welford state for the cross-thread combine.
+struct WelfordAcc {
+  float shift, s1, s2, n;
+};
+__device__ inline WelfordAcc welford_acc_add(WelfordAcc a, float x) {
+  const float c = a.n == 0.f ? x : a.shift;
+  const float d = x - c;
+  return WelfordAcc{c, a.s1 + d, fmaf(d, d, a.s2), a.n + 1.f};
+}
+__device__ inline Welford welford_finish(WelfordAcc a) {
+  if (a.n == 0.f) return Welford{0.f, 0.f, 0.f};
+  const float m = a.s1 / a.n;
+  return Welford{a.shift + m, fmaxf(fmaf(-a.s1, m, a.s2), 0.f), a.n};
+}
+
+// Welford states summed around a shift k: (sum w, sum w (mean - k),
+// sum m2 + w (mean - k)^2) add without divisions, and the state of the union
+// is mean = k + S1/W, m2 = S2 - S1^2/W.  With k the mean of one member, the
+// subtraction cancels only as much as that member's mean differs from the
+// union's (the parallel form of the shifted-data algorithm; Chan, Golub &
+// LeVeque 1983).  Empty members (w = 0) add nothing.
+__device__ inline void welford_shifted(Welford s, float k, float& w, float& s1, float& s2) {
+  const float d = s.weight > 0.f ? s.mean - k : 0.f;
+  w = s.weight;
+  s1 = s.weight * d;
+  s2 = fmaf(s1, d, s.m2);
+}
+__device__ inline Welford welford_unshift(float k, float w, float s1, float s2) {
+  if (!(w > 0.f)) return Welford{0.f, 0.f, 0.f};
+  const float m = s1 / w;
+  return Welford{k + m, fmaxf(fmaf(-s1, m, s2), 0.f), w};
+}
+
+// Welford state of the whole workgroup's row, on every thread: per wave,
+// shifted sums around lane 0's mean (three butterflies, no divisions); across
+// waves, the same around wave 0's mean.  Two barriers, so every thread of
+// the workgroup must call it.
 template <int BLOCK>
 __device__ inline Welford block_welford(Welford s, float* lds) {
+  const float k = __shfl(s.mean, 0, kWave);
+  float w, s1, s2;
+  welford_shifted(s, k, w, s1, s2);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
-    Welford o;
-    o.mean = __shfl_xor(s.mean, off, kWave);
-    o.m2 = __shfl_xor(s.m2, off, kWave);
-    o.weight = __shfl_xor(s.weight, off, kWave);
-    s = welford_combine(s, o);
+    w += __shfl_xor(w, off, kWave);
+    s1 += __shfl_xor(s1, off, kWave);
+    s2 += __shfl_xor(s2, off, kWave);
   }
+  s = welford_unshift(k, w, s1, s2);
   if constexpr (BLOCK > kWave) {
     constexpr int NW = BLOCK / kWave;
-    const int w = threadIdx.x / kWave;
+    const int wv = threadIdx.x / kWave;
     if ((threadIdx.x % kWave) == 0) {
-      lds[w] = s.mean;
-      lds[NW + w] = s.m2;
-      lds[2 * NW + w] = s.weight;
+      lds[wv] = s.mean;
+      lds[NW + wv] = s.m2;
+      lds[2 * NW + wv] = s.weight;
     }
     __syncthreads();
-    Welford r{lds[0], lds[NW], lds[2 * NW]};
+    const float k2 = lds[0];
+    float tw = 0.f, t1 = 0.f, t2 = 0.f;
 #pragma unroll
-    for (int k = 1; k < NW; ++k) r = welford_combine(r, Welford{lds[k], lds[NW + k], lds[2 * NW + k]});
+    for (int i = 0; i < NW; ++i) {
+      float a, b, c;
+      welford_shifted(Welford{lds[i], lds[NW + i], lds[2 * NW + i]}, k2, a, b, c);
+      tw += a;
+      t1 += b;
+      t2 += c;
+    }
     __syncthreads();
-    s = r;
+    s = welford_unshift(k2, tw, t1, t2);
   }
   return s;
 }

@@ -22,6 +22,7 @@ from __future__ import annotations
 
 import itertools
 import math
+import re
 from typing import Any, Optional, Union
 
 import sympy
@@ -56,6 +57,9 @@ DTYPE_TO_HIP = {
 
 # Values of these dtypes are widened to fp32 on load.
 _FLOAT_LOAD = {torch.float16, torch.bfloat16, torch.float32, torch.float64}
+_PRODUCT = re.compile(r"^(\w+) \* (\w+)$")
+_SUM = re.compile(r"^(\w+) \+ (\w+)$")
+_ERF = re.compile(r"^spy::erf_fast\((\w+)\)$")
 
 MAX_BLOCK = 512
 # Row loops of at most this many trips keep each loaded value in registers
@@ -172,8 +176,71 @@ class HipExprPrinter(ExprPrinter):
 _printer = HipExprPrinter()
 
 
+def _defining_expr(v: Any) -> Optional[str]:
+    """The expression a CSE variable of the current kernel was generated
+    from (None for anything else)."""
+    if not isinstance(v, CSEVariable):
+        return None
+    for key, var in V.kernel.cse._cache.items():
+        if var is v and isinstance(key, str):
+            return key
+    return None
+
+
+def _product(e: Optional[str]) -> Optional[tuple[str, str]]:
+    m = _PRODUCT.match(e) if e is not None else None
+    return (m.group(1), m.group(2)) if m else None
+
+
+def _scaled_by(e: Optional[str], const: str) -> Optional[str]:
+    """x when `e` is x * c or c * x with c a variable holding `const`."""
+    p = _product(e)
+    if p is None:
+        return None
+    for x, c in (p, p[::-1]):
+        var = V.kernel.cse.try_get(const)
+        if var is not None and str(var) == c:
+            return x
+    return None
+
+
+def _gelu_input(half: Any, tail: Any) -> Optional[str]:
+    """x when half * tail is the erf form of GELU that aten.gelu decomposes
+    into: (x * 0.5) * (erf(x * M_SQRT1_2) + 1)."""
+    x = _scaled_by(_defining_expr(half), hip_value(0.5))
+    if x is None:
+        return None
+    t = _defining_expr(tail)
+    m = _SUM.match(t) if t is not None else None
+    if m is None:
+        return None
+    one = V.kernel.cse.try_get(hip_value(1.0))
+    for e, c in ((m.group(1), m.group(2)), (m.group(2), m.group(1))):
+        if one is None or str(one) != c:
+            continue
+        evar = next((v for k, v in V.kernel.cse._cache.items() if str(v) == e), None)
+        f = _ERF.match(_defining_expr(evar) or "")
+        if f is None:
+            continue
+        arg = next((v for k, v in V.kernel.cse._cache.items() if str(v) == f.group(1)), None)
+        if _scaled_by(_defining_expr(arg), hip_value(math.sqrt(0.5))) == x:
+            return x
+    return None
+
+
 class SpyreOverrides(OpOverrides):
     """Pointwise ops as HIP C++ expressions on fp32 (or native int) values."""
+
+    @staticmethod
+    def mul(a, b):
+        # GELU's erf form collapses to one call (spy::gelu_erf): max(x, 0)
+        # minus |x| times a Gaussian tail, about a third of the operations
+        # of 0.5 x (1 + erf(x / sqrt 2)) through a general erf.
+        for h, t in ((a, b), (b, a)):
+            x = _gelu_input(h, t)
+            if x is not None:
+                return f"spy::gelu_erf({x})"
+        return f"{a} * {b}"
 
     @staticmethod
     def to_dtype(x, dtype: torch.dtype, src_dtype: Optional[torch.dtype] = None,
@@ -562,9 +629,24 @@ class SpyreKernel(SIMDKernel):
         index = self.prepare_indexing(index)
         dtype = V.graph.get_dtype(name)
         self._record_extent(str(var), index, False)
-        line = f"{var}[{self.index_to_str(index)}] = spy::cvt<{self.dtype_to_str(dtype)}>({value});"
+        ctype = self.dtype_to_str(dtype)
+        line = f"{var}[{self.index_to_str(index)}] = spy::cvt<{ctype}>({value});"
         if self.inside_reduction:
             self.compute.writeline(DeferredLine(name, line))
+            if self._cacheable_row_load(index):
+                # later phases of the row read the stored value (as rounded
+                # to the buffer's dtype) from registers, not back from memory
+                key = (str(var), self.index_to_str(index))
+                arr = self._row_cache.get(key)
+                fl = dtype in _FLOAT_LOAD
+                if arr is None:
+                    arr = f"rc{len(self._row_cache)}"
+                    self.indexing_code.writeline(
+                        f"{'float' if fl else ctype} {arr}[{self._trips() * self._rvec()}];")
+                    self._row_cache[key] = arr
+                stored = f"spy::cvt<{ctype}>({value})"
+                self.compute.writeline(f"{arr}[r0_cnt * {self._rvec()} + spy_v] = "
+                                       f"{f'spy::to_f({stored})' if fl else stored};")
         else:
             self.stores.writeline(DeferredLine(name, line))
 
@@ -628,10 +710,12 @@ class SpyreKernel(SIMDKernel):
                 self.stores, f"spy::block_arg<{is_max}, {b}>({av}, {ai}, spy_lds, spy_lds_i)",
                 dtype=torch.int64)
         if reduction_type == "welford_reduce":
-            acc = self._acc("spy::Welford {name} = {{0.f, 0.f, 0.f}};")
-            self.compute.writeline(f"{acc} = spy::welford_add({acc}, static_cast<float>({value}));")
-            res = self.cse.generate(self.stores, f"spy::block_welford<{b}>({acc}, spy_lds)",
-                                    dtype=torch.float32)
+            acc = self._acc("spy::WelfordAcc {name} = {{0.f, 0.f, 0.f, 0.f}};")
+            self.compute.writeline(
+                f"{acc} = spy::welford_acc_add({acc}, static_cast<float>({value}));")
+            res = self.cse.generate(
+                self.stores, f"spy::block_welford<{b}>(spy::welford_finish({acc}), spy_lds)",
+                dtype=torch.float32)
             return OpsWrapper._unwrap(
                 tuple(CSEVariable(f"{res}.{f}", ValueRanges.unknown(), torch.float32)
                       for f in ("mean", "m2", "weight")))
