@@ -89,6 +89,34 @@ def test_softmax_dtypes_log_scale_strided(in_dt, out_dt):
         assert torch.all(yd[:, cols:].cpu() == 0)  # nothing written past cols
 
 
+@pytest.mark.parametrize("in_dt,out_dt", [(torch.float16, torch.float16),
+                                          (torch.bfloat16, torch.bfloat16),
+                                          (torch.float32, torch.float32),
+                                          (torch.float16, torch.float32)])
+@pytest.mark.parametrize("cols", [512, 2048, 4096])
+def test_softmax_whole_rows(in_dt, out_dt, cols):
+    # rows of exactly one register configuration's width take the path
+    # without per-chunk bounds tests: strided rows, a partial last group of
+    # rows (several rows per workgroup at 512 / 2048 columns), log, scale and
+    # the causal mask
+    rows, ld = 9, cols + 64
+    _log(f"softmax whole rows {in_dt}->{out_dt} cols={cols}")
+    big = randn((rows, ld), k=4, scale=3.0, dtype=in_dt)
+    xd = big.to(DEV)
+    for flags, q_len in ((0, 0), (_capi.SOFTMAX_LOG, 0), (_capi.SOFTMAX_CAUSAL, 3)):
+        yd = torch.zeros(rows, ld, dtype=out_dt, device=DEV)
+        off = cols - 3 - 100 if q_len else 0
+        _capi.call("sph_softmax_rows", DT[in_dt], DT[out_dt], _p(xd), ld, _p(yd), ld,
+                   rows, cols, 0.5, flags, q_len, off, _stream())
+        _sync()
+        want = O.softmax(big[:, :cols].float().numpy(), scale=0.5, log=flags == _capi.SOFTMAX_LOG,
+                         causal_q_len=q_len, causal_offset=off)
+        tol = 1e-4 if out_dt == torch.float32 and in_dt == torch.float32 else 1e-2
+        assert_close_fp(yd[:, :cols], want, out_dtype=out_dt, rtol=tol, atol=tol,
+                        what=f"softmax whole rows flags={flags}")
+        assert torch.all(yd[:, cols:].cpu() == 0)
+
+
 @pytest.mark.parametrize("q_len,k_len", [(5, 9), (2048, 2048), (1, 1152), (7, 64)])
 def test_softmax_causal(q_len, k_len):
     _log(f"softmax causal {q_len}x{k_len}")

@@ -138,40 +138,54 @@ __device__ inline void wait_vmcnt() {
 constexpr uint8_t MB_ZERO = 0, MB_MIXED = 1, MB_NEGINF = 2;
 
 // One workgroup per (mask batch, row block, key block): class the block's
-// 128 x 64 mask values (keys past sk ignored).
+// 128 x 64 mask values (keys past sk ignored).  The classes are read off the
+// 16-bit patterns (fp16 and bf16 alike: zero is +-0, -inf is one pattern), two
+// values per 32-bit word, and the workgroup's verdicts meet in one LDS word
+// per wave behind a single barrier.
 template <typename T>
 __global__ void __launch_bounds__(256) mask_blocks_kernel(const uint16_t* __restrict__ mask,
                                                           int64_t ldm, int64_t smb, int64_t sk,
                                                           int64_t nbq, int64_t nkb,
                                                           uint8_t* __restrict__ out) {
+  constexpr uint16_t kNegInf = __is_same(T, half_t) ? 0xFC00u : 0xFF80u;
+  constexpr uint32_t kNegInf2 = (static_cast<uint32_t>(kNegInf) << 16) | kNegInf;
+  __shared__ uint32_t votes[4];
   const int64_t kb = blockIdx.x, rb = blockIdx.y, mb = blockIdx.z;
   const int t = threadIdx.x;
   const uint16_t* M = mask + mb * smb + (rb * AQ) * ldm + kb * AK;
   const int64_t kn = sk - kb * AK;  // keys of this block (<= 64 counts)
   bool nonzero = false, finite = false;
-  // 128 rows x 8 chunks of 8 keys: 4 chunks per thread
+  // 128 rows x 8 chunks of 8 keys: 4 chunks per thread, all loads first
+  u32x4 w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = t + 256 * i, r = c >> 3, k8 = (c & 7) * 8;
+    if (k8 + 8 <= kn) w[i] = *reinterpret_cast<const u32x4*>(M + r * ldm + k8);
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int c = t + 256 * i, r = c >> 3, k8 = (c & 7) * 8;
     if (k8 + 8 <= kn) {
-      const u32x4 w = *reinterpret_cast<const u32x4*>(M + r * ldm + k8);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint16_t bits = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
-        const float x = Num<T>::to_f(__builtin_bit_cast(T, bits));
-        nonzero |= x != 0.f;
-        finite |= x != -INFINITY;
+      for (int e = 0; e < 4; ++e) {
+        nonzero |= (w[i][e] & 0x7fff7fffu) != 0u;
+        finite |= w[i][e] != kNegInf2;
       }
     } else {
       for (int e = 0; e < 8 && k8 + e < kn; ++e) {
-        const float x = Num<T>::to_f(reinterpret_cast<const T*>(M + r * ldm)[k8 + e]);
-        nonzero |= x != 0.f;
-        finite |= x != -INFINITY;
+        const uint16_t bits = M[r * ldm + k8 + e];
+        nonzero |= (bits & 0x7fffu) != 0u;
+        finite |= bits != kNegInf;
       }
     }
   }
-  const int anynz = __syncthreads_or(nonzero), anyfin = __syncthreads_or(finite);
-  if (t == 0) out[(mb * nbq + rb) * nkb + kb] = !anyfin ? MB_NEGINF : (anynz ? MB_MIXED : MB_ZERO);
+  const uint64_t bnz = __ballot(nonzero), bfin = __ballot(finite);
+  if (t % kWave == 0) votes[t / kWave] = (bnz != 0 ? 1u : 0u) | (bfin != 0 ? 2u : 0u);
+  __syncthreads();
+  if (t == 0) {
+    const uint32_t v = votes[0] | votes[1] | votes[2] | votes[3];
+    out[(mb * nbq + rb) * nkb + kb] = !(v & 2u) ? MB_NEGINF : ((v & 1u) ? MB_MIXED : MB_ZERO);
+  }
 }
 
 // One workgroup: the jobs (b * nbq + rb) counting-sorted by the number of
