@@ -259,8 +259,9 @@ int sph_bmm_f16(int64_t batch, int64_t m, int64_t n, int64_t k,
  * causal_q > 0 additionally drops keys j > (i % causal_q) + causal_off
  * for row i (query heads stacked along the rows keep their positions).
  * dtype in {F16, BF16} for Q, K, V, M, O; fp32 scores and accumulation;
- * head_dim must be 128, mq a multiple of 128, rows 16-byte aligned
- * (mask rows 8-byte aligned).  A row with no visible key yields NaN, as
+ * head_dim must be 128, mq a multiple of 128 (or at most 16: the decode
+ * path, sph_attention_decode), rows 16-byte aligned (mask rows 8-byte
+ * aligned; ldm 0 shares one mask row between all rows).  A row with no visible key yields NaN, as
  * softmax over all -inf does.
  * workspace (device memory, may be NULL) of at least
  * sph_attention_workspace_bytes(batch, mq, sk, stride_m) bytes lets a mask
@@ -276,8 +277,36 @@ int sph_attention_fwd(sph_dtype dtype, int64_t batch, int64_t mq, int64_t sk,
                       void* o, int64_t ldo, int64_t stride_o, void* workspace,
                       int64_t workspace_bytes, sph_stream_t stream);
 /* Bytes of mask-block classes sph_attention_fwd uses for this shape: one
- * per (mask batch, 128-row block, 64-key block); 0 for an empty shape. */
+ * per (mask batch, 128-row block, 64-key block); 0 for an empty shape.
+ * For mq <= 16 (the decode path below) the split workspace of
+ * sph_attention_decode_workspace_bytes instead. */
 int64_t sph_attention_workspace_bytes(int64_t batch, int64_t mq, int64_t sk, int64_t stride_m);
+
+/* Decode-step attention: the same O[b] = softmax(scale * Q[b] K[b]^T +
+ * M[b]) V[b] for at most 16 query rows per batch entry (a KV head's group
+ * of query heads at one position) over sk keys.  sph_attention_fwd routes
+ * mq <= 16 here.  V is given by element strides: key-major (v_dim_stride
+ * 1, row stride v_key_stride >= 128) or dim-major (v_key_stride 1,
+ * v_dim_stride >= sk), as a KV cache kept for the P V product stores it.
+ * The mask row stride ldm may be 0 (one mask row for every query row).
+ * causal_q / causal_off as for sph_attention_fwd.  With a workspace of
+ * sph_attention_decode_workspace_bytes(batch, mq, sk) bytes the keys are
+ * split over several workgroups per batch entry and merged by a second
+ * kernel; without one (NULL or too small) one workgroup per batch entry
+ * walks every key.  Replaces, for decode shapes, the same reference chain
+ * as sph_attention_fwd (spyre_torch_ops.cpp:297-377, Metadata.yaml:275-
+ * 277). */
+int sph_attention_decode(sph_dtype dtype, int64_t batch, int64_t mq, int64_t sk,
+                         int64_t head_dim, const void* q, int64_t ldq, int64_t stride_q,
+                         const void* k, int64_t ldk, int64_t stride_k, const void* v,
+                         int64_t v_key_stride, int64_t v_dim_stride, int64_t stride_v,
+                         const void* mask, int64_t ldm, int64_t stride_m, int64_t causal_q,
+                         int64_t causal_off, float scale, void* o, int64_t ldo,
+                         int64_t stride_o, void* workspace, int64_t workspace_bytes,
+                         sph_stream_t stream);
+/* Split workspace bytes of sph_attention_decode (0: no split for this
+ * shape, or mq > 16). */
+int64_t sph_attention_decode_workspace_bytes(int64_t batch, int64_t mq, int64_t sk);
 
 /* ------------------------------------------------------------------ */
 /* Generic strided pointwise engine                                     */

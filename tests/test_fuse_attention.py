@@ -79,7 +79,7 @@ def test_chain_is_fused_and_unchanged(variant):
 
 
 @pytest.mark.parametrize("case", ["head64", "rows_off_block", "fp32", "scores_escape",
-                                  "probs_escape", "mask_rowvec"])
+                                  "probs_escape", "mask_cols_off"])
 def test_unfit_chains_stay_unfused(case):
     d, mq, dtype = 128, 256, torch.float16
     if case == "head64":
@@ -101,8 +101,8 @@ def test_unfit_chains_stay_unfused(case):
             return o, p
         return o
 
-    if case == "mask_rowvec":
-        mask = torch.zeros(1, 128, dtype=dtype)  # [1, sk]: broadcast rows, not a kernel layout
+    if case == "mask_cols_off":
+        mask = torch.zeros(mq, 1, dtype=dtype)  # [mq, 1]: broadcast keys, not a kernel layout
     _, n = _run(fn, q, k, v, mask)
     assert n == 0
 
@@ -130,3 +130,28 @@ def test_spyre_wrapper_calls_fused_attention(fake_device):
     assert "torch.ops.spyre.attention.default(" in code
     assert "extern_kernels.bmm(" not in code
     assert not any("softmax" in k or "amax" in k for k in _kernels(code)), _kernels(code)
+
+
+@pytest.mark.parametrize("mask_kind", ["row", "row2d", "full", "none"])
+@pytest.mark.parametrize("mq", [4, 16, 256])
+def test_row_broadcast_masks_fuse_and_decode_shapes_do_not(mask_kind, mq):
+    # one mask row shared by every query row ([sk] or [1, sk], expanded as a
+    # view) is fused; decode shapes (a few rows per KV head) stay on the
+    # unfused chain, which measured faster there than the fused decode kernel
+    sk = 96
+    q, k, v = _qkv(3, mq, sk, seed=4)
+    row = torch.zeros(sk, dtype=torch.float16)
+    row[80:] = float("-inf")
+    mask = {"row": row, "row2d": row[None], "full": row.expand(mq, sk).contiguous(),
+            "none": None}[mask_kind]
+    if mask is None:
+        out, n = _run(lambda q, k, v: _chain(q, k, v), q, k, v)
+        ref = _chain(q, k, v)
+    else:
+        out, n = _run(lambda q, k, v, m: _chain(q, k, v, m), q, k, v, mask)
+        ref = _chain(q, k, v, mask)
+    assert n == (1 if mq % 128 == 0 else 0)
+    if n:
+        assert torch.equal(out, ref)  # the fused op runs the same chain on CPU
+    else:
+        torch.testing.assert_close(out, ref, rtol=1e-2, atol=1e-2)  # Inductor's own kernels

@@ -924,3 +924,100 @@ def test_stick_pack_unpack_bit_exact(shape, order, dtype):
     _sync()
     assert torch.equal(back.cpu().view(torch.uint8) if dtype != torch.int8 else back.cpu(),
                        x.view(torch.uint8) if dtype != torch.int8 else x)
+
+
+# ---------------------------------------------------------------------------
+# decode-step attention (sph_attention_decode; sph_attention_fwd routes
+# mq <= 16 there)
+# ---------------------------------------------------------------------------
+def _decode(q, k, v, scale, mask=None, ldm=None, v_dim_major=False, causal_q=0, causal_off=0,
+            workspace=True, dtype=torch.float16, via_fwd=False):
+    """q [b, mq, 128], k [b, sk, 128], v [b, sk, 128] (values; stored
+    dim-major [b, 128, sk] when v_dim_major) on the device."""
+    b, mq, d = q.shape
+    sk = k.shape[1]
+    o = torch.empty(b, mq, d, dtype=dtype, device=DEV)
+    if v_dim_major:
+        skp = (sk + 7) // 8 * 8  # dim-major rows padded to 16 bytes
+        vt = torch.zeros(b, d, skp, dtype=dtype, device=DEV)
+        vt[..., :sk] = v.transpose(1, 2)
+        vks, vds, sv = 1, skp, vt[0].numel()
+        vbuf = vt
+    else:
+        vks, vds, sv, vbuf = d, 1, v[0].numel(), v
+    if ldm is None:
+        ldm = mask.stride(-2) if mask is not None else 0
+    sm = mask.stride(0) if mask is not None and mask.dim() == 3 else 0
+    nws = _capi.lib().sph_attention_decode_workspace_bytes(b, mq, sk)
+    ws = torch.full((max(nws, 1),), 0xAB, dtype=torch.uint8, device=DEV) if workspace else None
+    if via_fwd:
+        assert not v_dim_major
+        _capi.call("sph_attention_fwd", DT[dtype], b, mq, sk, d, _p(q), d, q[0].numel(), _p(k), d,
+                   k[0].numel(), _p(vbuf), d, sv, _p(mask), ldm, sm, causal_q, causal_off, scale,
+                   _p(o), d, o[0].numel(), _p(ws), nws if workspace else 0, _stream())
+    else:
+        _capi.call("sph_attention_decode", DT[dtype], b, mq, sk, d, _p(q), d, q[0].numel(), _p(k),
+                   d, k[0].numel(), _p(vbuf), vks, vds, sv, _p(mask), ldm, sm, causal_q,
+                   causal_off, scale, _p(o), d, o[0].numel(), _p(ws), nws if workspace else 0,
+                   _stream())
+    _sync()
+    return o
+
+
+@pytest.mark.parametrize("b,mq,sk", [(32, 4, 1152), (1, 1, 1), (3, 16, 63), (2, 7, 130),
+                                     (4, 4, 64), (64, 8, 2000)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_attention_decode_vs_oracle(b, mq, sk, dtype):
+    _log(f"decode attention b={b} mq={mq} sk={sk} {dtype}")
+    q = randn((b, mq, 128), k=61, dtype=dtype)
+    k = randn((b, sk, 128), k=62, dtype=dtype)
+    v = randn((b, sk, 128), k=63, dtype=dtype)
+    # one mask row for every query row (a decode step's key positions):
+    # the last 5 keys dropped (all keys when sk <= 5 would drop every key)
+    row = torch.zeros(sk, dtype=dtype)
+    if sk > 5:
+        row[sk - 5:] = float("-inf")
+    scale = 1 / math.sqrt(128)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    want = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), scale,
+                       mask=row.float().numpy())
+    tol = dict(rtol=1e-2, atol=1e-2) if dtype == torch.float16 else dict(rtol=2e-2, atol=2e-2)
+    outs = []
+    for vdm in (False, True):
+        for ws in (True, False):
+            got = _decode(qd, kd, vd, scale, mask=row.to(DEV), ldm=0, v_dim_major=vdm,
+                          workspace=ws, dtype=dtype)
+            assert_close_fp(got, want, out_dtype=dtype, what=f"decode vdm={vdm} ws={ws}", **tol)
+            outs.append(got)
+    # a full [mq, sk] mask, and the prefill entry routing to the same path
+    full = row.expand(mq, sk).contiguous().to(DEV)
+    got = _decode(qd, kd, vd, scale, mask=full, dtype=dtype, via_fwd=True)
+    torch.testing.assert_close(got, outs[0], rtol=0, atol=0)
+    # no mask
+    got = _decode(qd, kd, vd, scale, dtype=dtype)
+    want = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), scale)
+    assert_close_fp(got, want, out_dtype=dtype, what="decode no mask", **tol)
+
+
+def test_attention_decode_causal_and_empty_rows():
+    _log("decode attention causal / all-masked rows")
+    b, mq, sk = 3, 6, 300
+    q = randn((b, mq, 128), k=64)
+    k = randn((b, sk, 128), k=65)
+    v = randn((b, sk, 128), k=66)
+    scale = 0.1
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    # causal positions: row r sees keys <= r % 3 + 200
+    got = _decode(qd, kd, vd, scale, causal_q=3, causal_off=200)
+    want = O.attention(q.numpy(), k.numpy(), v.numpy(), scale, causal_q_len=3, causal_offset=200)
+    assert_close_fp(got, want, what="decode causal")
+    # per-row masks with one row masked everywhere: that row is NaN, the
+    # others are unaffected
+    m = torch.zeros(b, mq, sk, dtype=torch.float16)
+    m[:, 2, :] = float("-inf")
+    m[:, 4, 100:] = float("-inf")
+    got = _decode(qd, kd, vd, scale, mask=m.to(DEV))
+    want = O.attention(q.numpy(), k.numpy(), v.numpy(), scale, mask=m.float().numpy())
+    assert torch.isnan(got[:, 2].cpu().float()).all()
+    keep = [0, 1, 3, 4, 5]
+    assert_close_fp(got[:, keep], want[:, keep], what="decode masked rows")

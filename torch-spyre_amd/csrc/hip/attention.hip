@@ -568,6 +568,7 @@ int64_t mask_batches(int64_t batch, int64_t stride_m) { return (batch == 1 || st
 extern "C" int64_t sph_attention_workspace_bytes(int64_t batch, int64_t mq, int64_t sk,
                                                  int64_t stride_m) {
   if (batch <= 0 || mq <= 0 || sk <= 0) return 0;
+  if (mq <= 16 && mq % AQ != 0) return sph_attention_decode_workspace_bytes(batch, mq, sk);
   // mask block classes, then (256-byte aligned) the job order
   const int64_t cls = mask_batches(batch, stride_m) * ((mq + AQ - 1) / AQ) * ((sk + AK - 1) / AK);
   return (cls + 255) / 256 * 256 + 4 * batch * ((mq + AQ - 1) / AQ);
@@ -586,7 +587,12 @@ extern "C" int sph_attention_fwd(sph_dtype dtype, int64_t batch, int64_t mq, int
   SPH_REQUIRE(batch >= 0 && mq >= 0 && sk >= 0, SPH_ERR_INVALID_ARG, "attention: negative size");
   if (batch == 0 || mq == 0) return SPH_OK;
   SPH_REQUIRE(sk > 0, SPH_ERR_INVALID_ARG, "attention: no keys");
-  SPH_REQUIRE(mq % AQ == 0, SPH_ERR_UNSUPPORTED, "attention: query rows must be a multiple of 128");
+  if (mq <= 16 && mq % AQ != 0)  // a decode step's rows
+    return sph_attention_decode(dtype, batch, mq, sk, head_dim, q, ldq, stride_q, k, ldk, stride_k,
+                                v, ldv, 1, stride_v, mask, ldm, stride_m, causal_q, causal_off,
+                                scale, o, ldo, stride_o, workspace, workspace_bytes, stream);
+  SPH_REQUIRE(mq % AQ == 0, SPH_ERR_UNSUPPORTED,
+              "attention: query rows must be a multiple of 128 (or at most 16)");
   SPH_REQUIRE(batch * (mq / AQ) < (1LL << 31), SPH_ERR_TOO_LARGE, "attention: grid too large");
   SPH_REQUIRE(causal_q >= 0, SPH_ERR_INVALID_ARG, "attention: causal_q < 0");
   SPH_REQUIRE(scale > 0.f && scale < INFINITY, SPH_ERR_INVALID_ARG,
@@ -600,9 +606,9 @@ extern "C" int sph_attention_fwd(sph_dtype dtype, int64_t batch, int64_t mq, int
                   ldv % 8 == 0 && ldo % 8 == 0 && (batch == 1 || (stride_q % 8 == 0 &&
                   stride_k % 8 == 0 && stride_v % 8 == 0 && stride_o % 8 == 0)),
               SPH_ERR_INVALID_ARG, "attention: rows must be 16-byte aligned");
-  SPH_REQUIRE(mask == nullptr || (ldm >= sk && ldm % 4 == 0 && (reinterpret_cast<uintptr_t>(mask) & 7u) == 0 &&
+  SPH_REQUIRE(mask == nullptr || ((ldm == 0 || ldm >= sk) && ldm % 4 == 0 && (reinterpret_cast<uintptr_t>(mask) & 7u) == 0 &&
                                   (batch == 1 || stride_m % 4 == 0)),
-              SPH_ERR_INVALID_ARG, "attention: mask rows must be 8-byte aligned, ldm >= sk");
+              SPH_ERR_INVALID_ARG, "attention: mask rows must be 8-byte aligned, ldm 0 or >= sk");
   // DMA offsets within one key block are 32-bit.
   SPH_REQUIRE(AK * ldk * 2 < (1LL << 31) && AK * ldv * 2 < (1LL << 31), SPH_ERR_TOO_LARGE,
               "attention: K/V rows too long for 32-bit block offsets");

@@ -6,8 +6,9 @@ separate ops (spyre__bmm_default, codegen/inputs/spyre_torch_ops.cpp:297-377;
 add and _softmax, codegen/inputs/Metadata.yaml:275-277) and forbids fusion
 in its scheduler (torch_spyre/_inductor/choices.py:58-83).  Here the chain
 is replaced, on spyre graphs only, when the fused kernel takes its shapes:
-fp16 / bf16, head dim 128, query rows a multiple of 128 and a mask (if
-any) of the same dtype shaped [mq, sk] or [B or 1, mq, sk].  The fused op
+fp16 / bf16, head dim 128, query rows a multiple of 128, and a mask (if
+any) of the same dtype shaped [mq, sk] or [B or 1, mq, sk], or one mask row
+[sk] / [1, sk] broadcast over the rows (expanded to [mq, sk] as a view).  The fused op
 computes the same function (fp32 scores and softmax, probabilities rounded
 to the input dtype before the second product).
 
@@ -168,17 +169,23 @@ def _finish(bmm2, bmm1, chain, v, mask, scale) -> Optional[tuple]:
     sk = kv.shape[1]
     if not all(isinstance(x, int) for x in (B, mq, d, sk)):
         return None  # dynamic shapes stay unfused
+    # Decode shapes (a few rows per KV head) stay on the unfused chain: the
+    # fused decode kernel (sph_attention_decode) measured slower than it in
+    # the c5 decode step (4.77 against 4.65 ms per step).
     if d != HEAD_DIM or mq % ROW_BLOCK or tuple(kv.shape) != (B, sk, d) or \
             tuple(vv.shape) != (B, sk, d):
         return None
+    expand = None
     if mask is not None:
         mv = _val(mask)
         if mv is None or mv.dtype != dt:
             return None
         shp = tuple(mv.shape)
-        if not (shp == (mq, sk) or (len(shp) == 3 and shp[0] in (1, B) and shp[1:] == (mq, sk))):
+        if shp in ((sk,), (1, sk)):
+            expand = [mq, sk]
+        elif not (shp == (mq, sk) or (len(shp) == 3 and shp[0] in (1, B) and shp[1:] == (mq, sk))):
             return None
-    return q, k, v, mask, scale, chain
+    return q, k, v, mask, scale, chain, expand
 
 
 def fuse_attention(gm: torch.fx.GraphModule) -> int:
@@ -191,8 +198,11 @@ def fuse_attention(gm: torch.fx.GraphModule) -> int:
         m = _match(node)
         if m is None:
             continue
-        q, k, v, mask, scale, chain = m
+        q, k, v, mask, scale, chain, expand = m
         with g.inserting_before(node):
+            if expand is not None:  # one mask row for every query row
+                mask = g.call_function(aten.expand.default, (mask, expand))
+                mask.meta["val"] = _val(m[3]).expand(expand)
             new = g.call_function(torch.ops.spyre.attention.default, (q, k, v, mask, scale))
         new.meta.update(node.meta)
         node.replace_all_uses_with(new)
