@@ -95,16 +95,93 @@ def graph_us(launch, reps, per_graph=20):
     return start.elapsed_time(end) * 1e3 / (reps * per_graph)
 
 
-def _traffic_for(kernel_key):
-    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, calibrated against a copy kernel), committed under
-    profiles/traffic.json; None when that measurement is absent."""
-    path = os.path.join(REPO, "profiles", "traffic.json")
+# Symbols of the kernels bench.py times, by the key of their figure.  A
+# traffic measurement in profiles/traffic.json counts only for the kernel it
+# was taken of: entries are keyed by symbol, so a changed kernel reports no
+# traffic until it is measured again.
+TIMED_SYMBOLS = {
+    "gemm": "_ZN3sph12_GLOBAL__N_114gemm_dl_kernelIDF16_Lb0ELi256ELb0EEEvNS0_8GemmArgsE",
+    "bmm": "_ZN3sph12_GLOBAL__N_118gemm_shortk_kernelIDF16_Lb0ELi2EEEvNS0_8GemmArgsE",
+    "softmax": "_ZN3sph12_GLOBAL__N_112softmax_fullIDF16_DF16_Li256ELi2EEEvPKT_lPT0_llfill",
+    "rmsnorm": "_ZN3sph12_GLOBAL__N_19norm_regsIDF16_DF16_Li256ELi2ELb1ELb0EEEvPKT_S4_PKT0_S7_PS2_"
+               "S8_PfS9_llf",
+    "layernorm": "_ZN3sph12_GLOBAL__N_19norm_regsIDF16_DF16_Li256ELi2ELb1ELb1EEEvPKT_S4_PKT0_S7_"
+                 "PS2_S8_PfS9_llf",
+    "gelu_rowsum": "_ZN3sph12_GLOBAL__N_116gelu_rowsum_rowsIDF16_Li512ELi1ELi2EEEvPKT_S4_S4_ffPS2_"
+                   "S5_l",
+}
+# The calibration kernel (bench.py --kernel copy: 512 MiB read, 512 MiB written).
+COPY_SYMBOL = "_ZN3sph12_GLOBAL__N_16pw_vecIDF16_EEvNS0_6PwArgsE"
+COPY_BYTES = 512 * 1024 * 1024
+# Algorithmic bytes per launch of each timed kernel (operands read once,
+# results written once).
+ALGORITHMIC_BYTES = {
+    "gemm": 3 * 4096 * 4096 * 2,
+    "bmm": (2 * 32 * 2048 * 128 + 32 * 2048 * 2048) * 2,
+    "softmax": 2 * 512 * 4096 * 2,
+    "rmsnorm": 4 * 8192 * 4096 * 2 + 4096 * 2,
+    "layernorm": 4 * 8192 * 4096 * 2 + 2 * 4096 * 2,
+    "gelu_rowsum": 2 * 8192 * 4096 * 2 + 2 * 4096 * 2 + 8192 * 2,
+}
+TRAFFIC_JSON = os.path.join(REPO, "profiles", "traffic.json")
+
+
+def _traffic_for(key):
+    """HBM bytes per launch of the kernel timed under `key`, measured by
+    rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, each scaled by what the counter
+    reads for a plain copy of known size), committed in profiles/traffic.json
+    under the kernel's symbol; None when that kernel has not been measured."""
     try:
-        with open(path) as f:
-            return json.load(f).get(kernel_key, {}).get("bytes_per_launch")
+        with open(TRAFFIC_JSON) as f:
+            entry = json.load(f).get("kernels", {}).get(TIMED_SYMBOLS[key])
     except (OSError, ValueError):
         return None
+    return None if entry is None else entry.get("bytes_per_launch")
+
+
+def summarize_traffic(root, algorithmic):
+    """Reads rocprofv3 --pmc outputs under `root` (directories pmc_<part>_
+    <COUNTER>/ holding p_counter_collection.csv, one counter per pass) and
+    writes profiles/traffic.json: per timed kernel symbol the median
+    FETCH_SIZE / WRITE_SIZE (KiB per dispatch), both scaled by the copy
+    kernel's calibration."""
+    import csv
+    import glob
+    import statistics
+
+    vals = {}
+    for d in glob.glob(os.path.join(root, "pmc_*_*_SIZE")):
+        counter = "FETCH_SIZE" if d.endswith("FETCH_SIZE") else "WRITE_SIZE"
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(path) as f:
+                for row in csv.DictReader(f):
+                    vals.setdefault((row["Kernel_Name"], counter), []).append(
+                        float(row["Counter_Value"]))
+
+    def med(sym, counter):
+        v = vals.get((sym, counter))
+        return statistics.median(v) if v else None
+
+    cf, cw = med(COPY_SYMBOL, "FETCH_SIZE"), med(COPY_SYMBOL, "WRITE_SIZE")
+    if not cf or not cw:
+        raise SystemExit(f"no copy calibration ({COPY_SYMBOL}) under {root}")
+    ff, fw = COPY_BYTES / (cf * 1024), COPY_BYTES / (cw * 1024)
+    out = {"copy_calibration": {"kernel": COPY_SYMBOL, "bytes_read": COPY_BYTES,
+                                "bytes_written": COPY_BYTES, "fetch_kib_raw": cf,
+                                "write_kib_raw": cw, "fetch_factor": round(ff, 5),
+                                "write_factor": round(fw, 5)},
+           "kernels": {}}
+    for key, sym in TIMED_SYMBOLS.items():
+        f, w = med(sym, "FETCH_SIZE"), med(sym, "WRITE_SIZE")
+        if f is None or w is None:
+            continue
+        out["kernels"][sym] = {"key": key, "fetch_kib_raw": f, "write_kib_raw": w,
+                               "bytes_per_launch": int(f * 1024 * ff + w * 1024 * fw),
+                               "algorithmic_bytes": algorithmic.get(key)}
+    with open(TRAFFIC_JSON, "w") as fh:
+        json.dump(out, fh, indent=1)
+        fh.write("\n")
+    return out
 
 
 def bench_gemm(steps, warmup, stream, capi):
@@ -130,6 +207,13 @@ def bench_gemm(steps, warmup, stream, capi):
 
 def bench_extra(steps, warmup, stream, capi):
     """Secondary kernels: bytes / FLOPs per launch and roofline fractions."""
+    out = bench_rows(steps, warmup, stream, capi)
+    out.update(bench_bmm(steps, warmup, stream, capi))
+    return out
+
+
+def bench_rows(steps, warmup, stream, capi):
+    """c1 softmax and the c3 row kernels through the C-ABI."""
     import torch
 
     s = stream.cuda_stream
@@ -196,8 +280,6 @@ def bench_extra(steps, warmup, stream, capi):
               lambda: lib.sph_gelu_affine_rowsum_f16(x.data_ptr(), w.data_ptr(), bb.data_ptr(),
                                                      yy.data_ptr(), rs.data_ptr(), R, C, s))
     del x, r, yy, h
-
-    out.update(bench_bmm(steps, warmup, stream, capi))
     return out
 
 
@@ -537,98 +619,169 @@ def bench_eager_mm(steps, warmup):
     return {"ms_per_call": round(ms, 4), "TFLOP/s": round(2 * 4096 ** 3 / (ms * 1e-3) / 1e12, 1)}
 
 
-def cpu_per_config():
-    """The CPU side of every config, timed on this host in the same run:
-    the oracle's numpy restatements for c1 (softmax) and c3 (norms, GELU
-    chain) on the full or a row-sliced input, and the decoder's own torch
-    code run eagerly on CPU tensors (the reference's compare-with-CPU path)
-    for c4 and c5 on a bounded sample.  Figures are in the unit of the
-    config, with the sample stated; ~20 s in total."""
-    import numpy as np
+def _cpu_setup():
+    """Threads = the cores this process may run on (BASELINE's CPU protocol);
+    returns (threads, CPU model name)."""
     import torch
 
-    from oracle import ops as O
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return torch.get_num_threads(), model
+
+
+def _median_s(fn, reps=10, warmup=3):
+    """Median wall time of `reps` calls after `warmup` calls, and the times."""
+    import statistics
+
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), ts
+
+
+def cpu_per_config():
+    """The reference's CPU path for every config, timed on this host in the
+    same run: the config's function run eagerly by torch on CPU tensors of
+    the same shapes and dtype (fp16), as the reference's tests do
+    (compare_with_cpu, tests/_inductor/utils_inductor.py:186-198).  c1-c3:
+    full inputs, median of 10 after 3 warmups; c4: the full layer at seq
+    2048, median of 3 after 1; c5: a 2-layer slice of the prefill at the
+    full 4 x 1024 batch and decode steps of a 4-layer slice, each scaled to
+    40 layers (labelled as extrapolated); ~1 minute in total."""
+    import torch
+    import torch.nn.functional as F
+
     from torch_spyre.examples import decoder as D
 
-    def timed(fn, min_s=1.0, min_reps=3):
-        fn()
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            fn()
-            reps += 1
-            el = time.perf_counter() - t0
-            if el >= min_s and reps >= min_reps:
-                return el / reps, reps
+    threads, model = _cpu_setup()
+    out = {"threads": threads, "cpu": model}
 
-    out = {"threads": torch.get_num_threads()}
-    g = np.random.default_rng(SEED)
-    x = (g.standard_normal((512, 4096), dtype=np.float32) * 4).astype(np.float16)
-    t, n = timed(lambda: O.softmax(x))
-    out["c1_softmax_512x4096"] = {"GB/s": round(2 * x.size * 2 / t / 1e9, 2), "reps": n,
-                                  "sample": "full input, oracle.ops.softmax (numpy)"}
-    rows, C = 1024, 4096
-    xr = g.standard_normal((rows, C), dtype=np.float32).astype(np.float16)
-    rr = g.standard_normal((rows, C), dtype=np.float32).astype(np.float16)
-    w = (1 + 0.02 * g.standard_normal(C, dtype=np.float32)).astype(np.float16)
-    bb = (0.02 * g.standard_normal(C, dtype=np.float32)).astype(np.float16)
-    nb = 4 * rows * C * 2
-    t, n = timed(lambda: O.rmsnorm(xr, w, residual=rr))
-    out["c3_add_rmsnorm"] = {"GB/s": round(nb / t / 1e9, 2), "reps": n,
-                             "sample": f"rows 0..{rows} of 8192, oracle.ops.rmsnorm"}
-    t, n = timed(lambda: O.layernorm(xr, w, bb, residual=rr))
-    out["c3_add_layernorm"] = {"GB/s": round(nb / t / 1e9, 2), "reps": n,
-                               "sample": f"rows 0..{rows} of 8192, oracle.ops.layernorm"}
-    t, n = timed(lambda: O.gelu_affine_rowsum(xr, w, bb))
-    out["c3_gelu_rowsum"] = {"GB/s": round(2 * rows * C * 2 / t / 1e9, 2), "reps": n,
-                             "sample": f"rows 0..{rows} of 8192, oracle.ops.gelu_affine_rowsum"}
-    # c4 / c5: the decoder code itself on CPU tensors (fp32: torch's fp16
-    # CPU matmul is far slower, so this is the faster CPU figure)
+    def hbm(name, nbytes, fn, sample):
+        t, _ = _median_s(fn)
+        out[name] = {"GB/s": round(nbytes / t / 1e9, 2), "ms": round(t * 1e3, 3),
+                     "sample": sample}
+
+    R, C = 512, 4096
+    x = (torch.randn(R, C, generator=_gen(0)) * 4).half()
+    hbm("c1_softmax_512x4096", 2 * R * C * 2, lambda: torch.softmax(x, dim=-1),
+        "torch.softmax(x, -1), fp16 CPU, full input")
+    R, C = 8192, 4096
+    x = torch.randn(R, C, generator=_gen(0)).half()
+    r = torch.randn(R, C, generator=_gen(1)).half()
+    w = (torch.randn(C, generator=_gen(2)) * 0.02 + 1).half()
+    b = (torch.randn(C, generator=_gen(3)) * 0.02).half()
+    hbm("c3_add_rmsnorm", 4 * R * C * 2 + C * 2,
+        lambda: (lambda h: (h, torch.rms_norm(h, [C], w, 1e-5)))(x + r),
+        "h = x + res; rms_norm(h) * w, fp16 CPU, full input")
+    hbm("c3_add_layernorm", 4 * R * C * 2 + 2 * C * 2,
+        lambda: (lambda h: (h, F.layer_norm(h, [C], w, b, 1e-5)))(x + r),
+        "h = x + res; layer_norm(h, w, b), fp16 CPU, full input")
+    hbm("c3_gelu_rowsum", 2 * R * C * 2 + 2 * C * 2 + R * 2,
+        lambda: (lambda y: (y, y.sum(-1)))(F.gelu(x * w + b)),
+        "y = gelu(x * s + b); y.sum(-1), fp16 CPU, full input")
+    del x, r
+    A = (torch.rand(32, 2048, 128, generator=_gen(0)) * 2 - 1).half()
+    Bm = (torch.rand(32, 128, 2048, generator=_gen(1)) * 2 - 1).half()
+    t, _ = _median_s(lambda: torch.bmm(A, Bm))
+    out["c2_bmm_32x2048x2048x128"] = {
+        "TFLOP/s": round(2 * 32 * 2048 * 2048 * 128 / t / 1e12, 4), "ms": round(t * 1e3, 2),
+        "sample": "torch.bmm, fp16 CPU, full input"}
+    # c4: embedding + one layer at seq 2048, fp16
     cfg = D.C4
-    S = 256
-    params = D.init_params(cfg, "cpu", dtype=torch.float32, pool_elems=1 << 24)
-    cos, sin = D.rope_tables(cfg, S, "cpu", torch.float32)
-    mask = D.causal_mask(cfg, S, "cpu", torch.float32)
-    tok = torch.randint(0, cfg.vocab, (1, S), generator=torch.Generator().manual_seed(SEED))
+    S = 2048
+    params = D.init_params(cfg, "cpu", pool_elems=1 << 24)
+    cos, sin = D.rope_tables(cfg, S, "cpu")
+    mask = D.causal_mask(cfg, S, "cpu")
+    tok = torch.randint(0, cfg.vocab, (1, S), generator=_gen(0))
     with torch.no_grad():
-        t, n = timed(lambda: D.block_forward(tok, params, cos, sin, mask, cfg), min_s=3.0)
-    out["c4_layer_prefill"] = {"tok/s": round(S / t, 1), "reps": n,
-                               "sample": f"c4 layer (embedding + 1 layer) at seq {S} of 2048, "
-                                         "torch eager fp32 on CPU (decoder.block_forward)"}
-    out["c5_prefill_estimate"] = {
-        "tok/s": round(S / t / 40, 1),
-        "sample": "the c4 layer rate divided by c5's 40 layers (LM head not included)"}
+        t, _ = _median_s(lambda: D.block_forward(tok, params, cos, sin, mask, cfg), reps=3,
+                         warmup=1)
+    out["c4_layer_prefill"] = {"tok/s": round(S / t, 1), "ms": round(t * 1e3, 1),
+                               "sample": "decoder.block_forward (embedding + 1 layer), seq "
+                                         "2048, fp16 CPU, median of 3"}
+    # c5: layer slices of the model at its batch and lengths, scaled to 40
+    B, S, T = 4, 1024, 128
+    sl = D.DecoderConfig(n_layers=2)
+    params = D.init_params(sl, "cpu", pool_elems=1 << 24)
+    cos, sin = D.rope_tables(sl, S + T, "cpu")
+    mask = D.causal_mask(sl, S, "cpu")
+    prompt = torch.randint(0, sl.vocab, (B, S), generator=_gen(1))
+    cache = D.new_cache(sl, B, S + T, "cpu")
+    with torch.no_grad():
+        t0 = time.perf_counter()
+        logits = D.prefill(prompt, params, cos, sin, mask, cache, sl)
+        t_pre = time.perf_counter() - t0
+        h = torch.randn(B, sl.hidden, generator=_gen(2)).half()
+        t_head, _ = _median_s(lambda: D.lm_logits(h, params, sl), reps=3, warmup=1)
+        feed = logits.argmax(-1)
+        steps = 4
+        t0 = time.perf_counter()
+        for i in range(steps):
+            feed = D.decode_step(feed, S + i, params, cos, sin, cache, sl).argmax(-1)
+        t_dec = (time.perf_counter() - t0) / steps
+    per_layer_pre = (t_pre - t_head) / sl.n_layers
+    per_layer_dec = (t_dec - t_head) / sl.n_layers
+    pre40 = per_layer_pre * 40 + t_head
+    dec40 = per_layer_dec * 40 + t_head
+    out["c5_prefill_extrapolated"] = {
+        "tok/s": round(B * S / pre40, 1), "s": round(pre40, 2),
+        "sample": "decoder.prefill of a 2-layer slice at batch 4 x 1024, fp16 CPU, one run; "
+                  "per-layer time x 40 + the LM head (extrapolated)"}
+    out["c5_decode_extrapolated"] = {
+        "tok/s": round(B / dec40, 2), "ms_per_step": round(dec40 * 1e3, 1),
+        "sample": f"decoder.decode_step of the 2-layer slice, {steps} steps after its prefill, "
+                  "fp16 CPU; per-layer time x 40 + the LM head (extrapolated)"}
     return out
 
 
 def cpu_baseline_gemm(a, b):
-    """Oracle GEMM (numpy fp32) on a bounded row slice of the same problem,
-    timed on this host's cores."""
-    import numpy as np
+    """BASELINE's CPU baseline of the headline: the reference's CPU path
+    fn(*cpu_args) = torch.mm eager on the same fp16 tensors on this host's
+    CPU (what compare_with_cpu runs, tests/_inductor/utils_inductor.py:190),
+    full 4096^3 input, median of 10 after 3 warmups."""
+    import torch
 
+    threads, model = _cpu_setup()
+    ac, bc = a.cpu(), b.cpu()
+    t, ts = _median_s(lambda: torch.mm(ac, bc))
+    flop = 2.0 * ac.shape[0] * ac.shape[1] * bc.shape[1]
+    return {"value": round(flop / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "reference",
+            "sample": f"torch.mm eager on the same fp16 A, B on the CPU ({model}), full "
+                      f"4096^3, median of 10 after 3 warmups ({min(ts) * 1e3:.0f}-"
+                      f"{max(ts) * 1e3:.0f} ms)"}
+
+
+def cpu_oracle_gemm(a, b, seconds=3.0):
+    """The oracle's numpy fp32 GEMM (BLAS) on 512 rows of the same problem:
+    a second CPU figure, the restatement the parity tests check against."""
     from oracle import ops as O
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        cores = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
-    except Exception:
-        cores = os.cpu_count() or 1
     rows = 512
     an = a[:rows].float().cpu().numpy()
     bn = b.float().cpu().numpy()
-    O.gemm(an[:64], bn)  # warm the BLAS pool
+    O.gemm(an[:64], bn)
     reps, t0 = 0, time.perf_counter()
     while True:
         O.gemm(an, bn)
         reps += 1
         el = time.perf_counter() - t0
-        if el > 10.0:
+        if el > seconds:
             break
-    flop = 2.0 * rows * b.shape[0] * b.shape[1] * reps
-    return {"value": round(flop / el / 1e12, 4), "unit": "TFLOP/s", "cores": int(cores),
-            "kind": "port",
-            "sample": f"oracle.ops.gemm (numpy fp32 BLAS) on rows 0..{rows} of the 4096^3 "
-                      f"problem, {reps} reps, {el:.1f} s"}
+    return {"TFLOP/s": round(2.0 * rows * b.shape[0] * b.shape[1] * reps / el / 1e12, 4),
+            "sample": f"oracle.ops.gemm (numpy fp32) on rows 0..{rows}, {reps} reps"}
 
 
 def main(argv=None):
@@ -645,12 +798,18 @@ def main(argv=None):
     ap.add_argument("--c5-layers", type=int, default=40)
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--kernel", choices=["all", "gemm", "copy", "decoder", "bmm", "h2d",
-                                         "attention", "spyre"],
+                                         "attention", "spyre", "rows"],
                     default="all",
-                    help="gemm / copy / decoder / bmm / h2d / attention / spyre (the eager and "
-                         "compiled paths on spyre tensors): run only that part "
-                         "(for rocprofv3 passes)")
+                    help="gemm / copy / decoder / bmm / h2d / attention / rows (c1 softmax and "
+                         "the c3 row kernels) / spyre (the eager and compiled paths on spyre "
+                         "tensors): run only that part (for rocprofv3 passes)")
+    ap.add_argument("--traffic-from", metavar="DIR",
+                    help="summarise rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes under DIR "
+                         "(pmc_<part>_<COUNTER>/) into profiles/traffic.json and exit")
     args = ap.parse_args(argv)
+    if args.traffic_from:
+        print(json.dumps(summarize_traffic(args.traffic_from, ALGORITHMIC_BYTES), indent=1))
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; runs on more than one GPU are not "
               "part of it (see DESIGN.md, 'How the path would shard').", file=sys.stderr)
@@ -669,6 +828,9 @@ def main(argv=None):
         return 0
     if args.kernel == "bmm":
         print(json.dumps({"kernel": "bmm", **bench_bmm(args.steps, args.warmup, stream, _capi)}))
+        return 0
+    if args.kernel == "rows":
+        print(json.dumps({"kernel": "rows", **bench_rows(args.steps, args.warmup, stream, _capi)}))
         return 0
     if args.kernel == "attention":
         print(json.dumps({"kernel": "attention",
@@ -707,6 +869,7 @@ def main(argv=None):
     if not args.no_cpu:
         _log("cpu baseline")
         cpu = cpu_baseline_gemm(g["a"], g["b"])
+        extra["cpu_oracle_gemm_numpy"] = cpu_oracle_gemm(g["a"], g["b"])
         if not args.no_extra:
             _log("cpu side of every config")
             extra["cpu_per_config"] = cpu_per_config()

@@ -440,12 +440,15 @@ int sph_reduce(int op, const sph_operand* in, const sph_operand* out,
 /* Row gather (embedding / index_select on dim 0):
  * out[i, :] = table[idx[i], :] for i < n_idx; rows of `row_elems` elements
  * of `elem_bytes` bytes; idx is int64 (idx_is_i64 = 1) or int32.
- * An index outside [0, num_rows) yields a zero row (no fault); callers that
- * need torch's error check the indices themselves.
+ * An index outside [0, num_rows) yields a zero row (no fault) and, when
+ * `oob_flag` is not null, a store of 1 to *oob_flag (a device-accessible
+ * int32 the caller clears and reads after the stream has completed; torch
+ * raises IndexError for such an index, and the ATen backend raises it at its
+ * next synchronisation).
  * Replaces: generated embedding (Metadata.yaml:105-115). */
 int sph_gather_rows(const void* table, int64_t num_rows, int64_t row_elems,
                     int elem_bytes, const void* idx, int idx_is_i64,
-                    int64_t n_idx, void* out, sph_stream_t stream);
+                    int64_t n_idx, void* out, int32_t* oob_flag, sph_stream_t stream);
 
 /* tril/triu on the last two dims of a contiguous [batch, rows, cols]
  * tensor: keep element (r, c) when c - r <= diagonal (lower) or

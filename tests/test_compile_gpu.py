@@ -141,3 +141,29 @@ def test_pointwise_chain_and_broadcast_compiled():
     torch.testing.assert_close(f(x.to(DEV), y.to(DEV)).cpu(),
                                (torch.sigmoid(x * 2 + y).relu() - 1) * torch.tanh(x),
                                rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("sk", [77, 130])
+def test_fused_masked_attention_any_key_count(sk):
+    # a mask whose rows are not a multiple of 8 keys long goes through the
+    # fused kernel (the op pads its rows) and matches the oracle
+    _log(f"compiled fused masked attention sk={sk}")
+    from torch_spyre._inductor import customops  # noqa: F401  (torch.ops.spyre.attention)
+
+    b, mq = 2, 256
+    q, k, v = randn((b, mq, 128), k=70), randn((b, sk, 128), k=71), randn((b, sk, 128), k=72)
+    mask = torch.full((mq, sk), float("-inf")).triu(1 + sk - mq if sk > mq else 1)
+    mask[:, 0] = 0.0  # every row keeps a key
+    mask = mask.half()
+    scale = 1.0 / 128 ** 0.5
+
+    def fn(q, k, v, m):
+        s = torch.bmm(q, k.transpose(1, 2)) * scale + m
+        return torch.bmm(torch.softmax(s, dim=-1), v)
+
+    out = torch.compile(fn)(q.to(DEV), k.to(DEV), v.to(DEV), mask.to(DEV))
+    want = O.attention(q.numpy(), k.numpy(), v.numpy(), scale, mask.numpy())
+    assert_close_fp(out, want, what=f"fused masked attention sk={sk}")
+    # and the op itself, called directly with the unpadded mask
+    direct = torch.ops.spyre.attention(q.to(DEV), k.to(DEV), v.to(DEV), mask.to(DEV), scale)
+    assert_close_fp(direct, want, what=f"spyre.attention sk={sk}")

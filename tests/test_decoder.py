@@ -143,3 +143,69 @@ def test_fp16_rounding_model_tracks_fp32():
     a = OD.block(tok, p, cfg, act=np.float16)
     b = OD.block(tok, p, cfg, act=None)
     np.testing.assert_allclose(a, b, rtol=1e-2, atol=1e-2)
+
+
+# A shape at which every fused branch of the oracle's compiled-program mode
+# is taken: head dim 128 with the stacked query rows of a KV head a multiple
+# of 128 (fused prefill attention), rows % 256 == 0 with intermediate % 128
+# and hidden % 64 (SwiGLU GEMM), and at most 8 rows in decode (SwiGLU weight
+# stream).
+FUSED = D.DecoderConfig(hidden=256, n_heads=2, n_kv_heads=1, head_dim=128, intermediate=256,
+                        vocab=64, n_layers=2)
+
+
+def _f32(tp):
+    return {"embed": tp["embed"].float(), "final_norm": tp["final_norm"].float(),
+            "lm_head": tp["lm_head"].float(),
+            "layers": [{k: v.float() for k, v in w.items()} for w in tp["layers"]]}
+
+
+def _sdpa_logits(tokens, p, cfg):
+    h = _sdpa_block(tokens, p, cfg)
+    x = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + cfg.eps) * p["final_norm"]
+    return x @ p["lm_head"].T
+
+
+def test_fused_mode_is_exact_math_without_rounding():
+    # fused=True only moves rounding points: with act=None it is the same
+    # float32 function as fused=False (prefill and teacher-forced decode)
+    p = _np(D.init_params(FUSED, "cpu", seed=8))
+    tok = _tokens(4, 64, FUSED.vocab).numpy()
+    np.testing.assert_allclose(OD.block(tok, p, FUSED, act=None, fused=True),
+                               OD.block(tok, p, FUSED, act=None, fused=False),
+                               rtol=1e-5, atol=1e-6)
+
+
+def test_fused_rounding_model_tracks_independent_fp32_decoder():
+    # the compiled-program rounding model (fp16 at each fused kernel's
+    # output) against the independent SDPA decoder in float32, prefill at a
+    # shape that takes every fused branch, within the 1e-2 gate; and it
+    # rounds at fewer points than the eager model, so its mean error is no
+    # larger
+    tp = D.init_params(FUSED, "cpu", seed=8)
+    p = _np(tp)
+    tok = _tokens(4, 64, FUSED.vocab)
+    want = _sdpa_block(tok, _f32(tp), FUSED).numpy()
+    fused = OD.block(tok.numpy(), p, FUSED, act=np.float16, fused=True)
+    eager = OD.block(tok.numpy(), p, FUSED, act=np.float16, fused=False)
+    np.testing.assert_allclose(fused, want, rtol=1e-2, atol=1e-2)
+    assert np.abs(fused - want).mean() <= np.abs(eager - want).mean() * 1.05
+    # and the two rounding models are different programs
+    assert np.abs(fused - eager).max() > 0
+
+
+def test_fused_decode_tracks_independent_fp32_decoder():
+    # teacher-forced decode in the compiled-program rounding model (SwiGLU
+    # weight-stream branch, KV prefix) against the SDPA decoder run over the
+    # whole sequence: the logits of step t are the last-position logits of
+    # prompt + teacher[:t]
+    tp = D.init_params(FUSED, "cpu", seed=9)
+    tf = _f32(tp)
+    prompt = _tokens(2, 64, FUSED.vocab, seed=11)
+    teacher = _tokens(2, 3, FUSED.vocab, seed=12)
+    got = OD.generate_teacher_forced(prompt.numpy(), teacher.numpy(), _np(tp), FUSED,
+                                     fused=True)
+    for t in range(4):
+        seq = torch.cat([prompt, teacher[:, :t]], 1)
+        want = _sdpa_logits(seq, tf, FUSED)[:, -1].numpy()
+        np.testing.assert_allclose(got[t], want, rtol=1e-2, atol=1e-2)

@@ -406,3 +406,47 @@ def test_memory_stats_and_reuse():
     del y
     torch.spyre.empty_cache()
     assert torch.spyre.memory_reserved() >= torch.spyre.memory_allocated()
+
+
+def test_dropout_edges_and_scale():
+    # torch semantics: p = 1 drops everything to zeros (scale 0, no NaN),
+    # p = 0 and eval mode are the identity, otherwise kept values are x/(1-p)
+    _log("native_dropout p = 0 / 0.5 / 1, train and eval")
+    x = randn((128, 256), k=3)
+    xd = x.to(DEV)
+    y, m = torch.native_dropout(xd, 1.0, True)
+    assert torch.equal(y.cpu(), torch.zeros_like(x)) and not bool(m.cpu().any())
+    y, m = torch.native_dropout(xd, 0.0, True)
+    assert torch.equal(y.cpu(), x) and bool(m.cpu().all())
+    y, m = torch.native_dropout(xd, 0.5, False)
+    assert torch.equal(y.cpu(), x) and bool(m.cpu().all())
+    y, m = torch.native_dropout(xd, 0.5, True)
+    mc = m.cpu()
+    assert torch.equal(y.cpu(), torch.where(mc, x * 2, torch.zeros_like(x)))
+    assert 0.45 < mc.float().mean().item() < 0.55
+
+
+def test_out_of_range_indices_raise_index_error():
+    # torch's CPU ops raise IndexError for an index outside the table; the
+    # spyre ops raise it too, at the next synchronisation (the device
+    # reports through the error word; the kernel itself never traps), eager
+    # and compiled alike.  Only spyre tensors here: torch's own GPU kernels
+    # assert on the device for such an index.
+    _log("out-of-range gather indices raise")
+    table = randn((10, 8), k=3).to("spyre")
+    for bad in (10, -1, 1 << 40):
+        ids = torch.tensor([1, bad, 2]).to("spyre")
+        with pytest.raises(IndexError):
+            torch.nn.functional.embedding(ids, table).cpu()
+        with pytest.raises(IndexError):
+            table.index_select(0, ids)
+            torch.spyre.synchronize()
+    # the report is cleared once raised: valid work runs on
+    ok = torch.nn.functional.embedding(torch.tensor([3, 4]).to("spyre"), table).cpu()
+    assert torch.equal(ok, table.cpu()[[3, 4]])
+    torch._dynamo.reset()
+    f = torch.compile(lambda t, i: t[i] * 2)
+    with pytest.raises(IndexError):
+        f(table, torch.tensor([0, 11]).to("spyre")).cpu()
+    torch.testing.assert_close(f(table, torch.tensor([0, 9]).to("spyre")).cpu(),
+                               table.cpu()[[0, 9]] * 2)

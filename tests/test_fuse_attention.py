@@ -155,3 +155,35 @@ def test_row_broadcast_masks_fuse_and_decode_shapes_do_not(mask_kind, mq):
         assert torch.equal(out, ref)  # the fused op runs the same chain on CPU
     else:
         torch.testing.assert_close(out, ref, rtol=1e-2, atol=1e-2)  # Inductor's own kernels
+
+
+@pytest.mark.parametrize("sk", [77, 130])
+def test_masks_with_any_key_count_fuse(sk):
+    # the op pads mask rows to the kernel's 16-byte row alignment, so a key
+    # count off a multiple of 8 is fused like any other
+    q, k, v = _qkv(2, 128, sk, seed=5)
+    mask = _causal(128, sk)
+    out, n = _run(lambda q, k, v, m: _chain(q, k, v, m), q, k, v, mask)
+    assert n == 1
+    # (Inductor pads the stride of the 77- or 130-wide probability buffer,
+    # which moves CPU BLAS to another blocking: equal to rounding, not bits)
+    torch.testing.assert_close(out, _chain(q, k, v, mask), rtol=2e-3, atol=2e-3)
+
+
+@pytest.mark.parametrize("form", ["neg_mul", "neg_div", "neg_nomask", "zero", "inf"])
+def test_nonpositive_or_infinite_scales_stay_unfused(form):
+    # the kernel folds a positive finite scale into exp2 after the row max;
+    # every other scale keeps the unfused chain (and its result)
+    q, k, v = _qkv(2, 128, 64, seed=6)
+    mask = None if form == "neg_nomask" else _causal(128, 64)
+    scale = {"neg_mul": -0.125, "neg_div": -0.125, "neg_nomask": -0.125, "zero": 0.0,
+             "inf": float("inf")}[form]
+    if mask is None:
+        out, n = _run(lambda q, k, v: _chain(q, k, v, None, scale=scale), q, k, v)
+        ref = _chain(q, k, v, None, scale=scale)
+    else:
+        out, n = _run(lambda q, k, v, m: _chain(q, k, v, m, scale=scale, div=form == "neg_div"),
+                      q, k, v, mask)
+        ref = _chain(q, k, v, mask, scale=scale, div=form == "neg_div")
+    assert n == 0
+    torch.testing.assert_close(out, ref, rtol=1e-2, atol=1e-2, equal_nan=True)

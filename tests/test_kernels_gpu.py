@@ -858,21 +858,30 @@ def test_gather_rows_embedding():
     idx = torch.randint(0, 49155, (2048,), generator=torch.Generator().manual_seed(5))
     td, idd = table.to(DEV), idx.to(DEV)
     out = torch.empty(2048, 4096, dtype=torch.float16, device=DEV)
-    _capi.call("sph_gather_rows", _p(td), 49155, 4096, 2, _p(idd), 1, 2048, _p(out), _stream())
+    _capi.call("sph_gather_rows", _p(td), 49155, 4096, 2, _p(idd), 1, 2048, _p(out), None,
+               _stream())
     _sync()
     assert torch.equal(out.cpu(), table[idx])
-    # ragged rows, int32 indices, out-of-range -> zero row
+    # ragged rows, int32 indices, out-of-range: a zero row and the report
+    # word set (a device-accessible int32 the caller clears and reads)
     t2 = randn((10, 3), k=2)
     i2 = torch.tensor([9, 0, 10, -1, 4], dtype=torch.int32)
     o2 = torch.empty(5, 3, dtype=torch.float16, device=DEV)
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
     # keep the device copies referenced until the kernel has run: a dropped
     # temporary's block is reused by the next allocation
     t2d, i2d = t2.to(DEV), i2.to(DEV)
-    _capi.call("sph_gather_rows", _p(t2d), 10, 3, 2, _p(i2d), 0, 5, _p(o2), _stream())
+    _capi.call("sph_gather_rows", _p(t2d), 10, 3, 2, _p(i2d), 0, 5, _p(o2), _p(flag), _stream())
     _sync()
     want = torch.stack([t2[9], t2[0], torch.zeros(3, dtype=torch.float16),
                         torch.zeros(3, dtype=torch.float16), t2[4]])
     assert torch.equal(o2.cpu(), want)
+    assert int(flag.cpu()[0]) == 1
+    # in-range indices leave the word alone
+    flag.zero_()
+    _capi.call("sph_gather_rows", _p(t2d), 10, 3, 2, _p(i2d), 0, 2, _p(o2), _p(flag), _stream())
+    _sync()
+    assert int(flag.cpu()[0]) == 0
 
 
 @pytest.mark.parametrize("upper,diag", [(0, 0), (1, 0), (0, -2), (1, 3)])

@@ -17,9 +17,13 @@ namespace py = pybind11;
 
 namespace spyre {
 // Compiled-kernel loader / launcher (ops_launch.cpp).
-int64_t load_kernel(const std::string& code_object, const std::string& name);
+int64_t load_kernel(const std::string& code_object, const std::string& name, int64_t grid,
+                    int64_t block, const std::vector<int64_t>& extents, bool error_word);
+int64_t load_kernel_file(const std::string& path);
 void launch_kernel(int64_t handle, const std::vector<at::Tensor>& args, int64_t grid,
                    int64_t block, const std::vector<int64_t>& extents);
+void launch_kernel_stored(int64_t handle, const std::vector<at::Tensor>& args);
+void launch_kernel_path(const std::string& path, const std::vector<at::Tensor>& args);
 // Fused SwiGLU projection (ops_gemm.cpp).
 at::Tensor gemm_swiglu(const at::Tensor& x, const at::Tensor& w);
 // Fused attention (ops_attention.cpp).
@@ -34,10 +38,23 @@ PYBIND11_MODULE(_C, m) {
   m.def("start_runtime", &spyre::start_runtime, "Probes the HIP devices (idempotent).");
   m.def("free_runtime", &spyre::free_runtime,
         "Releases cached device memory and the spyre streams.");
-  m.def("load_kernel", [](py::bytes code, const std::string& name) {
-    return spyre::load_kernel(std::string(code), name);
-  }, py::arg("code_object"), py::arg("name"),
-        "Registers a gfx950 code object (loaded into each device on first launch).");
+  m.def("load_kernel", [](py::bytes code, const std::string& name, int64_t grid, int64_t block,
+                          const std::vector<int64_t>& extents, bool error_word) {
+    return spyre::load_kernel(std::string(code), name, grid, block, extents, error_word);
+  }, py::arg("code_object"), py::arg("name"), py::arg("grid") = -1, py::arg("block") = -1,
+        py::arg("extents") = std::vector<int64_t>{}, py::arg("error_word") = false,
+        "Registers a gfx950 code object (loaded into each device on first launch), "
+        "optionally with its launch shape and per-argument extents; error_word: the "
+        "kernel takes the device error word as its last parameter.");
+  m.def("load_kernel_file", &spyre::load_kernel_file, py::arg("path"),
+        "Registers the code object at `path` with its launch description `path`.launch.");
+  // The reference's form first: launch_kernel(path_or_handle, args), the
+  // output last (torch_spyre/csrc/module.cpp:176).
+  m.def("launch_kernel", &spyre::launch_kernel_path, py::arg("path"), py::arg("args"),
+        "Launches the code object at `path` (launch description in `path`.launch) on the "
+        "spyre stream of the arguments' device.");
+  m.def("launch_kernel", &spyre::launch_kernel_stored, py::arg("handle"), py::arg("args"),
+        "Launches a kernel loaded with its launch shape.");
   m.def("launch_kernel", &spyre::launch_kernel, py::arg("handle"), py::arg("args"),
         py::arg("grid"), py::arg("block"), py::arg("extents"),
         "Launches a loaded kernel on the spyre stream of the arguments' device; "
@@ -53,8 +70,10 @@ PYBIND11_MODULE(_C, m) {
   m.def("current_device", []() { return spyre::current_device(); });
   m.def("set_device", [](int d) { spyre::set_device(d); });
   m.def("synchronize", [](int d) {
-    py::gil_scoped_release nogil;
-    spyre::synchronize(d);
+    {
+      py::gil_scoped_release nogil;
+      spyre::synchronize(d);
+    }
   }, py::arg("device") = -1);
   m.def("is_available", []() { return spyre::device_count() > 0; });
   m.def("manual_seed", [](uint64_t seed, int device) { spyre::set_seed(device, seed); },

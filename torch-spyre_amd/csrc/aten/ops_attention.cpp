@@ -70,8 +70,16 @@ at::Tensor attention_fwd(const at::Tensor& q_in, const at::Tensor& k_in, const a
     // (a row stride of 0, one mask row for every query row, is kept)
     if (m.stride(-1) != 1 || (m.stride(-2) != 0 && m.stride(-2) < sk) || (m.stride(-2) % 8) != 0 ||
         reinterpret_cast<uintptr_t>(m.data_ptr()) % 16 != 0 ||
-        (m.dim() == 3 && m.size(0) > 1 && m.stride(0) % 8 != 0))
-      m = contiguous_on_device(m);
+        (m.dim() == 3 && m.size(0) > 1 && m.stride(0) % 8 != 0)) {
+      // Copied into rows padded to a multiple of 8 elements (16 bytes), the
+      // kernel's mask row alignment, whatever the key count.
+      const int64_t sk8 = (sk + 7) / 8 * 8;
+      std::vector<int64_t> shp(m.sizes().begin(), m.sizes().end());
+      shp.back() = sk8;
+      at::Tensor padded = empty_spyre(shp, dt, q_in.device());
+      padded.narrow(-1, 0, sk).copy_(m);
+      m = padded.narrow(-1, 0, sk);
+    }
     mask = m;
     mp = m.data_ptr();
     ldm = m.stride(-2);

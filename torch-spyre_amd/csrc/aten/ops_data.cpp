@@ -71,8 +71,10 @@ at::Tensor& tri_out(const at::Tensor& self, int64_t diagonal, at::Tensor& out) {
 }
 
 // Row gather along `dim` (embedding is index_select(weight, 0, ids)).  An
-// index outside [0, size) yields a zero row instead of torch's IndexError
-// (the check would need a device-to-host round trip per call).
+// index outside [0, size) zero-fills its row and is reported through the
+// device error word, which raises IndexError at the next synchronisation
+// (checking on the host at the call would cost a device-to-host round trip
+// per call).
 at::Tensor& index_select_out(const at::Tensor& self, int64_t dim, const at::Tensor& index,
                              at::Tensor& out) {
   TORCH_CHECK(index.dim() <= 1, "spyre: index_select expects a 0-D or 1-D index");
@@ -99,6 +101,7 @@ at::Tensor& index_select_out(const at::Tensor& self, int64_t dim, const at::Tens
   SPYRE_SPH_CHECK(sph_gather_rows(table.data_ptr(), nrows, row_elems,
                                   static_cast<int>(table.element_size()), idx.data_ptr(),
                                   idx.scalar_type() == at::kLong ? 1 : 0, n, g.data_ptr(),
+                                  device_error_word(self.get_device()),
                                   stream(self.get_device())));
   if (!direct) device_copy(out, d == 0 ? g : g.movedim(0, d));
   return out;
@@ -139,7 +142,8 @@ std::tuple<at::Tensor, at::Tensor> native_dropout(const at::Tensor& input, doubl
   keep_cpu.uniform_(0.0, 1.0, pick_gen(std::nullopt, input.get_device()));
   mask.copy_(keep_cpu.ge(p));
   at::Tensor out = at::where(mask, input, at::zeros({}, input.options()));
-  return {out.mul(1.0 / (1.0 - p)), mask};
+  // p == 1 drops everything: scale 0 (as torch), not 0 * inf
+  return {out.mul(p == 1.0 ? 0.0 : 1.0 / (1.0 - p)), mask};
 }
 
 at::Tensor& arange_out(const at::Scalar& start, const at::Scalar& end, const at::Scalar& step,

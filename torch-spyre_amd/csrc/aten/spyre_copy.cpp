@@ -162,10 +162,12 @@ void d2h_bytes(int dev, const at::Tensor& host, const void* src, size_t n, bool 
   char* dst = static_cast<char*>(host.data_ptr());
   if (host_ptr_pinned(dst)) {
     SPYRE_HIP_CHECK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, s));
-    if (non_blocking)
+    if (non_blocking) {
       keep_alive(e, s, host.storage());
-    else
+    } else {
       SPYRE_HIP_CHECK(hipStreamSynchronize(s));
+      check_device_errors(dev);
+    }
     return;
   }
   e.init(dev);
@@ -190,6 +192,7 @@ void d2h_bytes(int dev, const at::Tensor& host, const void* src, size_t n, bool 
     host_copy(dst + off, sl.buf, c);
     if (i + kSlots < nchunks) issue(i + kSlots);
   }
+  check_device_errors(dev);
 }
 
 void release_copy_keepalive(int dev) {

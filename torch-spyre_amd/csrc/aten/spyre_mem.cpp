@@ -270,6 +270,7 @@ c10::Scalar spyre_local_scalar_dense(const at::Tensor& self) {
   SPYRE_HIP_CHECK(hipMemcpyAsync(host.data_ptr(), self.data_ptr(), self.element_size(),
                                  hipMemcpyDeviceToHost, s));
   SPYRE_HIP_CHECK(hipStreamSynchronize(s));
+  check_device_errors(self.get_device());
   return host.item();
 }
 

@@ -30,6 +30,12 @@ std::array<hipStream_t, kMaxDevices> g_streams{};
 
 std::array<std::atomic<uint64_t>, kMaxDevices> g_seeds{};
 
+// Per device: the host address of its error word and the device-side
+// address kernels are given.
+std::mutex g_err_mu;
+std::array<volatile int32_t*, kMaxDevices> g_err_host{};
+std::array<int32_t*, kMaxDevices> g_err_dev{};
+
 void do_start() {
   int n = 0;
   hipError_t e = hipGetDeviceCount(&n);
@@ -87,11 +93,49 @@ void synchronize(int device) {
   if (device >= 0) {
     if (g_streams[device]) SPYRE_HIP_CHECK(hipStreamSynchronize(g_streams[device]));
     release_copy_keepalive(device);
+    check_device_errors(device);
     return;
   }
   for (int d = 0; d < device_count(); ++d)
     if (g_streams[d]) SPYRE_HIP_CHECK(hipStreamSynchronize(g_streams[d]));
   release_copy_keepalive(-1);
+  check_device_errors(-1);
+}
+
+int32_t* device_error_word(int device) {
+  if (device < 0) device = current_device();
+  TORCH_CHECK(device < device_count(), "spyre: invalid device index ", device);
+  if (g_err_dev[device]) return g_err_dev[device];
+  std::lock_guard<std::mutex> lk(g_err_mu);
+  if (!g_err_dev[device]) {
+    const int cur = current_device();
+    if (cur != device) SPYRE_HIP_CHECK(hipSetDevice(device));
+    void* h = nullptr;
+    // fine-grained (coherent) so a kernel's store is visible to the host
+    // once the kernel has completed
+    SPYRE_HIP_CHECK(hipHostMalloc(&h, 64, hipHostMallocMapped | hipHostMallocCoherent));
+    *static_cast<volatile int32_t*>(h) = 0;
+    void* d = nullptr;
+    SPYRE_HIP_CHECK(hipHostGetDevicePointer(&d, h, 0));
+    g_err_host[device] = static_cast<volatile int32_t*>(h);
+    g_err_dev[device] = static_cast<int32_t*>(d);
+    if (cur != device) SPYRE_HIP_CHECK(hipSetDevice(cur));
+  }
+  return g_err_dev[device];
+}
+
+void check_device_errors(int device) {
+  const int lo = device < 0 ? 0 : device;
+  const int hi = device < 0 ? kMaxDevices : device + 1;
+  for (int d = lo; d < hi; ++d) {
+    volatile int32_t* w = g_err_host[d];
+    if (w == nullptr || *w == 0) continue;
+    const int32_t code = *w;
+    *w = 0;
+    TORCH_CHECK_INDEX(false, "spyre: index out of range in a gather on spyre:", d,
+                      " (index_select / embedding / an indexed load of a compiled kernel; "
+                      "code ", code, "); the rows of out-of-range indices were zero-filled");
+  }
 }
 
 bool has_sph(at::ScalarType t) {

@@ -48,8 +48,22 @@ void set_device(int device);
 // The stream all spyre work on `device` is ordered on (-1: current device).
 // Created on first use with default priority.
 hipStream_t stream(int device = -1);
-// Blocks until all spyre work on `device` (-1: every device) has finished.
+// Blocks until all spyre work on `device` (-1: every device) has finished,
+// then raises for any out-of-range index a kernel reported meanwhile.
 void synchronize(int device = -1);
+
+// Device error word of `device`: 4 bytes of pinned host memory mapped into
+// the device's address space (the device-side address is returned).  A
+// kernel that meets an index outside its table writes a nonzero code there,
+// zero-fills what that index would have produced and carries on: there is
+// no device trap and no fault.  The host reads the word at every point where
+// it waits for the device (synchronize, blocking device-to-host copies,
+// .item()) and raises; torch's CPU kernels raise at the call instead.
+int32_t* device_error_word(int device);
+// Raises c10::IndexError if a kernel on `device` (-1: every device) reported
+// an out-of-range index since the last check; the report is cleared first.
+// Call only after the device work in question has completed.
+void check_device_errors(int device = -1);
 
 // Kernel-library element type of a torch dtype; throws for unsupported ones.
 sph_dtype to_sph(at::ScalarType t);

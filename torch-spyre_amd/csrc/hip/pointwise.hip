@@ -450,13 +450,16 @@ template <typename V>
 __global__ void __launch_bounds__(256)
 gather_rows_kernel(const V* __restrict__ table, int64_t num_rows, int64_t row_v,
                    const void* __restrict__ idx, int idx64, int64_t n_idx,
-                   V* __restrict__ out) {
+                   V* __restrict__ out, int32_t* __restrict__ oob) {
   const int64_t i = blockIdx.x;
   const int64_t r = idx64 ? static_cast<const int64_t*>(idx)[i]
                           : static_cast<int64_t>(static_cast<const int32_t*>(idx)[i]);
   V* o = out + i * row_v;
   if (r < 0 || r >= num_rows) {
     for (int64_t c = threadIdx.x; c < row_v; c += 256) o[c] = V{};
+    // one lane reports it (a plain vector store; any number of workgroups
+    // may store the same 1)
+    if (oob != nullptr && threadIdx.x == 0) *reinterpret_cast<volatile int32_t*>(oob) = 1;
     return;
   }
   const V* s = table + r * row_v;
@@ -468,7 +471,7 @@ gather_rows_kernel(const V* __restrict__ table, int64_t num_rows, int64_t row_v,
 extern "C" int sph_gather_rows(const void* table, int64_t num_rows,
                                int64_t row_elems, int elem_bytes,
                                const void* idx, int idx_is_i64, int64_t n_idx,
-                               void* out, sph_stream_t stream) {
+                               void* out, int32_t* oob_flag, sph_stream_t stream) {
   SPH_REQUIRE(num_rows >= 0 && row_elems >= 0 && n_idx >= 0, SPH_ERR_INVALID_ARG,
               "gather_rows: negative size");
   SPH_REQUIRE(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4 || elem_bytes == 8,
@@ -483,23 +486,23 @@ extern "C" int sph_gather_rows(const void* table, int64_t num_rows,
   if (v16) {
     gather_rows_kernel<u32x4><<<g, 256, 0, st>>>(static_cast<const u32x4*>(table), num_rows,
                                                  row_bytes / 16, idx, idx_is_i64, n_idx,
-                                                 static_cast<u32x4*>(out));
+                                                 static_cast<u32x4*>(out), oob_flag);
   } else if (elem_bytes == 2) {
     gather_rows_kernel<uint16_t><<<g, 256, 0, st>>>(static_cast<const uint16_t*>(table), num_rows,
                                                     row_elems, idx, idx_is_i64, n_idx,
-                                                    static_cast<uint16_t*>(out));
+                                                    static_cast<uint16_t*>(out), oob_flag);
   } else if (elem_bytes == 4) {
     gather_rows_kernel<uint32_t><<<g, 256, 0, st>>>(static_cast<const uint32_t*>(table), num_rows,
                                                     row_elems, idx, idx_is_i64, n_idx,
-                                                    static_cast<uint32_t*>(out));
+                                                    static_cast<uint32_t*>(out), oob_flag);
   } else if (elem_bytes == 8) {
     gather_rows_kernel<uint64_t><<<g, 256, 0, st>>>(static_cast<const uint64_t*>(table), num_rows,
                                                     row_elems, idx, idx_is_i64, n_idx,
-                                                    static_cast<uint64_t*>(out));
+                                                    static_cast<uint64_t*>(out), oob_flag);
   } else {
     gather_rows_kernel<uint8_t><<<g, 256, 0, st>>>(static_cast<const uint8_t*>(table), num_rows,
                                                    row_elems, idx, idx_is_i64, n_idx,
-                                                   static_cast<uint8_t*>(out));
+                                                   static_cast<uint8_t*>(out), oob_flag);
   }
   return check_launch("sph_gather_rows");
 }

@@ -76,7 +76,7 @@ _SIGS = {
                        c_f64, c_f64, vp], c_int),
     "sph_reduce": ([c_int, ctypes.POINTER(Operand), ctypes.POINTER(Operand), c_int,
                     ctypes.POINTER(c_i64), ctypes.c_uint32, vp], c_int),
-    "sph_gather_rows": ([vp, c_i64, c_i64, c_int, vp, c_int, c_i64, vp, vp], c_int),
+    "sph_gather_rows": ([vp, c_i64, c_i64, c_int, vp, c_int, c_i64, vp, vp, vp], c_int),
     "sph_tri": ([c_int, c_i64, c_int, vp, vp, c_i64, c_i64, c_i64, vp], c_int),
     "sph_rope": ([c_int, vp, vp, vp, c_i64, c_i64, c_i64, c_f32, vp], c_int),
     "sph_stick_nbytes": ([c_int, ctypes.POINTER(c_i64), ctypes.POINTER(ctypes.c_int32), c_int],

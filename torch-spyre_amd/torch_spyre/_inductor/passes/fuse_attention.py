@@ -27,6 +27,7 @@ which is matched too.
 
 from __future__ import annotations
 
+import math
 import numbers
 from typing import Optional
 
@@ -143,6 +144,11 @@ def _finish(bmm2, bmm1, chain, v, mask, scale) -> Optional[tuple]:
     """Operand, use and shape checks shared by both forms."""
     p16 = chain[0]
     if not _is(bmm1, aten.bmm.default):
+        return None
+    # The kernel folds the scale into exp2 after taking the row max, which
+    # holds for positive finite scales only (a negative sign form or a
+    # multiplication by a negative constant stays on the unfused chain).
+    if not (math.isfinite(scale) and scale > 0):
         return None
     q, kt = bmm1.args
     if not (_is(kt, aten.permute.default) and list(kt.args[1]) == [0, 2, 1]):

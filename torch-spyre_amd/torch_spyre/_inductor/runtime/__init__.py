@@ -43,6 +43,9 @@ class KernelSpec:
     block: int
     source: str                  # HIP C++ of the kernel `spyre_kernel`
     op_info: dict = dataclasses.field(default_factory=dict)
+    # the kernel takes the device error word as a last parameter (indirect
+    # indexing: out-of-range indices are reported there, see launch_kernel)
+    error_word: bool = False
 
 
 @dataclasses.dataclass

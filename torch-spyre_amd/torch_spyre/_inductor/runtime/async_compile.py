@@ -8,8 +8,8 @@ from __future__ import annotations
 from typing import Any, Union
 
 from . import KernelSpec, UnimplementedOp
-from .hiprtc import compile_source
-from .kernel_runner import SpyreHipKernelRunner, SpyreUnimplementedRunner
+from .hiprtc import compile_source, write_launchable
+from .kernel_runner import SpyreHipKernelRunner, SpyreUnimplementedRunner, launch_description
 
 
 class SpyreAsyncCompile:
@@ -20,7 +20,8 @@ class SpyreAsyncCompile:
         if isinstance(ks, UnimplementedOp):
             return SpyreUnimplementedRunner(kernel_name, ks.op)
         code = compile_source(ks.source, f"{kernel_name}.hip")
-        return SpyreHipKernelRunner(kernel_name, ks, code)
+        path = write_launchable(code, launch_description(ks))
+        return SpyreHipKernelRunner(kernel_name, ks, code, path)
 
     # Name kept from the reference's wrapper code.
     sdsc = hip

@@ -113,3 +113,20 @@ def compile_source(source: str, name: str = "spyre_kernel.hip") -> bytes:
         f.write(blob)
     os.replace(tmp, path)
     return blob
+
+
+def write_launchable(code: bytes, launch_line: str) -> str:
+    """Writes a code object and its launch description (`<path>.launch`)
+    under the cache directory, named by their content; returns the path that
+    torch_spyre._C.launch_kernel(path, args) takes."""
+    key = hashlib.sha256(code + b"\0" + launch_line.encode()).hexdigest()
+    d = os.path.join(_cache_dir(), "launch")
+    os.makedirs(d, exist_ok=True)
+    path = os.path.join(d, key + ".co")
+    if not (os.path.exists(path) and os.path.exists(path + ".launch")):
+        for p, blob in ((path, code), (path + ".launch", launch_line.encode())):
+            tmp = f"{p}.{os.getpid()}.tmp"
+            with open(tmp, "wb") as f:
+                f.write(blob)
+            os.replace(tmp, p)
+    return path

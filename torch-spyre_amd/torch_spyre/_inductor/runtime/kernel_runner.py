@@ -9,7 +9,24 @@ recompiles its program on every call, torch_spyre/csrc/module.cpp:64-170).
 
 from __future__ import annotations
 
+from typing import Optional
+
 from . import KernelSpec
+
+# the generated kernel's symbol (spyre_kernel.py emits `spyre_kernel`)
+KERNEL_SYMBOL = "spyre_kernel"
+
+
+def launch_extents(spec: KernelSpec) -> list[int]:
+    return [a.extent if a.extent is not None else -1 for a in spec.args]
+
+
+def launch_description(spec: KernelSpec) -> str:
+    """The `.launch` line torch_spyre._C.launch_kernel(path, args) reads:
+    "<kernel name> <grid> <block> <n> <extent>*n <error word>"."""
+    ext = launch_extents(spec)
+    return " ".join([KERNEL_SYMBOL, str(spec.grid), str(spec.block), str(len(ext)),
+                     *map(str, ext), str(int(spec.error_word))]) + "\n"
 
 
 class SpyreUnimplementedRunner:
@@ -23,16 +40,24 @@ class SpyreUnimplementedRunner:
 
 
 class SpyreHipKernelRunner:
-    def __init__(self, name: str, spec: KernelSpec, code_object: bytes):
+    """`path` (optional) is the kernel's code object on disk with its launch
+    description beside it (`path`.launch), for callers that launch by path
+    as the reference's runner does: torch_spyre._C.launch_kernel(path, args)."""
+
+    def __init__(self, name: str, spec: KernelSpec, code_object: bytes,
+                 path: Optional[str] = None):
         from torch_spyre import _C
 
         self.kernel_name = name
         self.spec = spec
-        self.handle = _C.load_kernel(code_object, "spyre_kernel")
+        self.path = path
         # extents[i] bounds argument i (-1 = not checked)
-        self.extents = [a.extent if a.extent is not None else -1 for a in spec.args]
+        self.extents = launch_extents(spec)
+        self.handle = _C.load_kernel(code_object, KERNEL_SYMBOL, spec.grid, spec.block,
+                                     self.extents, spec.error_word)
 
     def run(self, *args, **kwargs):
         from torch_spyre import _C
 
-        _C.launch_kernel(self.handle, list(args), self.spec.grid, self.spec.block, self.extents)
+        # the reference's two-argument form (torch_spyre/csrc/module.cpp:176)
+        _C.launch_kernel(self.handle, list(args))

@@ -660,15 +660,19 @@ class SpyreKernel(SIMDKernel):
         self.stores.writeline(DeferredLine(name, line))
 
     def check_bounds(self, expr: sympy.Expr, size: sympy.Expr, lower: bool, upper: bool) -> None:
-        # Indirect indices (gathers) are clamped into range instead of
-        # asserting: an out-of-range index reads row 0 rather than faulting.
+        # Indirect indices (gathers, scatters) are checked without a trap: an
+        # out-of-range index is reported to the device error word (a kernel
+        # parameter the launcher appends; the host raises IndexError at its
+        # next synchronisation) and replaced by 0, so the access stays in
+        # bounds.  Eager index_select / embedding report the same way.
         if not (lower or upper):
             return
         if not isinstance(expr, sympy.Symbol):
             raise Unsupported(f"bounds check on {expr}")
         e = str(expr)
         n = self.index_to_str(size)
-        self.compute.writeline(f"{e} = ({e} < 0 || {e} >= {n}) ? 0 : {e};")
+        self._needs_error_word = True
+        self.compute.writeline(f"if ({e} < 0 || {e} >= {n}) {{ *spy_err = 1; {e} = 0; }}")
 
     # -- reductions ---------------------------------------------------------------
     def _acc(self, decl: str) -> str:
@@ -796,6 +800,9 @@ class SpyreKernel(SIMDKernel):
             ext = self._extents.get(inner)
             spec_args.append(f"TensorArg(is_input={is_input}, arg_index={i}, "
                              f"dtype={dt!r}, extent={ext!r})")
+        if getattr(self, "_needs_error_word", False):
+            # the device error word, appended by the launcher after the buffers
+            params.append("volatile int* __restrict__ spy_err")
         code = IndentedBuffer()
         code.writeline('#include "spyre_inductor_rt.h"')
         code.writeline(f'extern "C" __global__ void __launch_bounds__({block}) spyre_kernel(')
@@ -858,6 +865,8 @@ class SpyreKernel(SIMDKernel):
             spec.writeline(f"is_reduction={is_red},")
             spec.writeline(f"dimensions={[xnumel, rnumel] if is_red else [xnumel]!r},")
             spec.writeline(f"grid={grid}, block={block},")
+            if getattr(self, "_needs_error_word", False):
+                spec.writeline("error_word=True,")
             spec.writeline("args=[")
             with spec.indent():
                 for a in spec_args:
