@@ -308,6 +308,30 @@ int sph_attention_decode(sph_dtype dtype, int64_t batch, int64_t mq, int64_t sk,
  * shape, or mq > 16). */
 int64_t sph_attention_decode_workspace_bytes(int64_t batch, int64_t mq, int64_t sk);
 
+/* sph_attention_fwd for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc): the same arguments without the workspace, the same kernels
+ * and results (bit for bit: a masked prefill call classes the mask blocks,
+ * a decode call splits its keys, as sph_attention_fwd with a workspace of
+ * sph_attention_workspace_bytes does).  The workspace is a static device
+ * array of sph_attention_fwd_noalloc_max_bytes() (4 MiB) per GPU, held
+ * until the process ends; a shape that needs more returns
+ * SPH_ERR_TOO_LARGE before any launch.  Nothing is allocated and nothing
+ * needs clearing between calls, but every call on one GPU uses that GPU's
+ * one array: calls that may overlap on a GPU (other streams, other host
+ * threads) race and must be ordered by the caller.
+ * No counterpart in the reference: it exists for callers that cannot
+ * allocate. */
+int sph_attention_fwd_noalloc(sph_dtype dtype, int64_t batch, int64_t mq, int64_t sk,
+                              int64_t head_dim, const void* q, int64_t ldq, int64_t stride_q,
+                              const void* k, int64_t ldk, int64_t stride_k, const void* v,
+                              int64_t ldv, int64_t stride_v, const void* mask, int64_t ldm,
+                              int64_t stride_m, int64_t causal_q, int64_t causal_off,
+                              float scale, void* o, int64_t ldo, int64_t stride_o,
+                              sph_stream_t stream);
+/* Bytes of the static workspace of sph_attention_fwd_noalloc. */
+int64_t sph_attention_fwd_noalloc_max_bytes(void);
+
 /* ------------------------------------------------------------------ */
 /* Generic strided pointwise engine                                     */
 /* Replaces: the generated base/list_inp eager ops of Metadata.yaml     */

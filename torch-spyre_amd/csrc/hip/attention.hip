@@ -47,6 +47,8 @@
 //     by the number of key blocks the mask leaves, counted and sorted on the
 //     device from the block classes), so short jobs fill in behind long
 //     ones.
+#include <mutex>
+
 #include "sph_common.h"
 
 namespace sph {
@@ -684,4 +686,93 @@ extern "C" int sph_attention_fwd(sph_dtype dtype, int64_t batch, int64_t mq, int
     SPH_ATTN(bf16_t);
 #undef SPH_ATTN
   return check_launch("sph_attention_fwd");
+}
+
+// ---------------------------------------------------------------------------
+// sph_attention_fwd without a caller workspace, for callers that cannot
+// allocate device memory (code under HIP graph capture, serving loops,
+// harnesses that forbid hipMalloc).  The workspace of sph_attention_fwd (the
+// mask-block classes and job order of a masked prefill call, the key-split
+// partials of a decode call) lives in one file-scope device array of
+// kScratchBytes per GPU, held until the process ends.  In host code the
+// array's name is only a stand-in: its device address is looked up once per
+// device with hipGetSymbolAddress (that device current) and that address is
+// what the kernels get.  Nothing in the workspace needs to start at zero
+// (every byte a call reads it has written before, on the same stream).
+// Every call on a GPU shares that GPU's array and leaves its contents
+// behind: calls that overlap on one GPU (different streams, or host threads
+// without an order between their streams) race.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int64_t kScratchBytes = int64_t(4) << 20;
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices] = {};
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+// The device address of `scratch` on `dev` (looked up on first use).
+int scratch_address(int dev, void** out) {
+  SPH_REQUIRE(dev >= 0 && dev < kScratchDevices, SPH_ERR_INVALID_ARG,
+              "attention (no-alloc): device index out of range");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur >= 0 && cur != dev) {
+      const hipError_t e2 = hipSetDevice(cur);
+      if (e == hipSuccess) e = e2;
+    }
+    if (e != hipSuccess || p == nullptr)
+      return set_error(e != hipSuccess ? static_cast<int>(e) : SPH_ERR_INVALID_ARG,
+                       std::string("attention (no-alloc): hipGetSymbolAddress(scratch) failed: ") +
+                           hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SPH_OK;
+}
+}  // namespace
+
+extern "C" int64_t sph_attention_fwd_noalloc_max_bytes(void) { return kScratchBytes; }
+
+extern "C" int sph_attention_fwd_noalloc(sph_dtype dtype, int64_t batch, int64_t mq, int64_t sk,
+                                         int64_t head_dim, const void* q, int64_t ldq,
+                                         int64_t stride_q, const void* k, int64_t ldk,
+                                         int64_t stride_k, const void* v, int64_t ldv,
+                                         int64_t stride_v, const void* mask, int64_t ldm,
+                                         int64_t stride_m, int64_t causal_q, int64_t causal_off,
+                                         float scale, void* o, int64_t ldo, int64_t stride_o,
+                                         sph_stream_t stream) {
+  SPH_REQUIRE(batch >= 0 && mq >= 0 && sk >= 0, SPH_ERR_INVALID_ARG,
+              "attention (no-alloc): negative size");
+  if (batch == 0 || mq == 0) return SPH_OK;
+  // the workspace this call would use: decode partials, or the classes and
+  // order of a masked prefill call (an unmasked prefill call uses none)
+  const bool decode = mq <= 16 && mq % AQ != 0;
+  const int64_t need = (decode || mask != nullptr)
+                           ? sph_attention_workspace_bytes(batch, mq, sk, stride_m) : 0;
+  SPH_REQUIRE(need <= kScratchBytes, SPH_ERR_TOO_LARGE,
+              "attention (no-alloc): this shape needs " + std::to_string(need) +
+                  " bytes of workspace, above the " + std::to_string(kScratchBytes) +
+                  "-byte static scratch; call sph_attention_fwd with a workspace");
+  void* ws = nullptr;
+  if (need > 0) {
+    hipDevice_t dev = 0;
+    const hipError_t e = hipStreamGetDevice(as_stream(stream), &dev);
+    if (e != hipSuccess)
+      return set_error(static_cast<int>(e),
+                       std::string("attention (no-alloc): hipStreamGetDevice failed: ") +
+                           hipGetErrorString(e));
+    const int rc = scratch_address(static_cast<int>(dev), &ws);
+    if (rc != SPH_OK) return rc;
+  }
+  return sph_attention_fwd(dtype, batch, mq, sk, head_dim, q, ldq, stride_q, k, ldk, stride_k, v,
+                           ldv, stride_v, mask, ldm, stride_m, causal_q, causal_off, scale, o, ldo,
+                           stride_o, ws, need > 0 ? kScratchBytes : 0, stream);
 }

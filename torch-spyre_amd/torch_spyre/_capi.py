@@ -72,6 +72,10 @@ _SIGS = {
                               c_i64, vp, c_i64, c_i64, c_i64, vp, c_i64, c_i64, c_i64, c_i64,
                               c_f32, vp, c_i64, c_i64, vp, c_i64, vp], c_int),
     "sph_attention_decode_workspace_bytes": ([c_i64, c_i64, c_i64], c_i64),
+    "sph_attention_fwd_noalloc": ([c_int, c_i64, c_i64, c_i64, c_i64, vp, c_i64, c_i64, vp,
+                                   c_i64, c_i64, vp, c_i64, c_i64, vp, c_i64, c_i64, c_i64, c_i64,
+                                   c_f32, vp, c_i64, c_i64, vp], c_int),
+    "sph_attention_fwd_noalloc_max_bytes": ([], c_i64),
     "sph_pointwise": ([c_int, c_int, ctypes.POINTER(Operand), c_int, ctypes.POINTER(c_i64),
                        c_f64, c_f64, vp], c_int),
     "sph_reduce": ([c_int, ctypes.POINTER(Operand), ctypes.POINTER(Operand), c_int,
