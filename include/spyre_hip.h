@@ -474,6 +474,70 @@ int sph_gather_rows(const void* table, int64_t num_rows, int64_t row_elems,
                     int elem_bytes, const void* idx, int idx_is_i64,
                     int64_t n_idx, void* out, int32_t* oob_flag, sph_stream_t stream);
 
+/* ------------------------------------------------------------------ */
+/* Generated and scanned fills                                          */
+/* Replaces: the CPU fallbacks of cumsum (spyre_torch_ops.cpp:502-505)  */
+/*   and the host paths of arange and the random fills; the identity    */
+/*   stub of native_dropout (:180-186).                                 */
+/* ------------------------------------------------------------------ */
+
+/* out[i] = start + step * i for i < n, in the output type's accumulation
+ * type as torch's CPU arange (float for F16/BF16, double for F32/F64 from
+ * start/step; int64 for integer types from istart/istep). */
+int sph_arange(sph_dtype dtype, double start, double step, int64_t istart, int64_t istep,
+               int64_t n, void* out, sph_stream_t stream);
+
+/* Inclusive prefix sum along the middle dimension of contiguous x, y
+ * [outer, len, inner] of one dtype, accumulated as torch's CPU cumsum does
+ * (float for F16/BF16, double for F32/F64, int64 for integer types, each
+ * partial sum rounded to the dtype when stored).  Columns (inner > 1) and
+ * rows of up to 8192 elements are walked sequentially, in the CPU kernel's
+ * order, so the results are bit-identical to it; longer rows of the last
+ * dimension are scanned by a workgroup each (floating-point sums then
+ * differ from the sequential order by rounding). */
+int sph_cumsum(sph_dtype dtype, const void* x, void* y, int64_t outer, int64_t len, int64_t inner,
+               sph_stream_t stream);
+
+/* Random fill kinds of sph_random_fill. */
+enum { SPH_RNG_UNIFORM = 0, SPH_RNG_NORMAL = 1, SPH_RNG_INT = 2 };
+
+/* Fills n contiguous elements from Philox4x32-10 (counter-based): block j
+ * is the generator's output for counter offset + j under key `seed`;
+ * element i of a fill of 32-bit draws takes word i % 4 of block i / 4, of
+ * 64-bit draws (F64 uniform / normal, integer ranges above 2^32) words
+ * 2(i % 2), 2(i % 2) + 1 of block i / 2.  SPH_RNG_UNIFORM: a + u (b - a), u
+ * in [0, 1) from the top 24 (F64: 53) bits, [a, b) kept half-open after
+ * rounding; SPH_RNG_NORMAL: a + b * n, n from Box-Muller on word pairs;
+ * SPH_RNG_INT: ifrom + draw % irange (any dtype).  The caller advances its
+ * offset by sph_random_blocks(...) per fill. */
+int sph_random_fill(int kind, sph_dtype dtype, void* out, int64_t n, uint64_t seed,
+                    uint64_t offset, double a, double b, int64_t ifrom, uint64_t irange,
+                    sph_stream_t stream);
+/* Counter blocks a fill of n elements uses. */
+int64_t sph_random_blocks(int kind, sph_dtype dtype, int64_t n, uint64_t irange);
+
+/* Dropout of n contiguous elements: element i is kept when its uniform
+ * draw (word i % 4 of Philox block offset + i / 4, top 24 bits) is >= p;
+ * y = keep ? x * scale : 0, mask = keep (one byte each).  F16, BF16, F32.
+ * Uses (n + 3) / 4 counter blocks. */
+int sph_dropout(sph_dtype dtype, const void* x, void* y, uint8_t* mask, int64_t n, float p,
+                float scale, uint64_t seed, uint64_t offset, sph_stream_t stream);
+
+/* Transposing copy of elem_bytes-byte elements: for every batch index
+ * (up to 4 batch dims of sizes bsizes, element strides bsrc_strides in
+ * src and bdst_strides in dst), dst[v * dv + u] = src[u * su + v] for
+ * u < U, v < V: v is contiguous in src, u in dst.  64 x 64 tiles through
+ * LDS, so reads and writes are both coalesced (a strided elementwise copy
+ * reads or writes one element per 64-byte run).  src and dst must not
+ * overlap.
+ * Replaces: the reference's transpose data ops (torch_spyre/_inductor/
+ * codegen/data_ops.py:16-630, "restickify"), for `.contiguous()` of a
+ * transposed tensor, eager or compiled. */
+int sph_transpose_copy(int elem_bytes, const void* src, void* dst, int64_t U, int64_t V,
+                       int64_t su, int64_t dv, int nb, const int64_t* bsizes,
+                       const int64_t* bsrc_strides, const int64_t* bdst_strides,
+                       sph_stream_t stream);
+
 /* tril/triu on the last two dims of a contiguous [batch, rows, cols]
  * tensor: keep element (r, c) when c - r <= diagonal (lower) or
  * c - r >= diagonal (upper), zero it otherwise.

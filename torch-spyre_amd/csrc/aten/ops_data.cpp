@@ -4,14 +4,18 @@
 // Reference: generated cat (codegen/inputs/Metadata.yaml:45-47), tril
 // (:322-324), embedding (:105-115); native_dropout stub
 // (codegen/inputs/spyre_torch_ops.cpp:180-186); CPU fallbacks for ne / cumsum
-// (:494-505).  Like the reference, cumsum, arange and the random fills run on
-// the host and copy the result; everything else runs on the GPU.
+// (:494-505).  Here all of them run on the GPU: cumsum as a device scan,
+// arange as a device fill, the random fills and dropout from the device's
+// Philox generator (seeded by torch.spyre.manual_seed).
 #include <ATen/CPUGeneratorImpl.h>
 #include <ATen/WrapDimUtils.h>
 #include <ATen/native/Resize.h>
 #include <torch/library.h>
 
+#include <cmath>
+#include <limits>
 #include <mutex>
+#include <utility>
 
 #include "spyre_ops_common.h"
 
@@ -112,22 +116,48 @@ at::Tensor index_select(const at::Tensor& self, int64_t dim, const at::Tensor& i
   return index_select_out(self, dim, index, out);
 }
 
-// Host-side generators of the random fills, seeded by torch.spyre.manual_seed.
-std::mutex g_gen_mu;
-at::Generator host_generator(int device) {
-  static std::vector<std::pair<uint64_t, at::Generator>> gens(64);
-  std::lock_guard<std::mutex> lk(g_gen_mu);
-  const uint64_t seed = get_seed(device);
-  auto& slot = gens[device];
-  if (!slot.second.defined() || slot.first != seed) {
-    slot = {seed, at::make_generator<at::CPUGeneratorImpl>(seed)};
+// (seed, counter offset) of the next random fill of `blocks` Philox blocks
+// on `device`: the device generator's, advanced past this fill.  With an
+// explicit CPU generator the fill is keyed by one 64-bit draw of it at
+// offset 0 instead, so it is reproducible from that generator.
+std::pair<uint64_t, uint64_t> philox_state(const std::optional<at::Generator>& gen, int device,
+                                           int64_t blocks) {
+  if (gen.has_value() && gen->defined()) {
+    TORCH_CHECK(gen->device().is_cpu(),
+                "spyre: random fills take a CPU generator or none (the device's own)");
+    at::Generator g = *gen;
+    auto* impl = at::check_generator<at::CPUGeneratorImpl>(g);
+    std::lock_guard<std::mutex> lk(g.mutex());
+    return {impl->random64(), 0};
   }
-  return slot.second;
+  return {get_seed(device), rng_offset_advance(device, static_cast<uint64_t>(blocks))};
 }
 
-at::Generator pick_gen(const std::optional<at::Generator>& g, int device) {
-  if (g.has_value() && g->defined() && g->device().is_cpu()) return *g;
-  return host_generator(device);
+// Runs `fill(ptr)` on a contiguous image of `self` and copies it in when
+// `self` is not contiguous itself.
+template <typename F>
+at::Tensor& fill_contiguous(at::Tensor& self, F&& fill) {
+  if (self.numel() == 0) return self;
+  c10::DeviceGuard guard(self.device());
+  if (self.is_contiguous()) {
+    fill(self);
+  } else {
+    at::Tensor tmp = empty_spyre(self.sizes(), self.scalar_type(), self.device());
+    fill(tmp);
+    device_copy(self, tmp);
+  }
+  return self;
+}
+
+at::Tensor& random_fill(at::Tensor& self, int kind, double a, double b, int64_t ifrom,
+                        uint64_t irange, const std::optional<at::Generator>& gen) {
+  const sph_dtype dt = to_sph(self.scalar_type());
+  const int64_t blocks = sph_random_blocks(kind, dt, self.numel(), irange);
+  const auto [seed, offset] = philox_state(gen, self.get_device(), blocks);
+  return fill_contiguous(self, [&](at::Tensor& t) {
+    SPYRE_SPH_CHECK(sph_random_fill(kind, dt, t.data_ptr(), t.numel(), seed, offset, a, b, ifrom,
+                                    irange, stream(t.get_device())));
+  });
 }
 
 std::tuple<at::Tensor, at::Tensor> native_dropout(const at::Tensor& input, double p,
@@ -138,52 +168,164 @@ std::tuple<at::Tensor, at::Tensor> native_dropout(const at::Tensor& input, doubl
     return {input.clone(), mask};
   }
   TORCH_CHECK(p > 0.0 && p <= 1.0, "spyre: dropout probability must be in [0, 1]");
-  at::Tensor keep_cpu = at::empty(input.sizes(), input.options().device(at::kCPU).dtype(at::kFloat));
-  keep_cpu.uniform_(0.0, 1.0, pick_gen(std::nullopt, input.get_device()));
-  mask.copy_(keep_cpu.ge(p));
-  at::Tensor out = at::where(mask, input, at::zeros({}, input.options()));
+  const at::ScalarType st = input.scalar_type();
+  TORCH_CHECK(st == at::kHalf || st == at::kBFloat16 || st == at::kFloat,
+              "spyre: dropout supports float16, bfloat16 and float32");
+  at::Tensor x = contiguous_on_device(input);
+  at::Tensor y = empty_spyre(input.sizes(), st, input.device());
+  const int64_t n = x.numel();
+  if (n == 0) return {y, mask};
   // p == 1 drops everything: scale 0 (as torch), not 0 * inf
-  return {out.mul(p == 1.0 ? 0.0 : 1.0 / (1.0 - p)), mask};
+  const float scale = p == 1.0 ? 0.0f : static_cast<float>(1.0 / (1.0 - p));
+  const auto [seed, offset] = philox_state(std::nullopt, input.get_device(), (n + 3) / 4);
+  c10::DeviceGuard guard(input.device());
+  SPYRE_SPH_CHECK(sph_dropout(to_sph(st), x.data_ptr(), y.data_ptr(),
+                              static_cast<uint8_t*>(mask.data_ptr()), n, static_cast<float>(p),
+                              scale, seed, offset, stream(input.get_device())));
+  return {y, mask};
+}
+
+at::ScalarType cumsum_type(const at::Tensor& self, std::optional<at::ScalarType> dtype);
+
+// Output length of arange as torch computes it: integer arithmetic for
+// int64 outputs, double otherwise.
+int64_t arange_size(const at::Scalar& start, const at::Scalar& end, const at::Scalar& step,
+                    at::ScalarType dt) {
+  if (dt == at::kLong) {
+    const int64_t xs = start.to<int64_t>(), xe = end.to<int64_t>(), st = step.to<int64_t>();
+    TORCH_CHECK(st != 0, "step must be nonzero");
+    TORCH_CHECK((st > 0 && xe >= xs) || (st < 0 && xe <= xs),
+                "upper bound and larger bound inconsistent with step sign");
+    const int64_t sgn = (st > 0) - (st < 0);
+    return (xe - xs + st - sgn) / st;
+  }
+  const double xs = start.to<double>(), xe = end.to<double>(), st = step.to<double>();
+  TORCH_CHECK(st > 0 || st < 0, "step must be nonzero");
+  TORCH_CHECK(std::isfinite(xs) && std::isfinite(xe), "unsupported range: ", xs, " -> ", xe);
+  TORCH_CHECK((st > 0 && xe >= xs) || (st < 0 && xe <= xs),
+              "upper bound and larger bound inconsistent with step sign");
+  const double size_d = std::ceil((xe - xs) / st);
+  TORCH_CHECK(size_d >= 0 && size_d <= static_cast<double>(std::numeric_limits<int64_t>::max()),
+              "invalid size, possible overflow?");
+  return static_cast<int64_t>(size_d);
 }
 
 at::Tensor& arange_out(const at::Scalar& start, const at::Scalar& end, const at::Scalar& step,
                        at::Tensor& out) {
-  at::Tensor host = at::arange(start, end, step, out.options().device(at::kCPU));
-  at::native::resize_output(out, host.sizes());
-  out.copy_(host);
-  return out;
+  const at::ScalarType dt = out.scalar_type();
+  TORCH_CHECK(dt != at::kBool, "spyre: arange does not produce bool");
+  const int64_t n = arange_size(start, end, step, dt);
+  if (out.numel() != n) at::native::resize_output(out, {n});
+  const bool integral = at::isIntegralType(dt, /*includeBool=*/false);
+  return fill_contiguous(out, [&](at::Tensor& t) {
+    SPYRE_SPH_CHECK(sph_arange(to_sph(dt), integral ? 0.0 : start.to<double>(),
+                               integral ? 0.0 : step.to<double>(),
+                               integral ? start.to<int64_t>() : 0,
+                               integral ? step.to<int64_t>() : 0, n, t.data_ptr(),
+                               stream(t.get_device())));
+  });
 }
 
 at::Tensor& cumsum_out(const at::Tensor& self, int64_t dim, std::optional<at::ScalarType> dtype,
                        at::Tensor& out) {
-  at::Tensor host = at::cumsum(self.to(at::kCPU), dim, dtype);
-  at::native::resize_output(out, host.sizes());
-  out.copy_(host);
-  return out;
+  // result dtype as torch: the requested one, int64 for integral (and bool)
+  // inputs, else the input's; the input is converted to it first
+  const at::ScalarType rt = cumsum_type(self, dtype);
+  TORCH_CHECK(out.scalar_type() == rt, "spyre: cumsum out dtype ", out.scalar_type(),
+              " does not match the result dtype ", rt);
+  TORCH_CHECK(rt != at::kBool, "spyre: cumsum does not accumulate in bool");
+  at::native::resize_output(out, self.sizes());
+  if (self.numel() == 0) return out;
+  if (self.dim() == 0) {
+    device_copy(out, self);
+    return out;
+  }
+  const int64_t d = at::maybe_wrap_dim(dim, self.dim());
+  at::Tensor x = contiguous_on_device(self.scalar_type() == rt ? self : self.to(rt));
+  int64_t outer = 1, inner = 1;
+  for (int64_t i = 0; i < d; ++i) outer *= x.size(i);
+  for (int64_t i = d + 1; i < x.dim(); ++i) inner *= x.size(i);
+  const int64_t len = x.size(d);
+  return fill_contiguous(out, [&](at::Tensor& t) {
+    SPYRE_SPH_CHECK(sph_cumsum(to_sph(rt), x.data_ptr(), t.data_ptr(), outer, len, inner,
+                               stream(t.get_device())));
+  });
+}
+
+at::ScalarType cumsum_type(const at::Tensor& self, std::optional<at::ScalarType> dtype) {
+  return dtype.has_value() ? *dtype
+         : at::isIntegralType(self.scalar_type(), /*includeBool=*/true) ? at::kLong
+                                                                         : self.scalar_type();
+}
+
+at::Tensor cumsum(const at::Tensor& self, int64_t dim, std::optional<at::ScalarType> dtype) {
+  at::Tensor out = empty_spyre(self.sizes(), cumsum_type(self, dtype), self.device());
+  return cumsum_out(self, dim, dtype, out);
+}
+
+at::Tensor& cumsum_(at::Tensor& self, int64_t dim, std::optional<at::ScalarType> dtype) {
+  TORCH_CHECK(!dtype.has_value() || *dtype == self.scalar_type(),
+              "spyre: in-place cumsum keeps the tensor's dtype");
+  TORCH_CHECK(cumsum_type(self, std::nullopt) == self.scalar_type(),
+              "spyre: in-place cumsum of ", self.scalar_type(), " would change its dtype");
+  return cumsum_out(self, dim, dtype, self);
 }
 
 at::Tensor& normal_(at::Tensor& self, double mean, double std,
                     std::optional<at::Generator> gen) {
-  at::Tensor host = at::empty(self.sizes(), self.options().device(at::kCPU));
-  host.normal_(mean, std, pick_gen(gen, self.get_device()));
-  self.copy_(host);
-  return self;
+  TORCH_CHECK(std >= 0.0, "normal expects std >= 0.0, but found std ", std);
+  TORCH_CHECK(at::isFloatingType(self.scalar_type()), "spyre: normal_ needs a float tensor");
+  return random_fill(self, SPH_RNG_NORMAL, mean, std, 0, 0, gen);
 }
 
 at::Tensor& uniform_(at::Tensor& self, double from, double to,
                      std::optional<at::Generator> gen) {
-  at::Tensor host = at::empty(self.sizes(), self.options().device(at::kCPU));
-  host.uniform_(from, to, pick_gen(gen, self.get_device()));
-  self.copy_(host);
-  return self;
+  TORCH_CHECK(from <= to, "uniform_ expects to return a [from, to) range, but found from=", from,
+              " > to=", to);
+  TORCH_CHECK(at::isFloatingType(self.scalar_type()), "spyre: uniform_ needs a float tensor");
+  return random_fill(self, SPH_RNG_UNIFORM, from, to, 0, 0, gen);
 }
 
+// random_(from, to): integers in [from, to), or [from, the dtype's largest
+// exactly representable integer] when `to` is None (2^mantissa bits for
+// floating types), as torch's random_.
 at::Tensor& random_from_(at::Tensor& self, int64_t from, std::optional<int64_t> to,
                          std::optional<at::Generator> gen) {
-  at::Tensor host = at::empty(self.sizes(), self.options().device(at::kCPU));
-  host.random_(from, to, pick_gen(gen, self.get_device()));
-  self.copy_(host);
-  return self;
+  const at::ScalarType dt = self.scalar_type();
+  uint64_t range = 0;
+  if (to.has_value()) {
+    TORCH_CHECK(from < *to, "random_ expects 'from' to be less than 'to', but got from=", from,
+                " >= to=", *to);
+    range = static_cast<uint64_t>(*to) - static_cast<uint64_t>(from);
+  } else {
+    int64_t to_inc = 0;
+    switch (dt) {
+      case at::kHalf: to_inc = int64_t(1) << 11; break;
+      case at::kBFloat16: to_inc = int64_t(1) << 8; break;
+      case at::kFloat: to_inc = int64_t(1) << 24; break;
+      case at::kDouble: to_inc = int64_t(1) << 53; break;
+      case at::kBool: to_inc = 1; break;
+      case at::kByte: to_inc = 255; break;
+      case at::kChar: to_inc = 127; break;
+      case at::kShort: to_inc = 32767; break;
+      case at::kInt: to_inc = 2147483647; break;
+      case at::kLong: to_inc = std::numeric_limits<int64_t>::max(); break;
+      default: TORCH_CHECK(false, "spyre: random_ does not support ", dt);
+    }
+    TORCH_CHECK(from <= to_inc, "random_ expects 'from' casted to dtype to be less than or equal "
+                "to 'to_inc' casted to dtype");
+    range = static_cast<uint64_t>(to_inc) - static_cast<uint64_t>(from) + 1;
+    if (range == 0) range = ~uint64_t(0);  // the full 64-bit range (from = int64 min)
+  }
+  return random_fill(self, SPH_RNG_INT, 0.0, 0.0, from, range, gen);
+}
+
+at::Tensor& random_(at::Tensor& self, std::optional<at::Generator> gen) {
+  return random_from_(self, 0, std::nullopt, gen);
+}
+
+at::Tensor& random_to_(at::Tensor& self, int64_t to, std::optional<at::Generator> gen) {
+  return random_from_(self, 0, to, gen);
 }
 
 }  // namespace
@@ -197,9 +339,13 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("native_dropout", TORCH_FN(native_dropout));
   m.impl("arange.start_out", TORCH_FN(arange_out));
   m.impl("cumsum.out", TORCH_FN(cumsum_out));
+  m.impl("cumsum", TORCH_FN(cumsum));
+  m.impl("cumsum_", TORCH_FN(cumsum_));
   m.impl("normal_", TORCH_FN(normal_));
   m.impl("uniform_", TORCH_FN(uniform_));
   m.impl("random_.from", TORCH_FN(random_from_));
+  m.impl("random_", TORCH_FN(random_));
+  m.impl("random_.to", TORCH_FN(random_to_));
 }
 
 }  // namespace spyre

@@ -13,6 +13,7 @@
 // their .out overload: torch's generic functional / in-place wrappers call
 // it.  Values follow torch's CPU semantics: fp16/bf16 inputs are computed
 // in fp32 and rounded once; integer add/sub/mul/compare stay exact.
+#include <ATen/MemoryOverlap.h>
 #include <ATen/native/Resize.h>
 #include <torch/library.h>
 
@@ -91,8 +92,47 @@ void launch_iter(int op, const at::TensorIteratorBase& iter, double alpha, doubl
   SPYRE_SPH_CHECK(sph_pointwise(op, nt - 1, ops.data(), nd, sizes, alpha, beta, stream(dev)));
 }
 
+namespace {
+
+// A same-dtype copy into a dense destination whose source is contiguous
+// along another dimension than the destination (a transposed view made
+// contiguous, a head split or merge): one tiled transpose, coalesced on both
+// sides.  Other copies (and small transposes) take the elementwise engine.
+bool transpose_copy(const at::Tensor& dst, const at::Tensor& src) {
+  if (src.scalar_type() != dst.scalar_type() || !src.sizes().equals(dst.sizes()) ||
+      !is_spyre(src) || src.get_device() != dst.get_device() ||
+      !dst.is_non_overlapping_and_dense())
+    return false;
+  int u = -1, v = -1;
+  for (int64_t d = 0; d < dst.dim(); ++d) {
+    if (dst.size(d) == 1) continue;
+    if (dst.stride(d) == 1 && u < 0) u = static_cast<int>(d);
+    if (src.stride(d) == 1 && v < 0) v = static_cast<int>(d);
+  }
+  if (u < 0 || v < 0 || u == v || dst.size(u) < 16 || dst.size(v) < 16) return false;
+  int64_t bs[4], bsrc[4], bdst[4];
+  int nb = 0;
+  for (int64_t d = 0; d < dst.dim(); ++d) {
+    if (d == u || d == v || dst.size(d) == 1) continue;
+    if (nb == 4) return false;
+    bs[nb] = dst.size(d);
+    bsrc[nb] = src.stride(d);
+    bdst[nb] = dst.stride(d);
+    ++nb;
+  }
+  if (at::get_overlap_status(dst, src) != at::MemOverlapStatus::No) return false;
+  c10::DeviceGuard guard(dst.device());
+  SPYRE_SPH_CHECK(sph_transpose_copy(static_cast<int>(dst.element_size()), src.data_ptr(),
+                                     dst.data_ptr(), dst.size(u), dst.size(v), src.stride(u),
+                                     dst.stride(v), nb, bs, bsrc, bdst, stream(dst.get_device())));
+  return true;
+}
+
+}  // namespace
+
 void device_copy(const at::Tensor& dst, const at::Tensor& src) {
   if (dst.numel() == 0) return;
+  if (transpose_copy(dst, src)) return;
   auto iter = at::TensorIteratorConfig()
                   .add_output(dst)
                   .add_const_input(src)

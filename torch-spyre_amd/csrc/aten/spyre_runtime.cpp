@@ -29,6 +29,8 @@ std::mutex g_stream_mu;
 std::array<hipStream_t, kMaxDevices> g_streams{};
 
 std::array<std::atomic<uint64_t>, kMaxDevices> g_seeds{};
+// Philox counter offset of each device's generator (blocks used so far).
+std::array<std::atomic<uint64_t>, kMaxDevices> g_rng_offsets{};
 
 // Per device: the host address of its error word and the device-side
 // address kernels are given.
@@ -195,10 +197,17 @@ int64_t stick_alloc_nbytes(c10::IntArrayRef sizes, int64_t elem_bytes) {
 void set_seed(int device, uint64_t seed) {
   if (device < 0) {
     for (auto& s : g_seeds) s = seed;
+    for (auto& o : g_rng_offsets) o = 0;
   } else {
     TORCH_CHECK(device < kMaxDevices, "spyre: invalid device index ", device);
     g_seeds[device] = seed;
+    g_rng_offsets[device] = 0;
   }
+}
+
+uint64_t rng_offset_advance(int device, uint64_t blocks) {
+  TORCH_CHECK(device >= 0 && device < kMaxDevices, "spyre: invalid device index ", device);
+  return g_rng_offsets[device].fetch_add(blocks);
 }
 
 uint64_t get_seed(int device) { return g_seeds[device < 0 ? 0 : device].load(); }

@@ -131,7 +131,11 @@ class Graph {
 // bytes for a 0-d tensor.
 int64_t stick_alloc_nbytes(c10::IntArrayRef sizes, int64_t elem_bytes);
 
+// The device generator: Philox4x32-10 keyed by the seed, its counter offset
+// advanced by the blocks each fill uses.  set_seed resets the offset.
 void set_seed(int device, uint64_t seed);
 uint64_t get_seed(int device);
+// Returns the offset of the next fill on `device` and advances it by `blocks`.
+uint64_t rng_offset_advance(int device, uint64_t blocks);
 
 }  // namespace spyre

@@ -508,6 +508,105 @@ extern "C" int sph_gather_rows(const void* table, int64_t num_rows,
 }
 
 // ---------------------------------------------------------------------------
+// Transposing copy: dst[b, v, u] = src[b, u, v] through 64 x 64 LDS tiles
+// ---------------------------------------------------------------------------
+namespace sph {
+namespace {
+
+constexpr int kTT = 64;  // tile edge (elements)
+
+struct TransposeArgs {
+  const void* src;
+  void* dst;
+  int64_t U, V;     // sizes of the dst-contiguous dim u and the src-contiguous dim v
+  int64_t su, dv;   // stride of u in src, of v in dst (elements)
+  int64_t nbatch, tiles_u, tiles_v;
+  int nb;           // batch dims (<= 4), outermost first
+  int64_t bsize[4], bsrc[4], bdst[4];
+};
+
+// One 256-thread workgroup per 64 x 64 tile of one batch entry: the load
+// walks v (contiguous in src) across lanes, the store walks u (contiguous
+// in dst) across lanes, so both sides are coalesced; the tile sits in LDS
+// as [v][u] with one element of padding per row.
+template <typename T>
+__global__ void __launch_bounds__(256) transpose_tile_kernel(TransposeArgs a) {
+  __shared__ T tile[kTT][kTT + 1];
+  const int64_t tu = blockIdx.x % a.tiles_u, tv = blockIdx.x / a.tiles_u;
+  const int64_t u0 = tu * kTT, v0 = tv * kTT;
+  const int tx = threadIdx.x % kTT, ty = threadIdx.x / kTT;
+  for (int64_t b = blockIdx.y; b < a.nbatch; b += gridDim.y) {
+    int64_t rem = b, so = 0, doff = 0;
+    for (int d = a.nb - 1; d >= 0; --d) {
+      const int64_t i = rem % a.bsize[d];
+      rem /= a.bsize[d];
+      so += i * a.bsrc[d];
+      doff += i * a.bdst[d];
+    }
+    const T* src = static_cast<const T*>(a.src) + so;
+    T* dst = static_cast<T*>(a.dst) + doff;
+    const int64_t v = v0 + tx;
+#pragma unroll 4
+    for (int i = ty; i < kTT; i += 4) {
+      const int64_t u = u0 + i;
+      if (u < a.U && v < a.V) tile[tx][i] = src[u * a.su + v];
+    }
+    __syncthreads();
+    const int64_t u = u0 + tx;
+#pragma unroll 4
+    for (int i = ty; i < kTT; i += 4) {
+      const int64_t vv = v0 + i;
+      if (u < a.U && vv < a.V) dst[vv * a.dv + u] = tile[i][tx];
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace
+}  // namespace sph
+
+extern "C" int sph_transpose_copy(int elem_bytes, const void* src, void* dst, int64_t U, int64_t V,
+                                  int64_t su, int64_t dv, int nb, const int64_t* bsizes,
+                                  const int64_t* bsrc_strides, const int64_t* bdst_strides,
+                                  sph_stream_t stream) {
+  SPH_REQUIRE(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4 || elem_bytes == 8,
+              SPH_ERR_INVALID_ARG, "transpose_copy: elem_bytes");
+  SPH_REQUIRE(U >= 0 && V >= 0 && nb >= 0 && nb <= 4, SPH_ERR_INVALID_ARG,
+              "transpose_copy: negative size or more than 4 batch dims");
+  TransposeArgs a{};
+  a.src = src;
+  a.dst = dst;
+  a.U = U;
+  a.V = V;
+  a.su = su;
+  a.dv = dv;
+  a.nb = nb;
+  a.nbatch = 1;
+  for (int d = 0; d < nb; ++d) {
+    SPH_REQUIRE(bsizes[d] >= 0, SPH_ERR_INVALID_ARG, "transpose_copy: negative batch size");
+    a.bsize[d] = bsizes[d];
+    a.bsrc[d] = bsrc_strides[d];
+    a.bdst[d] = bdst_strides[d];
+    a.nbatch *= bsizes[d];
+  }
+  if (U == 0 || V == 0 || a.nbatch == 0) return SPH_OK;
+  a.tiles_u = ceil_div(U, kTT);
+  a.tiles_v = ceil_div(V, kTT);
+  SPH_REQUIRE(a.tiles_u * a.tiles_v < (int64_t(1) << 31), SPH_ERR_TOO_LARGE,
+              "transpose_copy: too many tiles");
+  dim3 grid(static_cast<unsigned>(a.tiles_u * a.tiles_v),
+            static_cast<unsigned>(a.nbatch < 65535 ? a.nbatch : 65535));
+  hipStream_t st = as_stream(stream);
+  switch (elem_bytes) {
+    case 1: transpose_tile_kernel<uint8_t><<<grid, 256, 0, st>>>(a); break;
+    case 2: transpose_tile_kernel<uint16_t><<<grid, 256, 0, st>>>(a); break;
+    case 4: transpose_tile_kernel<uint32_t><<<grid, 256, 0, st>>>(a); break;
+    default: transpose_tile_kernel<uint64_t><<<grid, 256, 0, st>>>(a); break;
+  }
+  return check_launch("sph_transpose_copy");
+}
+
+// ---------------------------------------------------------------------------
 // tril / triu
 // ---------------------------------------------------------------------------
 namespace sph {

@@ -154,20 +154,80 @@ softmax_regs(const TI* __restrict__ x, int64_t ldx, TO* __restrict__ y,
   store_row<TO, TPR, VPT, VEC>(y + row * ldy, cols, t, v);
 }
 
+// (max, sum) state of an online softmax: `s` sums exp2(x - m) over the
+// values seen, m their maximum.  Merging two states rescales both sums to the
+// larger maximum.  A state that has seen only -inf is (-inf, 0); the base
+// 0 in place of an infinite maximum keeps exp2 away from inf - inf.
+__device__ inline void ms_merge(float& m, float& s, float mo, float so) {
+  const float mn = fmaxf(m, mo);
+  const float base = mn == -INFINITY ? 0.f : mn;
+  s = s * __builtin_amdgcn_exp2f(m - base) + so * __builtin_amdgcn_exp2f(mo - base);
+  m = mn;
+}
+
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// (m, s) over the TPR threads of a row group (TPR a multiple of 64), every
+// thread of the group receiving the result: DPP butterflies inside each
+// 16-lane row (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror,
+// row_mirror), the four rows of the wave through readlane, and for groups
+// of several waves one LDS exchange with a single barrier.  `lds_m` and
+// `lds_s` hold blockDim/64 floats each; every thread of the workgroup must
+// reach the call.
+template <int TPR>
+__device__ inline void group_ms(float& m, float& s, float* lds_m, float* lds_s) {
+  static_assert(TPR % kWave == 0, "row groups of whole waves");
+  ms_merge(m, s, dpp_f<0xB1>(m), dpp_f<0xB1>(s));
+  ms_merge(m, s, dpp_f<0x4E>(m), dpp_f<0x4E>(s));
+  ms_merge(m, s, dpp_f<0x141>(m), dpp_f<0x141>(s));
+  ms_merge(m, s, dpp_f<0x140>(m), dpp_f<0x140>(s));
+  float rm[4], rs[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    rm[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), r * 16));
+    rs[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), r * 16));
+  }
+  m = rm[0];
+  s = rs[0];
+#pragma unroll
+  for (int r = 1; r < 4; ++r) ms_merge(m, s, rm[r], rs[r]);
+  if constexpr (TPR > kWave) {
+    constexpr int NW = TPR / kWave;
+    const int wave = threadIdx.x / kWave;
+    if (threadIdx.x % kWave == 0) {
+      lds_m[wave] = m;
+      lds_s[wave] = s;
+    }
+    __syncthreads();
+    const int first = (wave / NW) * NW;
+    m = lds_m[first];
+    s = lds_s[first];
+#pragma unroll
+    for (int k = 1; k < NW; ++k) ms_merge(m, s, lds_m[first + k], lds_s[first + k]);
+  }
+}
+
 // Rows of exactly TPR * VPT * 8 columns with 16-byte aligned rows (c1's
-// [512, 4096] among them): whole chunks without per-chunk bounds tests, and
-// the causal mask and log form chosen once per thread rather than tested per
-// element.  At this size the kernel is latency-bound (one load round trip
-// and two block reductions per row), so instructions on that chain are what
-// it costs: 3.29 against 3.58 us per launch at [512, 4096] for the general
-// kernel.  A row past the end (several rows per workgroup) loads the last
-// row and stores nothing.
+// [512, 4096] among them): whole chunks without per-chunk bounds tests, the
+// causal mask and log form chosen once per thread rather than tested per
+// element, and one combined (max, sum) reduction per row: each thread sums
+// exp2 of its values against its own maximum, and the states merge in one
+// pass (group_ms).  At this size the kernel is latency-bound: a kernel
+// launched back to back costs 1.53 us empty and 2.69 us when one thread
+// loads and stores one value, and this one 2.9-3.0 us at [512, 4096] (on
+// 128 threads x 4 chunks per row, two rows per workgroup), against 3.3 us
+// for two serial block reductions on 256 threads x 2 chunks.  A row past
+// the end (several rows per workgroup) loads the last row and stores
+// nothing.
 template <typename TI, typename TO, int TPR, int VPT>
 __global__ void __launch_bounds__(block_of<TPR>())
 softmax_full(const TI* __restrict__ x, int64_t ldx, TO* __restrict__ y, int64_t ldy,
              int64_t rows, float scale, int flags, int64_t qlen, int64_t qoff) {
   constexpr int BLOCK = block_of<TPR>(), RPB = BLOCK / TPR, COLS = TPR * VPT * 8;
-  __shared__ float lds[BLOCK / kWave];
+  __shared__ float lds_m[BLOCK / kWave], lds_s[BLOCK / kWave];
   const int t = threadIdx.x % TPR;
   int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / TPR;
   const bool valid = row < rows;
@@ -197,35 +257,46 @@ softmax_full(const TI* __restrict__ x, int64_t ldx, TO* __restrict__ y, int64_t 
         m = fmaxf(m, v[i][j]);
       }
   }
-  m = group_reduce<MaxOp, TPR>(m, lds);
+  // this thread's state against its own maximum
+  const float mt = m;
+  const float bt = mt == -INFINITY ? 0.f : mt;
   float s = 0.f;
-  if (flags & SPH_SOFTMAX_LOG) {
+  const bool lg = flags & SPH_SOFTMAX_LOG;
+  if (lg) {
 #pragma unroll
     for (int i = 0; i < VPT; ++i)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) s += __builtin_amdgcn_exp2f(v[i][j] - m);
-    s = group_reduce<SumOp, TPR>(s, lds);
+      for (int j = 0; j < 8; ++j) s += __builtin_amdgcn_exp2f(v[i][j] - bt);
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        v[i][j] = __builtin_amdgcn_exp2f(v[i][j] - bt);
+        s += v[i][j];
+      }
+  }
+  group_ms<TPR>(m, s, lds_m, lds_s);
+  if (!valid) return;
+  if (lg) {
     const float ls = m + log2f(s);
 #pragma unroll
     for (int i = 0; i < VPT; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) v[i][j] = (v[i][j] - ls) * kLn2;
   } else {
+    // e^(x - m) / s = exp2(v - bt) * exp2(bt - m) / s.  A thread whose
+    // values are all masked holds zeros (its factor is 0, never exp2 of a
+    // large difference); a row with no finite value is NaN, as softmax over
+    // all -inf is.
+    const float f = m == -INFINITY   ? NAN
+                    : mt == -INFINITY ? 0.f
+                                      : __builtin_amdgcn_exp2f(bt - m) / s;
 #pragma unroll
     for (int i = 0; i < VPT; ++i)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        v[i][j] = __builtin_amdgcn_exp2f(v[i][j] - m);
-        s += v[i][j];
-      }
-    s = group_reduce<SumOp, TPR>(s, lds);
-    const float inv = 1.0f / s;
-#pragma unroll
-    for (int i = 0; i < VPT; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[i][j] *= inv;
+      for (int j = 0; j < 8; ++j) v[i][j] *= f;
   }
-  if (!valid) return;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) store8<TO>(y + row * ldy + (i * TPR + t) * 8, v[i]);
 }
@@ -557,6 +628,13 @@ int softmax_impl(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
   const TI* xi = static_cast<const TI*>(x);
   TO* yo = static_cast<TO*>(y);
   const bool vec = vec_ok<TI>(x, ldx) && vec_ok<TO>(y, ldy);
+  if (vec && cols == 4096 && rows <= 0xffffffffLL * 2) {
+    // 128 threads x 4 chunks per row, two rows per workgroup (measured best
+    // of the register layouts at [512, 4096])
+    softmax_full<TI, TO, 128, 4><<<grid_rows<128>(rows), block_of<128>(), 0, st>>>(
+        xi, ldx, yo, ldy, rows, scale, flags, qlen, qoff);
+    return check_launch("sph_softmax_rows");
+  }
   const int cfg = pick_cfg(cols);
 #define SPH_SOFTMAX_CASE(I)                                                     \
   case I: {                                                                     \

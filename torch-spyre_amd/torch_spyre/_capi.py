@@ -76,6 +76,15 @@ _SIGS = {
                                    c_i64, c_i64, vp, c_i64, c_i64, vp, c_i64, c_i64, c_i64, c_i64,
                                    c_f32, vp, c_i64, c_i64, vp], c_int),
     "sph_attention_fwd_noalloc_max_bytes": ([], c_i64),
+    "sph_arange": ([c_int, c_f64, c_f64, c_i64, c_i64, c_i64, vp, vp], c_int),
+    "sph_cumsum": ([c_int, vp, vp, c_i64, c_i64, c_i64, vp], c_int),
+    "sph_random_fill": ([c_int, c_int, vp, c_i64, ctypes.c_uint64, ctypes.c_uint64, c_f64, c_f64,
+                         c_i64, ctypes.c_uint64, vp], c_int),
+    "sph_random_blocks": ([c_int, c_int, c_i64, ctypes.c_uint64], c_i64),
+    "sph_transpose_copy": ([c_int, vp, vp, c_i64, c_i64, c_i64, c_i64, c_int, vp, vp, vp, vp],
+                           c_int),
+    "sph_dropout": ([c_int, vp, vp, vp, c_i64, c_f32, c_f32, ctypes.c_uint64, ctypes.c_uint64,
+                     vp], c_int),
     "sph_pointwise": ([c_int, c_int, ctypes.POINTER(Operand), c_int, ctypes.POINTER(c_i64),
                        c_f64, c_f64, vp], c_int),
     "sph_reduce": ([c_int, ctypes.POINTER(Operand), ctypes.POINTER(Operand), c_int,

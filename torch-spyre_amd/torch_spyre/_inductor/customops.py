@@ -284,3 +284,20 @@ def _(x, w):
 @swiglu_mm.register_fake
 def _(x, w):
     return x.new_empty((x.shape[0], w.shape[0] // 2))
+
+
+# ---- transposing copy --------------------------------------------------------
+
+@torch.library.custom_op("spyre::transpose_copy", mutates_args=())
+def transpose_copy(x: torch.Tensor, dims: list[int]) -> torch.Tensor:
+    """x.permute(dims).contiguous(): the reference's transpose data op
+    (torch_spyre/_inductor/codegen/data_ops.py:16-630, "restickify") as a
+    copy.  On spyre the copy runs as one LDS-tiled transpose
+    (sph_transpose_copy) whenever the permutation moves the contiguous
+    dimension; elsewhere it is the plain permute and copy."""
+    return x.permute(dims).contiguous()
+
+
+@transpose_copy.register_fake
+def _(x, dims):
+    return x.new_empty([x.shape[d] for d in dims])

@@ -8,8 +8,9 @@ global config.  Here the passes run through the per-device custom pass of
 tensors, and no conversion is removed: kernels upcast to fp32 internally, so
 the conversions Inductor sees are the ones the program asked for.  The list
 holds the attention fusion (bmm -> softmax -> bmm as one fused kernel,
-fuse_attention.py) and the SwiGLU projection fusion (x W^T -> silu(gate) *
-up as one GEMM, fuse_swiglu.py); a pass is any callable taking the
+fuse_attention.py), the SwiGLU projection fusion (x W^T -> silu(gate) *
+up as one GEMM, fuse_swiglu.py) and transposing copies as one tiled
+transpose (fuse_transpose.py); a pass is any callable taking the
 GraphModule.
 """
 
@@ -22,8 +23,10 @@ from torch._inductor.custom_graph_pass import CustomGraphModulePass, get_hash_fo
 
 from .fuse_attention import fuse_attention
 from .fuse_swiglu import fuse_swiglu
+from .fuse_transpose import fuse_transpose
 
-custom_post_passes: List[Callable[[torch.fx.GraphModule], None]] = [fuse_attention, fuse_swiglu]
+custom_post_passes: List[Callable[[torch.fx.GraphModule], None]] = [fuse_attention, fuse_swiglu,
+                                                                    fuse_transpose]
 
 
 class CustomPostPasses(CustomGraphModulePass):
