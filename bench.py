@@ -653,14 +653,24 @@ def _cpu_setup():
     return torch.get_num_threads(), model
 
 
-def _median_s(fn, reps=10, warmup=3):
-    """Median wall time of `reps` calls after `warmup` calls, and the times."""
+CPU_BUDGET_S = 6.0  # wall time of one CPU figure's repetitions
+
+
+def _median_s(fn, reps=10, warmup=3, budget_s=CPU_BUDGET_S):
+    """Median wall time of up to `reps` calls after up to `warmup` calls,
+    cut so that the calls fit about `budget_s` (the first call, timed, sets
+    the counts; at least one timed call follows it).  Returns (median,
+    times)."""
     import statistics
 
-    for _ in range(warmup):
+    t0 = time.perf_counter()
+    fn()
+    first = time.perf_counter() - t0
+    fit = int(budget_s / max(first, 1e-6))
+    for _ in range(max(0, min(warmup - 1, fit // 4))):
         fn()
     ts = []
-    for _ in range(reps):
+    for _ in range(max(1, min(reps, fit))):
         t0 = time.perf_counter()
         fn()
         ts.append(time.perf_counter() - t0)
@@ -672,10 +682,13 @@ def cpu_per_config():
     same run: the config's function run eagerly by torch on CPU tensors of
     the same shapes and dtype (fp16), as the reference's tests do
     (compare_with_cpu, tests/_inductor/utils_inductor.py:186-198).  c1-c3:
-    full inputs, median of 10 after 3 warmups; c4: the full layer at seq
-    2048, median of 3 after 1; c5: a 2-layer slice of the prefill at the
-    full 4 x 1024 batch and decode steps of a 4-layer slice, each scaled to
-    40 layers (labelled as extrapolated); ~1 minute in total."""
+    full inputs, median of up to 10 after 3 warmups; c4: the full layer at
+    seq 2048, median of up to 3, or a shorter sequence when one full call
+    would take more than a few seconds on this CPU (torch's fp16 matmul is
+    slow on CPUs without fp16 arithmetic); c5: one layer of the prefill and
+    decode steps of a 2-layer slice, scaled to 40 layers.  Each figure is
+    bounded to a few seconds, so the whole section takes well under a
+    minute on any host; every sample is stated."""
     import torch
     import torch.nn.functional as F
 
@@ -685,9 +698,10 @@ def cpu_per_config():
     out = {"threads": threads, "cpu": model}
 
     def hbm(name, nbytes, fn, sample):
-        t, _ = _median_s(fn)
+        _log(f"cpu {name}")
+        t, ts = _median_s(fn)
         out[name] = {"GB/s": round(nbytes / t / 1e9, 2), "ms": round(t * 1e3, 3),
-                     "sample": sample}
+                     "reps": len(ts), "sample": sample}
 
     R, C = 512, 4096
     x = (torch.randn(R, C, generator=_gen(0)) * 4).half()
@@ -708,76 +722,121 @@ def cpu_per_config():
         lambda: (lambda y: (y, y.sum(-1)))(F.gelu(x * w + b)),
         "y = gelu(x * s + b); y.sum(-1), fp16 CPU, full input")
     del x, r
+    _log("cpu c2 bmm")
     A = (torch.rand(32, 2048, 128, generator=_gen(0)) * 2 - 1).half()
     Bm = (torch.rand(32, 128, 2048, generator=_gen(1)) * 2 - 1).half()
-    t, _ = _median_s(lambda: torch.bmm(A, Bm))
+    # batches are independent: time the first nb of them when all 32 would
+    # not fit the budget (one probe batch sets nb)
+    t0 = time.perf_counter()
+    torch.bmm(A[:1], Bm[:1])
+    one = time.perf_counter() - t0
+    nb = 32 if one * 32 <= 2.0 else max(1, min(32, int(2.0 / max(one, 1e-6))))
+    As, Bs = A[:nb], Bm[:nb]
+    t, ts = _median_s(lambda: torch.bmm(As, Bs))
     out["c2_bmm_32x2048x2048x128"] = {
-        "TFLOP/s": round(2 * 32 * 2048 * 2048 * 128 / t / 1e12, 4), "ms": round(t * 1e3, 2),
-        "sample": "torch.bmm, fp16 CPU, full input"}
-    # c4: embedding + one layer at seq 2048, fp16
+        "TFLOP/s": round(2 * nb * 2048 * 2048 * 128 / t / 1e12, 4), "ms": round(t * 1e3, 2),
+        "reps": len(ts),
+        "sample": "torch.bmm, fp16 CPU, " + ("full input" if nb == 32 else
+                                             f"batches 0..{nb} of 32")}
+    # c4: embedding + one layer, fp16; the sequence length is cut when a
+    # full-length call would not fit the budget
     cfg = D.C4
-    S = 2048
     params = D.init_params(cfg, "cpu", pool_elems=1 << 24)
-    cos, sin = D.rope_tables(cfg, S, "cpu")
-    mask = D.causal_mask(cfg, S, "cpu")
-    tok = torch.randint(0, cfg.vocab, (1, S), generator=_gen(0))
     with torch.no_grad():
-        t, _ = _median_s(lambda: D.block_forward(tok, params, cos, sin, mask, cfg), reps=3,
-                         warmup=1)
+        S = 2048
+        for S in (256, 512, 1024, 2048):
+            cos, sin = D.rope_tables(cfg, S, "cpu")
+            mask = D.causal_mask(cfg, S, "cpu")
+            tok = torch.randint(0, cfg.vocab, (1, S), generator=_gen(0))
+            _log(f"cpu c4 layer, seq {S}")
+            t0 = time.perf_counter()
+            D.block_forward(tok, params, cos, sin, mask, cfg)
+            if S == 2048 or (time.perf_counter() - t0) * 2.5 > 2.0:
+                break
+        t, ts = _median_s(lambda: D.block_forward(tok, params, cos, sin, mask, cfg), reps=3,
+                          warmup=1)
     out["c4_layer_prefill"] = {"tok/s": round(S / t, 1), "ms": round(t * 1e3, 1),
-                               "sample": "decoder.block_forward (embedding + 1 layer), seq "
-                                         "2048, fp16 CPU, median of 3"}
-    # c5: layer slices of the model at its batch and lengths, scaled to 40
+                               "reps": len(ts),
+                               "sample": f"decoder.block_forward (embedding + 1 layer), seq {S}"
+                                         f"{'' if S == 2048 else ' of 2048'}, fp16 CPU"}
+    del params
+    # c5: one layer of the prefill at batch 4 (or fewer rows), and decode
+    # steps of a 2-layer slice; per-layer times x 40 + the LM head
     B, S, T = 4, 1024, 128
     sl = D.DecoderConfig(n_layers=2)
     params = D.init_params(sl, "cpu", pool_elems=1 << 24)
     cos, sin = D.rope_tables(sl, S + T, "cpu")
     mask = D.causal_mask(sl, S, "cpu")
-    prompt = torch.randint(0, sl.vocab, (B, S), generator=_gen(1))
-    cache = D.new_cache(sl, B, S + T, "cpu")
+    w0 = params["layers"][0]
     with torch.no_grad():
+        # one layer over the first Sp prompt positions of one sequence
+        # (causal: the same work as a prompt of length Sp), Sp doubled from
+        # 128 while the next call fits the budget; time per token is scaled
+        # to 4 x 1024, which undercounts attention's quadratic part, so the
+        # CPU figure is an upper bound of the CPU's throughput
+        Sp, one = 128, None
+        for sp in (128, 256, 512, 1024):
+            if one is not None and one * 2.2 > 3.0:
+                break
+            Sp = sp
+            h = torch.randn(1, Sp, sl.hidden, generator=_gen(2)).half()
+            _log(f"cpu c5 prefill layer (1 x {Sp})")
+            t0 = time.perf_counter()
+            D.layer_forward(h, w0, cos[:Sp], sin[:Sp], D.causal_mask(sl, Sp, "cpu"), sl)
+            one = time.perf_counter() - t0
+        hl = torch.randn(1, sl.hidden, generator=_gen(3)).half()
+        t_head, _ = _median_s(lambda: D.lm_logits(hl, params, sl), reps=3, warmup=1, budget_s=3.0)
+        pre40 = (one * 40 + t_head) * (B * S / Sp)
+        _log("cpu c5 decode steps (2-layer slice)")
+        cache = D.new_cache(sl, B, S + T, "cpu")
+        feed = torch.randint(0, sl.vocab, (B,), generator=_gen(4))
+        D.decode_step(feed, S, params, cos, sin, cache, sl)
         t0 = time.perf_counter()
-        logits = D.prefill(prompt, params, cos, sin, mask, cache, sl)
-        t_pre = time.perf_counter() - t0
-        h = torch.randn(B, sl.hidden, generator=_gen(2)).half()
-        t_head, _ = _median_s(lambda: D.lm_logits(h, params, sl), reps=3, warmup=1)
-        feed = logits.argmax(-1)
-        steps = 4
-        t0 = time.perf_counter()
+        steps = 2
         for i in range(steps):
-            feed = D.decode_step(feed, S + i, params, cos, sin, cache, sl).argmax(-1)
+            D.decode_step(feed, S + 1 + i, params, cos, sin, cache, sl)
         t_dec = (time.perf_counter() - t0) / steps
-    per_layer_pre = (t_pre - t_head) / sl.n_layers
-    per_layer_dec = (t_dec - t_head) / sl.n_layers
-    pre40 = per_layer_pre * 40 + t_head
-    dec40 = per_layer_dec * 40 + t_head
+        h4 = torch.randn(B, sl.hidden, generator=_gen(5)).half()
+        t_head4, _ = _median_s(lambda: D.lm_logits(h4, params, sl), reps=3, warmup=1,
+                               budget_s=3.0)
+    dec40 = (t_dec - t_head4) / sl.n_layers * 40 + t_head4
     out["c5_prefill_extrapolated"] = {
         "tok/s": round(B * S / pre40, 1), "s": round(pre40, 2),
-        "sample": "decoder.prefill of a 2-layer slice at batch 4 x 1024, fp16 CPU, one run; "
-                  "per-layer time x 40 + the LM head (extrapolated)"}
+        "sample": f"one decoder layer over 1 x {Sp} prompt positions, fp16 CPU, one call; "
+                  "x 40 layers + the LM head, scaled by tokens to 4 x 1024 (extrapolated)"}
     out["c5_decode_extrapolated"] = {
         "tok/s": round(B / dec40, 2), "ms_per_step": round(dec40 * 1e3, 1),
-        "sample": f"decoder.decode_step of the 2-layer slice, {steps} steps after its prefill, "
-                  "fp16 CPU; per-layer time x 40 + the LM head (extrapolated)"}
+        "sample": f"decoder.decode_step of a 2-layer slice, batch 4, {steps} steps, fp16 CPU; "
+                  "per-layer time x 40 + the LM head (extrapolated)"}
     return out
 
 
 def cpu_baseline_gemm(a, b):
-    """BASELINE's CPU baseline of the headline: the reference's CPU path
+    """The CPU baseline of the headline: the reference's CPU path
     fn(*cpu_args) = torch.mm eager on the same fp16 tensors on this host's
     CPU (what compare_with_cpu runs, tests/_inductor/utils_inductor.py:190),
-    full 4096^3 input, median of 10 after 3 warmups."""
+    median of up to 10 after 3 warmups.  Full 4096^3 when a call takes at
+    most ~1.5 s here; otherwise the first rows of A (a GEMM's time is linear
+    in its rows: a 16-row probe sets how many rows fill about 4 s), stated in
+    `sample`."""
     import torch
 
     threads, model = _cpu_setup()
     ac, bc = a.cpu(), b.cpu()
-    t, ts = _median_s(lambda: torch.mm(ac, bc))
-    flop = 2.0 * ac.shape[0] * ac.shape[1] * bc.shape[1]
+    t0 = time.perf_counter()
+    torch.mm(ac[:16], bc)
+    est = (time.perf_counter() - t0) * (ac.shape[0] / 16)
+    rows = ac.shape[0]
+    if est > 1.5:
+        rows = max(16, int(ac.shape[0] * 4.0 / est) // 16 * 16)
+    a_s = ac[:rows]
+    t, ts = _median_s(lambda: torch.mm(a_s, bc), budget_s=12.0)
+    flop = 2.0 * rows * ac.shape[1] * bc.shape[1]
+    what = "full 4096^3" if rows == ac.shape[0] else f"rows 0..{rows} of A (4096 x 4096 B)"
     return {"value": round(flop / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
             "kind": "reference",
-            "sample": f"torch.mm eager on the same fp16 A, B on the CPU ({model}), full "
-                      f"4096^3, median of 10 after 3 warmups ({min(ts) * 1e3:.0f}-"
-                      f"{max(ts) * 1e3:.0f} ms)"}
+            "sample": f"torch.mm eager on the same fp16 A, B on the CPU ({model}), {what}, "
+                      f"median of {len(ts)} ({min(ts) * 1e3:.0f}-{max(ts) * 1e3:.0f} ms)"}
 
 
 def cpu_oracle_gemm(a, b, seconds=3.0):

@@ -200,6 +200,21 @@ int sph_gemm_strided_batched(sph_dtype dtype, int trans_a, int trans_b,
                              int64_t stride_d, int epilogue,
                              sph_stream_t stream);
 
+/* D = rms_norm(X) W^T for decode shapes (1 <= m <= 8 rows): row i of X
+ * [m, k] is normalised as X[i] * norm_w * rsqrt(mean(X[i]^2) + eps) inside
+ * the weight-stream kernels (no separate norm kernel, no normalised copy of
+ * X): norm_w multiplies each chunk of X as it is loaded (rounded to the
+ * dtype), the row scale multiplies the finished sums.  W [n, k] (or, with
+ * swiglu, [2n, k]: gate rows then up rows, D = silu(g) * u) is the
+ * nn.Linear weight layout.  F16 / BF16; 64 <= k <= 8192, k % 8 == 0, rows
+ * of X, norm_w and W 16-byte aligned.
+ * Replaces: the reference's RMSNorm composite (pow / mean / add / rsqrt /
+ * mul, Metadata.yaml:236-253, spyre_torch_ops.cpp:456-474) followed by
+ * spyre__mm_default (spyre_torch_ops.cpp:214-293). */
+int sph_gemm_rmsnorm(sph_dtype dtype, int64_t m, int64_t n, int64_t k, const void* a, int64_t lda,
+                     const void* norm_w, float eps, const void* w, int64_t ldw, void* d,
+                     int64_t ldd, int swiglu, sph_stream_t stream);
+
 /* D[m, j] = silu(sum_k A[m, k] W[j, k]) * (sum_k A[m, k] W[n + j, k]) for
  * j < n: the gate and up projections of a SwiGLU MLP from one weight
  * matrix W [2n, k] (gate rows first), both K-contiguous, and the

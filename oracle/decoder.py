@@ -20,7 +20,13 @@ query rows of a KV head a multiple of 128 - the scores are not rounded at
 all, only the probabilities before the second product; where it runs the
 gate / up projection and silu(gate) * up as one kernel - rows % 256 == 0,
 intermediate % 128 == 0, hidden % 64 == 0, or at most 8 rows with
-64 <= hidden <= 8192 - gate and up are not rounded either).
+64 <= hidden <= 8192 - gate and up are not rounded either).  At most 8 rows
+(a decode step) the compiled program also folds each RMSNorm into the
+projection that reads it (rows <= 8, hidden % 8 == 0, 64 <= hidden <= 8192:
+x * w rounds to fp16, the float32 sums are scaled by the row's
+1 / rms(x), so the normalized activations are never rounded) and each
+residual add into the projection that feeds it (at most 8 rows: h + x W^T
+rounds once, from the float32 sums).
 
 Pinned by tests/test_decoder.py against torch's CPU float32 ops with
 F.scaled_dot_product_attention (is_causal, enable_gqa) as an independent
@@ -48,6 +54,20 @@ def _rmsnorm(x, w, eps, act):
     x = np.asarray(x, np.float32)
     ms = np.mean(x.astype(np.float64) ** 2, axis=-1, keepdims=True)
     return _r(x / np.sqrt(ms + eps).astype(np.float32) * np.asarray(w, np.float32), act)
+
+
+def _norm_linear(h, nw, w, eps, act):
+    """RMSNorm folded into a projection (float32 result, not rounded): the
+    sums of fp16(h * nw) against w's rows, scaled by rsqrt(mean(h^2) + eps)
+    of each row of h."""
+    return O.rmsnorm_linear(h, nw, w, eps, act)
+
+
+def _decode_fusions(rows, hidden, fused):
+    """(norm folded into the projections, residual folded into the
+    projections) for a compiled program over `rows` token rows."""
+    small = fused and rows <= 8
+    return small and hidden % 8 == 0 and 64 <= hidden <= 8192, small
 
 
 def rope_tables(head_dim, positions, theta=1e4):
@@ -101,10 +121,14 @@ def layer(h, w, cfg, positions, act=np.float16, kv_prefix=None, fused=False):
     Returns (h_out, (k, v) of all positions)."""
     B, S, _ = h.shape
     H, Hkv, D = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
-    x = _rmsnorm(h, w["attn_norm"], cfg.eps, act)
-    q = _linear(x, w["wq"], act).reshape(B, S, H, D)
-    k = _linear(x, w["wk"], act).reshape(B, S, Hkv, D)
-    v = _linear(x, w["wv"], act).reshape(B, S, Hkv, D)
+    fold_norm, fold_res = _decode_fusions(B * S, cfg.hidden, fused)
+    if fold_norm:
+        q, k, v = (_r(_norm_linear(h, w["attn_norm"], w[n], cfg.eps, act), act)
+                   for n in ("wq", "wk", "wv"))
+    else:
+        x = _rmsnorm(h, w["attn_norm"], cfg.eps, act)
+        q, k, v = (_linear(x, w[n], act) for n in ("wq", "wk", "wv"))
+    q, k, v = q.reshape(B, S, H, D), k.reshape(B, S, Hkv, D), v.reshape(B, S, Hkv, D)
     cos, sin = rope_tables(D, positions, cfg.rope_theta)
     q, k = _rope(q, cos, sin, act, fused), _rope(k, cos, sin, act, fused)
     k_pos = np.asarray(positions)
@@ -116,18 +140,23 @@ def layer(h, w, cfg, positions, act=np.float16, kv_prefix=None, fused=False):
     # shapes fit (head dim 128, stacked query rows per KV head % 128 == 0)
     fused_attn = fused and kv_prefix is None and D == 128 and (S * (H // Hkv)) % 128 == 0
     a = attention(q, k, v, np.asarray(positions), k_pos, act, fused, scores_fp32=fused_attn)
-    h = _r(h + _linear(a, w["wo"], act), act)
-    x = _rmsnorm(h, w["mlp_norm"], cfg.eps, act)
+    res_act = None if fold_res else act
+    h = _r(h + _linear(a, w["wo"], res_act), act)
     # the compiled program's fused SwiGLU kernels keep gate / up in fp32
     # (tiled GEMM for whole 256-row blocks, weight stream for <= 8 rows)
     fused_mlp = fused and (((B * S) % 256 == 0 and cfg.intermediate % 128 == 0 and
                             cfg.hidden % 64 == 0) or
                            (B * S <= 8 and cfg.hidden % 8 == 0 and 64 <= cfg.hidden <= 8192))
     lin_act = None if fused_mlp else act
-    gte = _linear(x, w["wg"], lin_act)
-    up = _linear(x, w["wu"], lin_act)
+    if fold_norm:
+        gte = _norm_linear(h, w["mlp_norm"], w["wg"], cfg.eps, act)
+        up = _norm_linear(h, w["mlp_norm"], w["wu"], cfg.eps, act)
+    else:
+        x = _rmsnorm(h, w["mlp_norm"], cfg.eps, act)
+        gte = _linear(x, w["wg"], lin_act)
+        up = _linear(x, w["wu"], lin_act)
     m = _r((O.silu(gte) if fused else _r(O.silu(gte), act)) * up, act)
-    return _r(h + _linear(m, w["wd"], act), act), (k, v)
+    return _r(h + _linear(m, w["wd"], res_act), act), (k, v)
 
 
 def embed(tokens, table, act=np.float16):
@@ -143,14 +172,21 @@ def block(tokens, params, cfg, act=np.float16, fused=False):
     return h
 
 
-def logits(h_last, params, cfg, act=np.float16):
+def logits(h_last, params, cfg, act=np.float16, fused=False):
+    """Final RMSNorm + LM head on h_last [B, hidden]; fused: the compiled
+    decode step's program (the norm folded into the head for <= 8 rows)."""
+    if _decode_fusions(np.asarray(h_last).shape[0], cfg.hidden, fused)[0]:
+        return _r(_norm_linear(h_last, params["final_norm"], params["lm_head"], cfg.eps, act),
+                  act)
     x = _rmsnorm(h_last, params["final_norm"], cfg.eps, act)
     return _linear(x, params["lm_head"], act)
 
 
 def generate_teacher_forced(prompt, teacher, params, cfg, act=np.float16, fused=False):
     """Prefill `prompt` [B, S], then feed `teacher` [B, T] one token at a
-    time.  Returns logits [T+1, B, vocab] (prefill's last position first)."""
+    time.  Returns logits [T+1, B, vocab] (prefill's last position first;
+    its LM head runs eagerly, the decode steps' heads in the step's
+    program)."""
     prompt = np.asarray(prompt)
     B, S = prompt.shape
     h = embed(prompt, params["embed"], act)
@@ -164,5 +200,5 @@ def generate_teacher_forced(prompt, teacher, params, cfg, act=np.float16, fused=
         for i, w in enumerate(params["layers"]):
             h, caches[i] = layer(h, w, cfg, np.array([S + t]), act, kv_prefix=caches[i],
                                  fused=fused)
-        out.append(logits(h[:, -1], params, cfg, act))
+        out.append(logits(h[:, -1], params, cfg, act, fused=fused))
     return np.stack(out, 0)

@@ -51,7 +51,15 @@ def softmax(x, axis=-1, scale=1.0, causal_q_len=0, causal_offset=0, log=False):
 
 
 def _round_to(x, dtype):
-    return np.asarray(x, dtype=np.float32).astype(dtype).astype(np.float32)
+    """float32 values rounded to `dtype` (a numpy dtype, or "bfloat16":
+    round to nearest even on the upper 16 bits of the float32 pattern)."""
+    x = np.asarray(x, dtype=np.float32)
+    if isinstance(dtype, str) and dtype == "bfloat16":
+        b = x.view(np.uint32).astype(np.uint64)
+        r = (b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFF0000
+        out = r.astype(np.uint32).view(np.float32)
+        return np.where(np.isnan(x), x, out)
+    return x.astype(dtype).astype(np.float32)
 
 
 def rmsnorm(x, weight=None, eps=1e-5, residual=None, act_dtype=np.float16):
@@ -70,6 +78,27 @@ def rmsnorm(x, weight=None, eps=1e-5, residual=None, act_dtype=np.float16):
     if weight is not None:
         y = y * _f32(weight)
     return y.astype(np.float32), h
+
+
+def rmsnorm_linear(x, norm_w, w, eps=1e-5, act_dtype=np.float16, swiglu=False):
+    """rms_norm(x, norm_w) @ w.T with the norm folded into the product (the
+    decode-step kernel, no reference counterpart: the reference runs the
+    norm's composite and spyre__mm_default, spyre_torch_ops.cpp:214-293):
+    x * norm_w is rounded to act_dtype (None: not rounded), the float32 sums
+    are scaled by each row's rsqrt(mean(x^2) + eps).  swiglu: w stacks gate
+    and up rows [2n, K] and the result is silu(gate) * up.  Float32 result,
+    not rounded."""
+    h = _f32(x)
+    ms = np.mean(h.astype(np.float64) ** 2, axis=-1, keepdims=True)
+    rs = (1.0 / np.sqrt(ms + eps)).astype(np.float32)
+    xw = h * _f32(norm_w)
+    if act_dtype is not None:
+        xw = _round_to(xw, act_dtype)
+    y = np.matmul(xw, _f32(w).T) * rs
+    if swiglu:
+        n = y.shape[-1] // 2
+        y = silu(y[..., :n]) * y[..., n:]
+    return y.astype(np.float32)
 
 
 def layernorm(x, weight=None, bias=None, eps=1e-5, residual=None, act_dtype=np.float16):

@@ -174,6 +174,30 @@ def test_fused_mode_is_exact_math_without_rounding():
     np.testing.assert_allclose(OD.block(tok, p, FUSED, act=None, fused=True),
                                OD.block(tok, p, FUSED, act=None, fused=False),
                                rtol=1e-5, atol=1e-6)
+    # decode steps (<= 8 rows): RMSNorm and the residual adds folded into
+    # the projections
+    teacher = _tokens(4, 2, FUSED.vocab, seed=3).numpy()
+    np.testing.assert_allclose(
+        OD.generate_teacher_forced(tok[:, :16], teacher, p, FUSED, act=None, fused=True),
+        OD.generate_teacher_forced(tok[:, :16], teacher, p, FUSED, act=None, fused=False),
+        rtol=1e-4, atol=1e-5)
+
+
+def test_decode_folds_change_only_rounding_points():
+    # the decode-step folds (norm into the projection, residual into its
+    # sums) move rounding points: one decode layer in fp16 differs from the
+    # eager rounding model, by at most a few fp16 ulps of the activations
+    p = _np(D.init_params(FUSED, "cpu", seed=8))
+    w = p["layers"][0]
+    h = np.random.default_rng(5).standard_normal((4, 1, FUSED.hidden)).astype(np.float16)
+    pre = OD.layer(np.random.default_rng(6).standard_normal((4, 8, FUSED.hidden))
+                   .astype(np.float16), w, FUSED, np.arange(8))[1]
+    got, _ = OD.layer(h, w, FUSED, np.array([8]), kv_prefix=pre, fused=True)
+    want, _ = OD.layer(h, w, FUSED, np.array([8]), kv_prefix=pre, fused=False)
+    exact, _ = OD.layer(h, w, FUSED, np.array([8]), act=None, kv_prefix=pre, fused=False)
+    assert np.abs(got - want).max() > 0
+    np.testing.assert_allclose(got, exact, rtol=1e-2, atol=1e-2)
+    assert np.abs(got - exact).mean() <= np.abs(want - exact).mean() * 1.05
 
 
 def test_fused_rounding_model_tracks_independent_fp32_decoder():

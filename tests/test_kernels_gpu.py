@@ -6,6 +6,7 @@ Bars: bit-exact for layout / copy / gather / integer work; rtol = atol = 1e-2
 against the oracle's fp32 result rounded to the output dtype for fp16 / bf16
 floating point (fp32 outputs: 1e-4)."""
 
+import ctypes
 import math
 
 import numpy as np
@@ -526,6 +527,75 @@ def test_gemm_splitk_tail(m, n, k, tb, epi):
                   epilogue={0: "none", 2: "gelu", 3: "silu"}[epi])
     assert_close_fp(outs[0], want, what="split-K tail")
     torch.testing.assert_close(outs[0].float(), outs[1].float(), rtol=2e-3, atol=2e-3)
+
+
+@pytest.mark.parametrize("m,n,k,swiglu,pad,dtype", [
+    (4, 6144, 4096, 0, 0, torch.float16),      # QKV shape: small-M kernel
+    (4, 12800, 4096, 1, 0, torch.float16),     # gate / up: weight stream, SwiGLU
+    (4, 49155, 4096, 0, 8, torch.float16),     # LM head: weight stream
+    (1, 200, 264, 0, 8, torch.bfloat16),       # narrow, ragged, one row
+    (8, 1000, 8192, 1, 0, torch.bfloat16),     # longest rows, eight rows
+    (3, 25600, 1024, 0, 0, torch.float16)])
+def test_gemm_rmsnorm(m, n, k, swiglu, pad, dtype):
+    # rms_norm(x) W^T with the norm as the prologue of the decode GEMM:
+    # against the oracle's fold (x * w staged in the activation type, sums
+    # scaled by 1 / rms) at fp16's output rounding, and the exact composite
+    # at the north star's 1e-2; row 1 is tiny so eps carries weight
+    _log(f"gemm rmsnorm {m}x{n}x{k} swiglu={swiglu} pad={pad} {dtype}")
+    X = uniform((m, k), k=71) * 3
+    if m > 1:
+        X[1] *= 1e-3
+    X = X.to(dtype)
+    nw = (1 + 0.1 * uniform((k,), k=72)).to(dtype)
+    N = 2 * n if swiglu else n
+    W = (uniform((N, k), k=73) * 0.05).to(dtype)
+    xd = torch.zeros(m, k + pad, dtype=dtype, device=DEV)
+    xd[:, :k] = X.to(DEV)
+    wd = torch.zeros(N, k + pad, dtype=dtype, device=DEV)
+    wd[:, :k] = W.to(DEV)
+    nwd = nw.to(DEV)
+    d = torch.full((m, n + pad), 7.0, dtype=dtype, device=DEV)
+    _capi.call("sph_gemm_rmsnorm", DT[dtype], m, n, k, _p(xd), k + pad, _p(nwd), 1e-5, _p(wd),
+               k + pad, _p(d), n + pad, swiglu, _stream())
+    _sync()
+    xf, nf, wf = X.float().numpy(), nw.float().numpy(), W.float().numpy()
+    act = np.float16 if dtype == torch.float16 else "bfloat16"
+    fold = O.rmsnorm_linear(xf, nf, wf, 1e-5, act_dtype=act, swiglu=bool(swiglu))
+    tight = dict(rtol=4e-3, atol=1e-3) if dtype == torch.float16 else dict(rtol=1.6e-2, atol=4e-3)
+    assert_close_fp(d[:, :n], fold, out_dtype=dtype, what="rmsnorm fold", **tight)
+    exact = O.rmsnorm_linear(xf, nf, wf, 1e-5, act_dtype=None, swiglu=bool(swiglu))
+    if dtype == torch.float16:
+        assert_close_fp(d[:, :n], exact, out_dtype=dtype, what="rmsnorm composite")
+    else:
+        # bf16 staging carries 2^-9 per term, as the eager path's rounded
+        # normalized activations do: relative L2 against the exact result
+        got = d[:, :n].float().cpu().numpy()
+        rel = np.linalg.norm(got - exact) / np.linalg.norm(exact)
+        assert rel <= 1e-2, f"rmsnorm composite (bf16): relative L2 {rel:.2e}"
+    if pad:
+        assert bool((d[:, n:] == 7.0).all()), "padding columns written"
+
+
+def test_gemm_rmsnorm_op_and_rejects():
+    # the ATen op on spyre tensors (decode rows: one kernel; more rows: the
+    # norm and the product as separate ops) against the CPU composite
+    _log("spyre rms_norm_mm op")
+    for m in (4, 12):
+        x = (uniform((m, 512), k=81) * 2).half()
+        nw = (1 + 0.1 * uniform((512,), k=82)).half()
+        w = (uniform((384, 512), k=83) * 0.05).half()
+        for sw in (False, True):
+            got = torch.ops.spyre.rms_norm_mm(x.to("spyre"), nw.to("spyre"), 1e-5,
+                                              w.to("spyre"), sw).cpu()
+            want = torch.ops.spyre.rms_norm_mm(x.float(), nw.float(), 1e-5, w.float(), sw)
+            torch.testing.assert_close(got.float(), want, rtol=1e-2, atol=1e-2)
+    x = torch.zeros(9, 64, dtype=torch.float16, device=DEV)
+    w = torch.zeros(64, 64, dtype=torch.float16, device=DEV)
+    nw = torch.zeros(64, dtype=torch.float16, device=DEV)
+    d = torch.zeros(9, 64, dtype=torch.float16, device=DEV)
+    rc = _capi.lib().sph_gemm_rmsnorm(_capi.F16, 9, 64, 64, _p(x), 64, _p(nw),
+                                      ctypes.c_float(1e-5), _p(w), 64, _p(d), 64, 0, _stream())
+    assert rc == 1002  # SPH_ERR_UNSUPPORTED: more than 8 rows
 
 
 def test_gemm_swiglu_rejects_unfit_shapes():

@@ -188,6 +188,27 @@ def test_rmsnorm_vs_torch_and_invariant():
     np.testing.assert_allclose(np.sqrt((y1.astype(np.float64) ** 2).mean(-1)), 1.0, rtol=1e-5)
 
 
+def test_rmsnorm_linear_vs_torch_composite():
+    # the folded norm: unrounded, it is torch's rms_norm then linear; with
+    # fp16 staging it moves only the rounding of x * w; swiglu splits the
+    # stacked product; eps matters for rows of tiny values
+    x = randn((5, 256), k=21)
+    x[3] *= 1e-3
+    nw = randn((256,), k=22, scale=0.1, mean=1.0)
+    w = randn((96, 256), k=23, scale=0.05)
+    ref = F.linear(F.rms_norm(x.float(), (256,), nw.float(), 1e-5), w.float()).numpy()
+    got = O.rmsnorm_linear(x.numpy(), nw.numpy(), w.numpy(), 1e-5, act_dtype=None)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+    wrong_eps = O.rmsnorm_linear(x.numpy(), nw.numpy(), w.numpy(), 1e-6, act_dtype=None)
+    assert np.abs(wrong_eps[3] - ref[3]).max() > 1e-2
+    half = O.rmsnorm_linear(x.numpy(), nw.numpy(), w.numpy(), 1e-5)
+    np.testing.assert_allclose(half, ref, rtol=1e-2, atol=1e-2)
+    assert np.abs(half - ref).max() > 0
+    sw = O.rmsnorm_linear(x.numpy(), nw.numpy(), w.numpy(), 1e-5, act_dtype=None, swiglu=True)
+    np.testing.assert_allclose(sw, F.silu(torch.from_numpy(ref[:, :48])).numpy() * ref[:, 48:],
+                               rtol=1e-5, atol=1e-6)
+
+
 def test_layernorm_vs_torch_and_invariants():
     x, r = randn((16, 300), k=4), randn((16, 300), k=5)
     w = randn((300,), k=6, scale=0.02, mean=1.0)
@@ -311,3 +332,11 @@ def test_attention_vs_torch_sdpa():
     np.testing.assert_allclose(got, want.numpy(), rtol=1e-5, atol=1e-5)
     bad = O.attention(q.numpy(), v.numpy(), k.numpy(), scale, mask=mask.numpy())
     assert not np.allclose(bad, want.numpy(), rtol=1e-3, atol=1e-3)
+
+
+def test_round_to_bfloat16_matches_torch():
+    x = np.concatenate([randn((4096,), k=31, scale=50.0).float().numpy(),
+                        np.array([0.0, -0.0, 1.0, 3.0039062, -3.0039062, 65504.0, 1e-40,
+                                  np.inf, -np.inf], np.float32)])
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(O._round_to(x, "bfloat16"), want)

@@ -24,8 +24,10 @@ void launch_kernel(int64_t handle, const std::vector<at::Tensor>& args, int64_t 
                    int64_t block, const std::vector<int64_t>& extents);
 void launch_kernel_stored(int64_t handle, const std::vector<at::Tensor>& args);
 void launch_kernel_path(const std::string& path, const std::vector<at::Tensor>& args);
-// Fused SwiGLU projection (ops_gemm.cpp).
+// Fused SwiGLU projection and RMSNorm-prologue GEMM (ops_gemm.cpp).
 at::Tensor gemm_swiglu(const at::Tensor& x, const at::Tensor& w);
+at::Tensor gemm_rmsnorm(const at::Tensor& x, const at::Tensor& norm_w, double eps,
+                        const at::Tensor& w, bool swiglu);
 // Fused attention (ops_attention.cpp).
 at::Tensor attention_fwd(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                          const c10::optional<at::Tensor>& mask, double scale, int64_t causal_q,
@@ -66,6 +68,10 @@ PYBIND11_MODULE(_C, m) {
         "[B, sk, 128], mask [mq, sk] / [B or 1, mq, sk] or None; fp16 / bf16).");
   m.def("gemm_swiglu", &spyre::gemm_swiglu, py::arg("x"), py::arg("w"),
         "silu(x w[:n]^T) * (x w[n:]^T) on the spyre stream (x [M, K], w [2n, K]).");
+  m.def("gemm_rmsnorm", &spyre::gemm_rmsnorm, py::arg("x"), py::arg("norm_w"), py::arg("eps"),
+        py::arg("w"), py::arg("swiglu") = false,
+        "rms_norm(x) w^T, or with swiglu silu(gate) * up of the stacked weight, on the spyre "
+        "stream (x [M, K], M <= 8 in one weight-stream kernel).");
   m.def("device_count", []() { return spyre::device_count(); });
   m.def("current_device", []() { return spyre::current_device(); });
   m.def("set_device", [](int d) { spyre::set_device(d); });

@@ -230,6 +230,48 @@ at::Tensor gemm_swiglu(const at::Tensor& x_in, const at::Tensor& w_in) {
   return out;
 }
 
+// rms_norm(x) w^T (swiglu: silu(gate) * up of the stacked [2n, K] weight)
+// for decode rows (M <= 8) in one weight-stream launch (sph_gemm_rmsnorm);
+// other shapes run the norm and the product as separate spyre ops.
+at::Tensor gemm_rmsnorm(const at::Tensor& x_in, const at::Tensor& norm_w_in, double eps,
+                        const at::Tensor& w_in, bool swiglu) {
+  TORCH_CHECK(is_spyre(x_in) && is_spyre(norm_w_in) && is_spyre(w_in),
+              "spyre rms_norm_mm: spyre tensors expected");
+  TORCH_CHECK(x_in.dim() == 2 && w_in.dim() == 2 && norm_w_in.dim() == 1 &&
+                  x_in.size(1) == w_in.size(1) && norm_w_in.size(0) == x_in.size(1) &&
+                  (!swiglu || w_in.size(0) % 2 == 0),
+              "spyre rms_norm_mm: x [M, K], norm_w [K] and w [N, K] (swiglu: [2n, K]) expected");
+  check_gemm_dtype(x_in, w_in, "rms_norm_mm");
+  TORCH_CHECK(norm_w_in.scalar_type() == x_in.scalar_type(),
+              "spyre rms_norm_mm: norm weight dtype must match x");
+  const int64_t m = x_in.size(0), k = x_in.size(1);
+  const int64_t n = swiglu ? w_in.size(0) / 2 : w_in.size(0);
+  at::Tensor out = empty_spyre({m, n}, x_in.scalar_type(), x_in.device());
+  if (out.numel() == 0) return out;
+  at::Tensor x = x_in.stride(1) == 1 ? x_in : contiguous_on_device(x_in);
+  at::Tensor w = w_in.stride(1) == 1 ? w_in : contiguous_on_device(w_in);
+  at::Tensor nw = contiguous_on_device(norm_w_in);
+  auto al = [](const at::Tensor& t) {
+    return reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 == 0;
+  };
+  const bool fits = m <= 8 && k >= 64 && k % 8 == 0 && k <= 8192 && x.stride(0) % 8 == 0 &&
+                    w.stride(0) % 8 == 0 && al(x) && al(w) && al(nw);
+  c10::DeviceGuard guard(out.device());
+  if (fits) {
+    check_matrix_extent(x, x.data_ptr(), m, k, x.stride(0), 0, 1, 0, "rms_norm_mm x");
+    check_matrix_extent(w, w.data_ptr(), swiglu ? 2 * n : n, k, w.stride(0), 0, 1, 0,
+                        "rms_norm_mm w");
+    SPYRE_SPH_CHECK(sph_gemm_rmsnorm(to_sph(out.scalar_type()), m, n, k, x.data_ptr(),
+                                     x.stride(0), nw.data_ptr(), static_cast<float>(eps),
+                                     w.data_ptr(), w.stride(0), out.data_ptr(), n, swiglu ? 1 : 0,
+                                     stream(out.get_device())));
+    return out;
+  }
+  at::Tensor xn = at::rms_norm(x, {k}, nw, eps);
+  if (!swiglu) return at::mm(xn, w.t());
+  return gemm_swiglu(xn, w);
+}
+
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("mm.out", TORCH_FN(mm_out));
   m.impl("bmm.out", TORCH_FN(bmm_out));

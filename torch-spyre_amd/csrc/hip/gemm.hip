@@ -31,6 +31,8 @@
 //     weight W[N,K]) are HBM-bound on reading W once; they run a separate
 //     streaming kernel (gemm_skinny_kernel) with packed fp16 dot products
 //     instead of MFMA tiles, which would leave most CUs idle at M <= 16.
+#include <algorithm>
+
 #include "sph_common.h"
 
 namespace sph {
@@ -63,6 +65,14 @@ struct GemmArgs {
   int tail_start, splits, kslice;
   float* part;
   int64_t part_bytes;
+  // RMSNorm prologue of the small-M kernels (decode): with norm_w set, row m
+  // of A enters the product as A[m] * norm_w * rsqrt(mean(A[m]^2) + norm_eps).
+  // The weight multiplies each A chunk as it is loaded (rounded to the
+  // element type, as a separate norm kernel's output would be); the row scale
+  // multiplies the finished sums, its sum of squares accumulated alongside
+  // them from the same loads.
+  const void* norm_w;
+  float norm_eps;
 };
 
 template <typename T>
@@ -74,6 +84,23 @@ __device__ inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
         __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
+}
+
+// x * w elementwise on 8 packed 2-byte values, each product rounded to T;
+// adds the squares of x's values to ss.
+template <typename T>
+__device__ inline u32x4 norm_chunk(u32x4 x, u32x4 w, float& ss) {
+  const T* xe = reinterpret_cast<const T*>(&x);
+  const T* we = reinterpret_cast<const T*>(&w);
+  u32x4 r;
+  T* re = reinterpret_cast<T*>(&r);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float xf = Num<T>::to_f(xe[e]);
+    ss = fmaf(xf, xf, ss);
+    re[e] = Num<T>::from_f(xf * Num<T>::to_f(we[e]));
+  }
+  return r;
 }
 
 __device__ inline u32x4 zero4() {
@@ -1109,18 +1136,22 @@ __device__ inline float skinny_epilogue(const GemmArgs& p, float v, int64_t bz, 
   return v;
 }
 
-template <typename T, int MT, int R, int TPR>
+// NORM: the RMSNorm prologue of GemmArgs (norm_w, norm_eps) on A's rows.
+template <typename T, int MT, int R, int TPR, bool NORM = false>
 __global__ void __launch_bounds__(kSkinnyThreads) gemm_skinny_kernel(const GemmArgs p,
                                                                      int64_t nblocks) {
   constexpr int G = kSkinnyThreads / TPR;   // row groups per workgroup
   constexpr int WPG = TPR > 64 ? TPR / 64 : 1;  // waves per group
   __shared__ float red[TPR > 64 ? G * WPG * MT * R : 1];
+  __shared__ float red_ss[NORM && TPR > 64 ? G * WPG * MT : 1];
   const int g = threadIdx.x / TPR, t = threadIdx.x % TPR;
   const int64_t bz = blockIdx.y;
   const uint16_t* A = static_cast<const uint16_t*>(p.a) + bz * p.stride_a;
   const uint16_t* B = static_cast<const uint16_t*>(p.b) + bz * p.stride_b;
+  const uint16_t* NW = static_cast<const uint16_t*>(p.norm_w);
   T* D = static_cast<T*>(p.d) + bz * p.stride_d;
   const int mrows = static_cast<int>(p.m);
+  const float inv_k = 1.0f / static_cast<float>(p.k);
   // Every thread runs the same number of outer iterations (the bound does
   // not depend on the group), so the barriers below are uniform.
   for (int64_t base = static_cast<int64_t>(blockIdx.x) * G; base < nblocks;
@@ -1128,10 +1159,13 @@ __global__ void __launch_bounds__(kSkinnyThreads) gemm_skinny_kernel(const GemmA
     const int64_t blk = base + g;
     const int64_t n0 = blk * R;
     float acc[MT][R];
+    float ss[MT];
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
+    for (int m = 0; m < MT; ++m) {
+      ss[m] = 0.f;
 #pragma unroll
       for (int r = 0; r < R; ++r) acc[m][r] = 0.f;
+    }
     if (blk < nblocks) {
       // Loads are unconditional (rows past N and M read a valid row, whose
       // results are never stored) so no branch separates them: the R + MT
@@ -1146,31 +1180,36 @@ __global__ void __launch_bounds__(kSkinnyThreads) gemm_skinny_kernel(const GemmA
       constexpr int64_t STEP = TPR * 8;
       int64_t k = static_cast<int64_t>(t) * 8;
       if (k < p.k) {
-        u32x4 w[R], x[MT];
+        u32x4 w[R], x[MT], nw = zero4();
 #pragma unroll
         for (int r = 0; r < R; ++r)
           w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bp[r] + k));
 #pragma unroll
         for (int m = 0; m < MT; ++m) x[m] = *reinterpret_cast<const u32x4*>(ap[m] + k);
+        if constexpr (NORM) nw = *reinterpret_cast<const u32x4*>(NW + k);
         while (true) {
           const int64_t kn = k + STEP;
           const bool more = kn < p.k;
           const int64_t kl = more ? kn : k;  // reload the current step when done
-          u32x4 w2[R], x2[MT];
+          u32x4 w2[R], x2[MT], nw2 = zero4();
 #pragma unroll
           for (int r = 0; r < R; ++r)
             w2[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bp[r] + kl));
 #pragma unroll
           for (int m = 0; m < MT; ++m) x2[m] = *reinterpret_cast<const u32x4*>(ap[m] + kl);
+          if constexpr (NORM) nw2 = *reinterpret_cast<const u32x4*>(NW + kl);
 #pragma unroll
-          for (int m = 0; m < MT; ++m)
+          for (int m = 0; m < MT; ++m) {
+            const u32x4 xm = NORM ? norm_chunk<T>(x[m], nw, ss[m]) : x[m];
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[m][r] = dot8_acc<T>(x[m], w[r], acc[m][r]);
+            for (int r = 0; r < R; ++r) acc[m][r] = dot8_acc<T>(xm, w[r], acc[m][r]);
+          }
           if (!more) break;
 #pragma unroll
           for (int r = 0; r < R; ++r) w[r] = w2[r];
 #pragma unroll
           for (int m = 0; m < MT; ++m) x[m] = x2[m];
+          nw = nw2;
           k = kn;
         }
       }
@@ -1178,28 +1217,39 @@ __global__ void __launch_bounds__(kSkinnyThreads) gemm_skinny_kernel(const GemmA
     // Butterflies within the group's wave segment (all lanes take part).
     constexpr int LANES = TPR > 64 ? 64 : TPR;
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
+    for (int m = 0; m < MT; ++m) {
 #pragma unroll
       for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int off = LANES / 2; off > 0; off >>= 1)
           acc[m][r] += __shfl_xor(acc[m][r], off, 64);
+      if constexpr (NORM) {
+#pragma unroll
+        for (int off = LANES / 2; off > 0; off >>= 1) ss[m] += __shfl_xor(ss[m], off, 64);
+      }
+    }
     if constexpr (TPR > 64) {
       const int wig = t / 64;  // wave within the group
       if ((t & 63) == 0) {
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
+        for (int m = 0; m < MT; ++m) {
 #pragma unroll
           for (int r = 0; r < R; ++r) red[((g * WPG) + wig) * MT * R + m * R + r] = acc[m][r];
+          if constexpr (NORM) red_ss[((g * WPG) + wig) * MT + m] = ss[m];
+        }
       }
       __syncthreads();
       for (int q = t; q < MT * R; q += TPR) {
         const int m = q / R, r = q % R;
         const int64_t n = n0 + r;
         if (blk < nblocks && m < mrows && n < p.n) {
-          float v = 0.f;
+          float v = 0.f, sq = 0.f;
 #pragma unroll
-          for (int w = 0; w < WPG; ++w) v += red[(g * WPG + w) * MT * R + q];
+          for (int w = 0; w < WPG; ++w) {
+            v += red[(g * WPG + w) * MT * R + q];
+            if constexpr (NORM) sq += red_ss[(g * WPG + w) * MT + m];
+          }
+          if constexpr (NORM) v *= rsqrtf(sq * inv_k + p.norm_eps);
           D[m * p.ldd + n] = Num<T>::from_f(skinny_epilogue<T>(p, v, bz, m, n));
         }
       }
@@ -1211,15 +1261,18 @@ __global__ void __launch_bounds__(kSkinnyThreads) gemm_skinny_kernel(const GemmA
 #pragma unroll
           for (int r = 0; r < R; ++r) {
             const int64_t n = n0 + r;
-            if (t == (m * R + r) % TPR && m < mrows && n < p.n)
-              D[m * p.ldd + n] = Num<T>::from_f(skinny_epilogue<T>(p, acc[m][r], bz, m, n));
+            if (t == (m * R + r) % TPR && m < mrows && n < p.n) {
+              float v = acc[m][r];
+              if constexpr (NORM) v *= rsqrtf(ss[m] * inv_k + p.norm_eps);
+              D[m * p.ldd + n] = Num<T>::from_f(skinny_epilogue<T>(p, v, bz, m, n));
+            }
           }
       }
     }
   }
 }
 
-template <typename T, int MT, int R, int TPR>
+template <typename T, int MT, int R, int TPR, bool NORM = false>
 void launch_skinny_cfg(const GemmArgs& p, int64_t batch, hipStream_t st) {
   const int64_t nblocks = ceil_div(p.n, R);
   constexpr int G = kSkinnyThreads / TPR;
@@ -1227,7 +1280,7 @@ void launch_skinny_cfg(const GemmArgs& p, int64_t batch, hipStream_t st) {
   const int64_t cap = batch >= 4096 ? 1 : 4096 / batch;
   if (gx > cap) gx = cap;
   dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(batch));
-  gemm_skinny_kernel<T, MT, R, TPR><<<grid, dim3(kSkinnyThreads), 0, st>>>(p, nblocks);
+  gemm_skinny_kernel<T, MT, R, TPR, NORM><<<grid, dim3(kSkinnyThreads), 0, st>>>(p, nblocks);
 }
 
 // Launch shape from a sweep on MI355X over the decode shapes (x[4, K] times
@@ -1235,7 +1288,7 @@ void launch_skinny_cfg(const GemmArgs& p, int64_t batch, hipStream_t st) {
 // columns each for K ~ 4096, four columns for long rows, one-wave groups of
 // four columns for very wide W (LM heads), whole-workgroup groups for narrow
 // W; TPR never exceeds K / 8 (every thread owns at least one K chunk).
-template <typename T, int MT>
+template <typename T, int MT, bool NORM = false>
 void launch_skinny_m(const GemmArgs& p, int64_t batch, hipStream_t st) {
   int tmax = 256;
   while (tmax > 16 && static_cast<int64_t>(tmax) * 8 > p.k) tmax >>= 1;
@@ -1244,27 +1297,27 @@ void launch_skinny_m(const GemmArgs& p, int64_t batch, hipStream_t st) {
   if (cols >= 32768) tpr = 64, r = 4;
   else if (cols <= 2048) tpr = 256, r = 2;
   if (tpr > tmax) tpr = tmax, r = 2;
-  if (r == 4 && tpr == 64) return launch_skinny_cfg<T, MT, 4, 64>(p, batch, st);
-  if (r == 4) return launch_skinny_cfg<T, MT, 4, 128>(p, batch, st);
+  if (r == 4 && tpr == 64) return launch_skinny_cfg<T, MT, 4, 64, NORM>(p, batch, st);
+  if (r == 4) return launch_skinny_cfg<T, MT, 4, 128, NORM>(p, batch, st);
   switch (tpr) {
-    case 256: return launch_skinny_cfg<T, MT, 2, 256>(p, batch, st);
-    case 128: return launch_skinny_cfg<T, MT, 2, 128>(p, batch, st);
-    case 64: return launch_skinny_cfg<T, MT, 2, 64>(p, batch, st);
-    case 32: return launch_skinny_cfg<T, MT, 2, 32>(p, batch, st);
-    default: return launch_skinny_cfg<T, MT, 2, 16>(p, batch, st);
+    case 256: return launch_skinny_cfg<T, MT, 2, 256, NORM>(p, batch, st);
+    case 128: return launch_skinny_cfg<T, MT, 2, 128, NORM>(p, batch, st);
+    case 64: return launch_skinny_cfg<T, MT, 2, 64, NORM>(p, batch, st);
+    case 32: return launch_skinny_cfg<T, MT, 2, 32, NORM>(p, batch, st);
+    default: return launch_skinny_cfg<T, MT, 2, 16, NORM>(p, batch, st);
   }
 }
 
-template <typename T>
+template <typename T, bool NORM = false>
 int launch_skinny(const GemmArgs& p, int64_t batch, hipStream_t st) {
   if (p.m <= 1)
-    launch_skinny_m<T, 1>(p, batch, st);
+    launch_skinny_m<T, 1, NORM>(p, batch, st);
   else if (p.m <= 4)
-    launch_skinny_m<T, 4>(p, batch, st);
+    launch_skinny_m<T, 4, NORM>(p, batch, st);
   else if (p.m <= 8)
-    launch_skinny_m<T, 8>(p, batch, st);
+    launch_skinny_m<T, 8, NORM>(p, batch, st);
   else
-    launch_skinny_m<T, 16>(p, batch, st);
+    launch_skinny_m<T, 16, NORM>(p, batch, st);
   return check_launch("sph_gemm (small M)");
 }
 
@@ -1293,11 +1346,15 @@ constexpr int WAVES = 16, THREADS = WAVES * 64, SEG = 8;
 // is silu(x W[j]) * (x W[n + j]).  A wave's item then loads SEG / 2 chunks
 // of both rows (the same register footprint) and the end of the row
 // combines the two sums.
-template <typename T, int MT, int KMAX, bool SWIGLU = false>
+// NORM: the RMSNorm prologue of GemmArgs (norm_w, norm_eps), applied while
+// the activations are staged (sums of squares reduced through LDS at the
+// staging barrier) and to the finished sums of each row.
+template <typename T, int MT, int KMAX, bool SWIGLU = false, bool NORM = false>
 __global__ void __launch_bounds__(gv::THREADS) gemm_stream_kernel(const GemmArgs p) {
   using namespace gv;
   constexpr int NR = SWIGLU ? 2 : 1, SEGK = SEG / NR;  // rows per item, chunks per row
   __shared__ __attribute__((aligned(16))) uint16_t As[MT * KMAX];
+  __shared__ float lds_ss[NORM ? WAVES * MT : 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nc = static_cast<int>(p.k / 8);           // 16-byte chunks per row
   const int mrows = static_cast<int>(p.m);
@@ -1352,8 +1409,8 @@ __global__ void __launch_bounds__(gv::THREADS) gemm_stream_kernel(const GemmArgs
             acc[r_][m_] += __shfl_xor(acc[r_][m_], o_, 64);                                 \
     float v_ = 0.f;                                                                         \
     _Pragma("unroll") for (int m_ = 0; m_ < MT; ++m_) {                                     \
-      const float g_ = acc[0][m_];                                                          \
-      const float x_ = SWIGLU ? silu(g_) * acc[NR - 1][m_] : g_;                            \
+      const float g_ = acc[0][m_] * rs[m_];                                                 \
+      const float x_ = SWIGLU ? silu(g_) * (acc[NR - 1][m_] * rs[m_]) : g_;                 \
       v_ = lane == m_ ? x_ : v_;                                                            \
     }                                                                                       \
     if (lane < MT && lane < mrows)                                                          \
@@ -1367,13 +1424,43 @@ __global__ void __launch_bounds__(gv::THREADS) gemm_stream_kernel(const GemmArgs
   // the two latencies overlap.
   if (n < p.n) SPH_GV_LOAD(wa, n, 0);
   // Stage the activations ([m][chunk], rows past M as zeros).
+  float rs[MT];  // row scales of the RMSNorm prologue (1 without it)
+#pragma unroll
+  for (int m = 0; m < MT; ++m) rs[m] = 0.f;
   for (int i = threadIdx.x; i < MT * nc; i += THREADS) {
     const int m = i / nc, c = i - m * nc;
     u32x4 v = {0u, 0u, 0u, 0u};
     if (m < mrows) v = *reinterpret_cast<const u32x4*>(A + m * p.lda + c * 8);
+    if constexpr (NORM) {
+      float sq = 0.f;
+      v = norm_chunk<T>(v, *reinterpret_cast<const u32x4*>(
+                               static_cast<const uint16_t*>(p.norm_w) + c * 8), sq);
+#pragma unroll
+      for (int mm = 0; mm < MT; ++mm) rs[mm] += mm == m ? sq : 0.f;
+    }
     *reinterpret_cast<u32x4*>(As + (m * nc + c) * 8) = v;
   }
+  if constexpr (NORM) {
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) {
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) rs[mm] += __shfl_xor(rs[mm], o, 64);
+      if (lane == 0) lds_ss[wave * MT + mm] = rs[mm];
+    }
+  }
   __syncthreads();
+  if constexpr (NORM) {
+    const float inv_k = 1.0f / static_cast<float>(p.k);
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) {
+      float sq = 0.f;
+      for (int w = 0; w < WAVES; ++w) sq += lds_ss[w * MT + mm];
+      rs[mm] = rsqrtf(sq * inv_k + p.norm_eps);
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) rs[m] = 1.f;
+  }
   if (n >= p.n) return;  // no barrier follows
   // Items (row, segment) in order; item i+1 loads while item i computes.
   int s = 0;
@@ -1781,6 +1868,65 @@ extern "C" int sph_gemm_swiglu(sph_dtype dtype, int64_t m, int64_t n, int64_t k,
   if (dtype == SPH_F16)
     return launch_dl<half_t, 256, true>(p, 1, true, st, split ? &pl : nullptr);
   return launch_dl<bf16_t, 256, true>(p, 1, true, st, split ? &pl : nullptr);
+}
+
+extern "C" int sph_gemm_rmsnorm(sph_dtype dtype, int64_t m, int64_t n, int64_t k, const void* a,
+                                int64_t lda, const void* norm_w, float eps, const void* w,
+                                int64_t ldw, void* d, int64_t ldd, int swiglu,
+                                sph_stream_t stream) {
+  SPH_REQUIRE(dtype == SPH_F16 || dtype == SPH_BF16, SPH_ERR_UNSUPPORTED,
+              "gemm_rmsnorm: dtype must be F16 or BF16");
+  SPH_REQUIRE(m >= 0 && n >= 0 && k >= 0, SPH_ERR_INVALID_ARG, "gemm_rmsnorm: negative size");
+  if (m == 0 || n == 0) return SPH_OK;
+  SPH_REQUIRE(m <= 8, SPH_ERR_UNSUPPORTED, "gemm_rmsnorm: at most 8 rows (decode shapes)");
+  SPH_REQUIRE(k >= 64 && k % 8 == 0 && k <= 8192, SPH_ERR_UNSUPPORTED,
+              "gemm_rmsnorm: needs 64 <= k <= 8192, k % 8 == 0");
+  SPH_REQUIRE(std::isfinite(eps) && eps >= 0.f, SPH_ERR_INVALID_ARG,
+              "gemm_rmsnorm: eps must be finite and >= 0");
+  SPH_REQUIRE(lda >= k && ldw >= k && ldd >= n && n < (1LL << 40), SPH_ERR_INVALID_ARG,
+              "gemm_rmsnorm: leading dimension too small");
+  SPH_REQUIRE(al16(a) && al16(w) && al16(norm_w) && lda % 8 == 0 && ldw % 8 == 0,
+              SPH_ERR_UNSUPPORTED, "gemm_rmsnorm: x, norm_w and w rows must be 16-byte aligned");
+  GemmArgs q{};
+  q.m = m;
+  q.n = n;
+  q.k = k;
+  q.a = a;
+  q.lda = lda;
+  q.b = w;
+  q.ldb = ldw;
+  q.d = d;
+  q.ldd = ldd;
+  q.alpha = 1.f;
+  q.epilogue = SPH_EPI_NONE;
+  q.vec_a = q.vec_b = 1;
+  q.vec_d = al16(d) && ldd % 8 == 0;
+  q.norm_w = norm_w;
+  q.norm_eps = eps;
+  hipStream_t st = as_stream(stream);
+  constexpr int64_t kCUs = 256;
+  const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(n, gv::WAVES), kCUs));
+#define SPH_RN_STREAM(T_, SW_)                                                              \
+  do {                                                                                      \
+    if (m <= 4)                                                                             \
+      gemm_stream_kernel<T_, 4, 8192, SW_, true><<<grid, dim3(gv::THREADS), 0, st>>>(q);    \
+    else                                                                                    \
+      gemm_stream_kernel<T_, 8, 8192, SW_, true><<<grid, dim3(gv::THREADS), 0, st>>>(q);    \
+  } while (0)
+  if (swiglu) {
+    // w holds the gate rows [0, n) and the up rows [n, 2n)
+    if (dtype == SPH_F16) SPH_RN_STREAM(half_t, true);
+    else SPH_RN_STREAM(bf16_t, true);
+    return check_launch("sph_gemm_rmsnorm (swiglu stream)");
+  }
+  if (stream_fits(q, 1, true, true)) {
+    if (dtype == SPH_F16) SPH_RN_STREAM(half_t, false);
+    else SPH_RN_STREAM(bf16_t, false);
+    return check_launch("sph_gemm_rmsnorm (stream)");
+  }
+#undef SPH_RN_STREAM
+  if (dtype == SPH_F16) return launch_skinny<half_t, true>(q, 1, st);
+  return launch_skinny<bf16_t, true>(q, 1, st);
 }
 
 extern "C" int sph_gemm_f16(int64_t m, int64_t n, int64_t k, const void* a,

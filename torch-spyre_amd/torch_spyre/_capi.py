@@ -62,6 +62,8 @@ _SIGS = {
                      c_i64, c_i64, c_f32, vp, c_i64, c_i64, c_i64, vp, c_i64, c_i64, c_int, vp,
                      c_i64, vp], c_int),
     "sph_gemm_workspace_bytes": ([c_i64, c_i64, c_i64, c_i64], c_i64),
+    "sph_gemm_rmsnorm": ([c_int, c_i64, c_i64, c_i64, vp, c_i64, vp, c_f32, vp, c_i64, vp, c_i64,
+                          c_int, vp], c_int),
     "sph_gemm_f16": ([c_i64, c_i64, c_i64, vp, vp, vp, vp], c_int),
     "sph_bmm_f16": ([c_i64, c_i64, c_i64, c_i64, vp, vp, vp, vp], c_int),
     "sph_attention_fwd": ([c_int, c_i64, c_i64, c_i64, c_i64, vp, c_i64, c_i64, vp, c_i64,

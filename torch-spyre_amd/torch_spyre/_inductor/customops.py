@@ -301,3 +301,35 @@ def transpose_copy(x: torch.Tensor, dims: list[int]) -> torch.Tensor:
 @transpose_copy.register_fake
 def _(x, dims):
     return x.new_empty([x.shape[d] for d in dims])
+
+
+# ---- RMSNorm folded into the decode projections ----------------------------
+
+@torch.library.custom_op("spyre::rms_norm_mm", mutates_args=())
+def rms_norm_mm(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w: torch.Tensor,
+                swiglu: bool) -> torch.Tensor:
+    """rms_norm(x, norm_w, eps) @ w.T for x [M, K] and an nn.Linear weight w
+    [N, K]; with swiglu, w stacks the gate and up rows [2n, K] and the
+    result is silu(gate) * up.  The reference runs the norm as its composite
+    ops (pow / mean / add / rsqrt / mul, Metadata.yaml:236-253) and the
+    product as spyre__mm_default (spyre_torch_ops.cpp:214-293); on other
+    devices this is that chain, on spyre (decode rows, M <= 8) one
+    weight-stream kernel with the norm as its prologue (sph_gemm_rmsnorm)."""
+    xn = torch.nn.functional.rms_norm(x, (x.shape[-1],), norm_w, eps)
+    if not swiglu:
+        return torch.mm(xn, w.t())
+    n = w.shape[0] // 2
+    gu = torch.mm(xn, w.t())
+    return torch.nn.functional.silu(gu[:, :n]) * gu[:, n:]
+
+
+@rms_norm_mm.register_kernel("spyre")
+def _(x, norm_w, eps, w, swiglu):
+    from torch_spyre import _C
+
+    return _C.gemm_rmsnorm(x, norm_w, float(eps), w, bool(swiglu))
+
+
+@rms_norm_mm.register_fake
+def _(x, norm_w, eps, w, swiglu):
+    return x.new_empty((x.shape[0], w.shape[0] // 2 if swiglu else w.shape[0]))

@@ -9,9 +9,10 @@ tensors, and no conversion is removed: kernels upcast to fp32 internally, so
 the conversions Inductor sees are the ones the program asked for.  The list
 holds the attention fusion (bmm -> softmax -> bmm as one fused kernel,
 fuse_attention.py), the SwiGLU projection fusion (x W^T -> silu(gate) *
-up as one GEMM, fuse_swiglu.py) and transposing copies as one tiled
-transpose (fuse_transpose.py); a pass is any callable taking the
-GraphModule.
+up as one GEMM, fuse_swiglu.py), for decode steps RMSNorm folded into the
+projections that read it and residual adds into the projections that feed
+them (fuse_decode_norm.py), and transposing copies as one tiled transpose
+(fuse_transpose.py); a pass is any callable taking the GraphModule.
 """
 
 from __future__ import annotations
@@ -22,11 +23,12 @@ import torch
 from torch._inductor.custom_graph_pass import CustomGraphModulePass, get_hash_for_files
 
 from .fuse_attention import fuse_attention
+from .fuse_decode_norm import fuse_decode_norm, fuse_residual
 from .fuse_swiglu import fuse_swiglu
 from .fuse_transpose import fuse_transpose
 
-custom_post_passes: List[Callable[[torch.fx.GraphModule], None]] = [fuse_attention, fuse_swiglu,
-                                                                    fuse_transpose]
+custom_post_passes: List[Callable[[torch.fx.GraphModule], None]] = [
+    fuse_attention, fuse_swiglu, fuse_decode_norm, fuse_residual, fuse_transpose]
 
 
 class CustomPostPasses(CustomGraphModulePass):
