@@ -33,6 +33,8 @@ SEED = 0xAFFE
 # ~35 ms of sustained load; 300 launches of the shortest kernel cover that
 # only together with the ones before it).
 SUB_WARMUP = 300
+# untimed launches of the headline GEMM before its warmup (steady clock)
+PRECONDITION_MS = 100.0
 
 
 def _log(msg):
@@ -203,10 +205,25 @@ def bench_gemm(steps, warmup, stream, capi):
         if rc:
             capi.check(rc, "sph_gemm_f16")
 
+    # Preconditioning: the part lowers its clock under this MFMA + LDS load
+    # (power-limited) and needs ~35 ms of it to settle; launches before that
+    # measure the clock's transition, not the kernel (4096^3: 989 TFLOP/s
+    # after 10 launches, 1165 after 100, 1207-1212 after 300 or 1000).  So
+    # the kernel runs PRECONDITION_MS of untimed launches first; then come
+    # exactly `warmup` untimed and `steps` timed launches.
+    n_pre = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < PRECONDITION_MS:
+        for _ in range(50):
+            step()
+        n_pre += 50
+        torch.cuda.synchronize()
     kernel_ms, wall_ms = Timer(stream).run(step, steps, warmup)
     flop = 2.0 * M * N * K
     return {"kernel_ms": kernel_ms, "wall_ms": wall_ms, "flop": flop,
-            "tflops": flop / (kernel_ms * 1e-3) / 1e12, "a": a, "b": b, "d": d}
+            "tflops": flop / (kernel_ms * 1e-3) / 1e12, "a": a, "b": b, "d": d,
+            "precondition_launches": n_pre}
 
 
 def bench_extra(steps, warmup, stream, capi):
@@ -971,6 +988,9 @@ def main(argv=None):
         "data": "synthetic (U(-1,1), seed 0xAFFE)",
         "config": {"workload": "c2: fp16 mm C = A @ B, M=N=K=4096 (BASELINE configs[1])",
                    "M": 4096, "N": 4096, "K": 4096, "path": "C-ABI sph_gemm_f16"},
+        "precondition": {"launches": g["precondition_launches"], "ms": PRECONDITION_MS,
+                         "why": "untimed launches before the warmup so the timed steps run at "
+                                "the part's steady clock under this load"},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
                      "traffic": _traffic_for("gemm")},

@@ -323,6 +323,42 @@ int sph_attention_decode(sph_dtype dtype, int64_t batch, int64_t mq, int64_t sk,
  * shape, or mq > 16). */
 int64_t sph_attention_decode_workspace_bytes(int64_t batch, int64_t mq, int64_t sk);
 
+/* One decode step of grouped-query attention with its KV-cache append, for
+ * every batch entry and KV head in one launch.  qkv [batch, (n_heads +
+ * 2 n_kv_heads) * 128] (row stride ld_qkv) holds each entry's query heads,
+ * then its new keys, then its new values; P = *pos (a device int64) is the
+ * new token's position.  Queries and new keys are rotated by RoPE at P
+ * (rotate-half, tables cos / sin [max_len, 128], row stride ld_rope), the
+ * key and value are stored in the caches at P, and out[b] (row stride
+ * ld_out, query head j at columns j * 128) = softmax(scale q K[0..P]^T)
+ * V[0..P] for each query head j, over KV head j / (n_heads / n_kv_heads).
+ * K cache [batch, n_kv_heads, max_len, 128] by element strides (dim stride
+ * 1, 16-byte aligned rows); V cache key-major (v_dim_stride 1, 16-byte
+ * aligned rows) or dim-major (v_key_stride 1, rows of any length).
+ * dtype F16 / BF16; fp32 scores and sums; n_heads / n_kv_heads <= 8;
+ * batch * n_kv_heads <= 4096.  workspace: at least
+ * sph_decode_attention_step_workspace_bytes(...) bytes for the per-chunk
+ * partials.  A P outside [0, max_len) writes nothing and sets *error_word
+ * (device-visible int32, may be NULL) to 2.  Two launches on `stream`:
+ * per-chunk partials into the workspace, then their merge.
+ * Replaces, for a decode step, the chain the reference runs op by op: the
+ * RoPE pointwise ops and the cache copy (Metadata.yaml generated mul / add /
+ * neg / cat and spyre__copy_from, spyre_mem.cpp:661-703), then
+ * spyre__bmm_default (codegen/inputs/spyre_torch_ops.cpp:297-377), add +
+ * _softmax (Metadata.yaml:275-277) and spyre__bmm_default again. */
+int sph_decode_attention_step(sph_dtype dtype, int64_t batch, int64_t n_heads,
+                              int64_t n_kv_heads, int64_t head_dim, const void* qkv,
+                              int64_t ld_qkv, const void* cos, const void* sin, int64_t ld_rope,
+                              const int64_t* pos, int32_t* error_word, void* k_cache,
+                              int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_s,
+                              void* v_cache, int64_t v_stride_b, int64_t v_stride_h,
+                              int64_t v_key_stride, int64_t v_dim_stride, int64_t max_len,
+                              float scale, void* out, int64_t ld_out, void* workspace,
+                              int64_t workspace_bytes, sph_stream_t stream);
+/* Workspace bytes of sph_decode_attention_step (0 for an empty shape). */
+int64_t sph_decode_attention_step_workspace_bytes(int64_t batch, int64_t n_heads,
+                                                  int64_t n_kv_heads, int64_t max_len);
+
 /* sph_attention_fwd for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops, harnesses that forbid
  * hipMalloc): the same arguments without the workspace, the same kernels

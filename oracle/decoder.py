@@ -17,7 +17,10 @@ inside each fused kernel: RoPE and SiLU*up round once, the scale is applied
 to the fp16 bmm output without another rounding; where the compiled program
 runs attention as one fused kernel - prefill, head dim 128, the stacked
 query rows of a KV head a multiple of 128 - the scores are not rounded at
-all, only the probabilities before the second product; where it runs the
+all, only the probabilities before the second product; in a decode step
+(one new position, head dim 128, at most 8 query heads per KV head) RoPE,
+the cache append and attention are one kernel whose scores and
+probabilities stay float32 (only the output rounds); where it runs the
 gate / up projection and silu(gate) * up as one kernel - rows % 256 == 0,
 intermediate % 128 == 0, hidden % 64 == 0, or at most 8 rows with
 64 <= hidden <= 8192 - gate and up are not rounded either).  At most 8 rows
@@ -42,8 +45,10 @@ from . import ops as O
 
 
 def _r(x, act):
+    """x rounded to the activation type `act` (np.float16, "bfloat16", or
+    None for float32)."""
     x = np.asarray(x, dtype=np.float32)
-    return x if act is None else x.astype(act).astype(np.float32)
+    return x if act is None else O._round_to(x, act)
 
 
 def _linear(x, w, act):
@@ -91,10 +96,13 @@ def _rope(x, cos, sin, act, fused=False):
     return _r(_r(x * c, act) + _r(rot * s, act), act)
 
 
-def attention(q, k, v, q_pos, k_pos, act=None, fused=False, scores_fp32=False):
+def attention(q, k, v, q_pos, k_pos, act=None, fused=False, scores_fp32=False,
+              probs_fp32=False):
     """q [B, Sq, Hq, D], k / v [B, Sk, Hkv, D]; causal on absolute
     positions (key position <= query position).  Returns [B, Sq, Hq*D].
-    scores_fp32: the scores stay float32 (a fused attention kernel)."""
+    scores_fp32: the scores stay float32 (a fused attention kernel);
+    probs_fp32: so do the probabilities (the fused decode-step kernel,
+    which normalises the float32 output sums once at the end)."""
     B, Sq, Hq, D = q.shape
     Hkv = k.shape[2]
     g = Hq // Hkv
@@ -110,7 +118,9 @@ def attention(q, k, v, q_pos, k_pos, act=None, fused=False, scores_fp32=False):
             if not fused and not scores_fp32:
                 s = _r(s, act)
             s = np.where(allowed, s, np.float32(-np.inf))
-            p = _r(O.softmax(s, axis=-1), act)
+            p = O.softmax(s, axis=-1)
+            if not probs_fp32:
+                p = _r(p, act)
             out[b, :, h] = _r(p @ v[b, :, kh].astype(np.float32), act)
     return out.reshape(B, Sq, Hq * D)
 
@@ -139,7 +149,11 @@ def layer(h, w, cfg, positions, act=np.float16, kv_prefix=None, fused=False):
     # the compiled program's prefill attention is one fused kernel when its
     # shapes fit (head dim 128, stacked query rows per KV head % 128 == 0)
     fused_attn = fused and kv_prefix is None and D == 128 and (S * (H // Hkv)) % 128 == 0
-    a = attention(q, k, v, np.asarray(positions), k_pos, act, fused, scores_fp32=fused_attn)
+    # its decode step (one new position) runs RoPE, the cache append and
+    # attention as one kernel (torch.ops.spyre.decode_attention)
+    fused_step = fused and kv_prefix is not None and S == 1 and D == 128 and H // Hkv <= 8
+    a = attention(q, k, v, np.asarray(positions), k_pos, act, fused,
+                  scores_fp32=fused_attn or fused_step, probs_fp32=fused_step)
     res_act = None if fold_res else act
     h = _r(h + _linear(a, w["wo"], res_act), act)
     # the compiled program's fused SwiGLU kernels keep gate / up in fp32
@@ -202,3 +216,41 @@ def generate_teacher_forced(prompt, teacher, params, cfg, act=np.float16, fused=
                                  fused=fused)
         out.append(logits(h[:, -1], params, cfg, act, fused=fused))
     return np.stack(out, 0)
+
+
+def decode_step_attention(qkv, cos, sin, pos, k_cache, v_cache, n_heads, n_kv_heads, scale,
+                          act=np.float16):
+    """One decode step of attention with its cache append, as the fused
+    decode-step kernel computes it: qkv [B, (H + 2 Hkv) * D] (query heads,
+    then keys, then values), tables cos / sin [L, D] (already in the element
+    type), position pos, caches k [B, Hkv, L, D] and v [B, Hkv, L, D]
+    (key-major here).  Rotated q and k round once to `act`; scores,
+    probabilities and output sums are float32; the output rounds once.
+    Returns (out [B, H * D], k_cache', v_cache') with the new key / value at
+    pos and keys 0..pos attended.  Pinned by tests/test_decoder.py against
+    torch.ops.spyre.decode_attention's op-by-op CPU chain and against
+    layer()'s decode-step attention."""
+    qkv = np.asarray(qkv, np.float32)
+    B = qkv.shape[0]
+    H, Hkv = n_heads, n_kv_heads
+    D = np.asarray(k_cache).shape[-1]
+    q = qkv[:, :H * D].reshape(B, 1, H, D)
+    k = qkv[:, H * D:(H + Hkv) * D].reshape(B, 1, Hkv, D)
+    v = qkv[:, (H + Hkv) * D:].reshape(B, 1, Hkv, D)
+    c = np.asarray(cos, np.float32)[pos:pos + 1]
+    s = np.asarray(sin, np.float32)[pos:pos + 1]
+    q = _rope(q, c, s, act, fused=True)
+    k = _rope(k, c, s, act, fused=True)
+    kc = np.array(k_cache, np.float32)
+    vc = np.array(v_cache, np.float32)
+    kc[:, :, pos] = k[:, 0]
+    vc[:, :, pos] = v[:, 0]
+    G = H // Hkv
+    out = np.empty((B, H, D), np.float32)
+    for b in range(B):
+        for j in range(H):
+            kh = j // G
+            sc = (q[b, 0, j] @ kc[b, kh, :pos + 1].T) * np.float32(scale)
+            p = O.softmax(sc[None, :], axis=-1)[0]
+            out[b, j] = _r(p @ vc[b, kh, :pos + 1], act)
+    return out.reshape(B, H * D), kc, vc

@@ -233,3 +233,57 @@ def test_fused_decode_tracks_independent_fp32_decoder():
         seq = torch.cat([prompt, teacher[:, :t]], 1)
         want = _sdpa_logits(seq, tf, FUSED)[:, -1].numpy()
         np.testing.assert_allclose(got[t], want, rtol=1e-2, atol=1e-2)
+
+
+HD128 = D.DecoderConfig(hidden=256, n_heads=4, n_kv_heads=2, head_dim=128, intermediate=192,
+                        vocab=50, n_layers=2)
+
+
+def test_fused_decode_attention_op_matches_plain_step_on_cpu():
+    # decode_step_static through torch.ops.spyre.decode_attention (its CPU
+    # chain) against the plain-op eager decode, float32
+    p = _params(HD128)
+    prompt = _tokens(2, 9, HD128.vocab)
+    teacher = _tokens(2, 4, HD128.vocab, seed=7)
+    _, a = D.generate(prompt, p, HD128, 4, "cpu", teacher=teacher)
+    _, b = D.generate(prompt, p, HD128, 4, "cpu", teacher=teacher,
+                      decode_fn=D.decode_step_static)
+    torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("v_dim_major", [False, True])
+def test_oracle_decode_step_attention_pinned(v_dim_major):
+    # oracle.decoder.decode_step_attention (float32, act=None) against the
+    # op-by-op chain of torch.ops.spyre.decode_attention on the CPU; a
+    # rotation with the wrong sign and an off-by-one key range both fail
+    import math
+
+    import torch_spyre._inductor.customops  # noqa: F401
+
+    g = torch.Generator().manual_seed(21)
+    B, H, Hkv, L, Dh, pos = 2, 8, 2, 70, 128, 64
+    qkv = torch.randn(B, (H + 2 * Hkv) * Dh, generator=g)
+    kc = torch.randn(B, Hkv, L, Dh, generator=g)
+    vc = torch.randn(B, Hkv, L, Dh, generator=g)
+    ang = torch.arange(L, dtype=torch.float32)[:, None] * \
+        (1e4 ** (-torch.arange(0, Dh, 2, dtype=torch.float32) / Dh))[None, :]
+    ang = torch.cat([ang, ang], -1)
+    cs, sn = ang.cos(), ang.sin()
+    scale = 1.0 / math.sqrt(Dh)
+    kt, vt = kc.clone(), (vc.transpose(2, 3).contiguous() if v_dim_major else vc.clone())
+    out = torch.ops.spyre.decode_attention(qkv, cs, sn, torch.tensor([pos]), kt, vt, H, Hkv,
+                                           scale, v_dim_major)
+    o_want, k_want, v_want = OD.decode_step_attention(qkv.numpy(), cs.numpy(), sn.numpy(), pos,
+                                                      kc.numpy(), vc.numpy(), H, Hkv, scale,
+                                                      act=None)
+    np.testing.assert_allclose(out.numpy(), o_want, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(kt.numpy(), k_want, rtol=1e-6, atol=1e-6)
+    vt_kmaj = vt.transpose(2, 3) if v_dim_major else vt
+    assert np.array_equal(vt_kmaj.numpy(), v_want)
+    # planted mistakes: sin with the wrong sign; the new key left out
+    bad, _, _ = OD.decode_step_attention(qkv.numpy(), cs.numpy(), -sn.numpy(), pos, kc.numpy(),
+                                         vc.numpy(), H, Hkv, scale, act=None)
+    assert not np.allclose(bad, out.numpy(), rtol=1e-3, atol=1e-3)
+    bad2, _, _ = OD.decode_step_attention(qkv.numpy(), cs.numpy(), sn.numpy(), pos - 1,
+                                          kc.numpy(), vc.numpy(), H, Hkv, scale, act=None)
+    assert not np.allclose(bad2, out.numpy(), rtol=1e-3, atol=1e-3)

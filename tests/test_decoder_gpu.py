@@ -16,9 +16,11 @@ on a short prompt eagerly; greedy tokens must agree with the oracle's
 argmax wherever the oracle's top-2 logits are separated by more than the
 tolerance.
 
-Gates of the compiled programs, calibrated on the oracle itself (two
-correct fp16 programs differ beyond 1e-2 at a few elements per million at
-these sizes):
+Gates of the compiled programs and of the eager 2-layer flow, calibrated
+on the oracle itself (two correct fp16 programs differ beyond 1e-2 at a few
+elements per million at these sizes: a one-ulp difference in an fp16
+activation, from another summation order of the same fp32 products, can
+move a logit two layers later by ~0.01):
   * against the oracle at the device's rounding points: at most 1e-4 of
     the elements beyond rtol = atol = 1e-2, and no more (fraction and
     largest deviation) than the oracle's fp16 form deviates from its
@@ -156,13 +158,11 @@ def test_c5_flow_teacher_forced_vs_oracle(compiled):
     pn = _np(params)
     want = OD.generate_teacher_forced(prompt.numpy(), teacher.numpy(), pn, cfg, fused=compiled)
     got = logits.cpu().float().numpy()
-    if not compiled:
-        np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2)
-    else:
-        exact = OD.generate_teacher_forced(prompt.numpy(), teacher.numpy(), pn, cfg, act=None)
-        eager = OD.generate_teacher_forced(prompt.numpy(), teacher.numpy(), pn, cfg,
-                                           fused=False)
-        _gate(got, want, exact, "c5 2-layer short prompt", floor16=eager)
+    exact = OD.generate_teacher_forced(prompt.numpy(), teacher.numpy(), pn, cfg, act=None)
+    # the other fp16 rounding variant of the oracle sets the noise floor too
+    other = OD.generate_teacher_forced(prompt.numpy(), teacher.numpy(), pn, cfg,
+                                       fused=not compiled)
+    _gate(got, want, exact, f"c5 2-layer short prompt compiled={compiled}", floor16=other)
     _check_greedy(toks, want)
 
 

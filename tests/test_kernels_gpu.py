@@ -297,8 +297,6 @@ def test_gemm_reference_kat_exact():
                                    (64, 49155, 64)])
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 def test_gemm_shapes_transposes(m, n, k, ta, tb):
-    if m * n * k >= 2**30 and (ta or tb):
-        pytest.skip("large case covered by the NN / NT layouts")
     _log(f"gemm {m}x{n}x{k} ta={ta} tb={tb}")
     A = uniform((m, k), k=1)
     B = uniform((k, n), k=2)
@@ -442,13 +440,18 @@ def test_gemm_small_m_weight_layout(m, n, k, dtype):
 
 @pytest.mark.parametrize("m,n,k", [(4, 25600, 4096), (4, 49155, 4096), (5, 16400, 2056),
                                    (8, 4100, 8192), (2, 32770, 1024), (3, 4097, 8192),
-                                   (1, 4100, 8200)])
+                                   (1, 4100, 8200), (4, 6144, 4096), (4, 4096, 4096),
+                                   (4, 4096, 12800), (4, 2100, 4096), (2, 1030, 16384),
+                                   (8, 2050, 8200)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_gemm_stream_decode_shapes(m, n, k, dtype):
     # the persistent weight-stream kernel (batch 1, M <= 8, K >= 1024):
     # K not a multiple of the 512-element lane sweep, N off the 16 waves of
-    # a workgroup, several rows per wave, K at the LDS staging limit (and
-    # just past it, on the small-M kernel)
+    # a workgroup, several rows per wave; leftover rows split along K over
+    # 2 to 16 waves (N % 4096 of 2048, 1024, 16, 3, 2 rows), every row split
+    # (N below one round), no leftover (N = 4096); K at the LDS staging
+    # limits (16384 for M <= 4, 8192 for M <= 8) and past them (M = 8,
+    # K = 8200: the small-M kernel)
     _log(f"gemm stream {m}x{n}x{k} {dtype}")
     X = uniform((m, k), k=21, dtype=dtype)
     W = (uniform((n, k), k=22) * 0.05).to(dtype)
@@ -458,9 +461,10 @@ def test_gemm_stream_decode_shapes(m, n, k, dtype):
                     what=f"stream {dtype}", **tol)
 
 
-def test_gemm_stream_epilogue():
-    _log("gemm stream epilogue")
-    m, n, k = 4, 8192, 4096
+@pytest.mark.parametrize("n,k", [(8192, 4096), (6144, 4096), (4096, 12800)])
+def test_gemm_stream_epilogue(n, k):
+    _log(f"gemm stream epilogue n={n} k={k}")
+    m = 4
     X, W = uniform((m, k), k=23), uniform((n, k), k=24) * 0.02
     bias = uniform((n,), k=25)
     d = _gemm(X.to(DEV), W.to(DEV), trans_b=True, alpha=0.5, beta=1.5, c=bias.to(DEV), crow=0,
@@ -468,6 +472,11 @@ def test_gemm_stream_epilogue():
     want = O.gemm(X.numpy(), W.numpy().T, alpha=0.5, beta=1.5, c=bias.numpy()[None, :],
                   epilogue="silu")
     assert_close_fp(d, want, what="stream silu epilogue")
+    # the decode residual: D = x W^T + H with a full [m, n] H
+    H = uniform((m, n), k=26)
+    d2 = _gemm(X.to(DEV), W.to(DEV), trans_b=True, beta=1.0, c=H.to(DEV), crow=n, ccol=1)
+    assert_close_fp(d2, O.gemm(X.numpy(), W.numpy().T, beta=1.0, c=H.numpy()),
+                    what="stream residual epilogue")
 
 
 @pytest.mark.parametrize("m,n,k,pad", [(256, 128, 64, 0), (512, 384, 256, 8), (1024, 1280, 4096, 0),
@@ -919,6 +928,42 @@ def test_reduce_argmax_ties_nan_and_ints():
     assert torch.equal(s.cpu(), ints.long().sum(0, keepdim=True))
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("start", [0, 1, 3, 7])
+def test_reduce_long_rows_vector_path(dtype, start):
+    """Rows of >= 8192 contiguous elements (the LM-head argmax shape) take
+    the vectorised one-workgroup-per-row path: rows that start off a
+    16-byte boundary, ties placed in the unaligned head, the body and the
+    tail, NaNs, and every op of that path against torch on the CPU."""
+    _log(f"reduce long rows dtype={dtype} start={start}")
+    n = 49155
+    base = randn((5, n + 8), k=11).to(dtype)
+    top = torch.tensor(9.0, dtype=dtype)
+    base[0, start + 1] = top            # tie between the head ...
+    base[0, start + 30000] = top        # ... and the body
+    base[1, start + n - 1] = top        # maximum in the tail
+    base[1, start + 40] = top           # ... tied with an earlier body element
+    base[2, start + 5000] = float("nan")
+    base[2, start + 7000] = float("nan")
+    base[3, start + 2] = -top           # minimum in the head
+    x = base[:, start:start + n]        # rows start `start` elements in
+    xd = base.to(DEV)[:, start:start + n]
+    xf = x.float()
+    for op, fn in [(4, lambda t: torch.argmax(t, 1, keepdim=True)),
+                   (5, lambda t: torch.argmin(t, 1, keepdim=True))]:
+        got = _reduce(op, xd, [1], out_dtype=torch.int64)
+        assert torch.equal(got.cpu(), fn(xf)), f"op {op}"
+    for op, fn in [(2, lambda t: t.amax(1, keepdim=True)), (3, lambda t: t.amin(1, keepdim=True))]:
+        got = _reduce(op, xd, [1])
+        torch.testing.assert_close(got.cpu().float(), fn(xf).to(dtype).float(), rtol=0, atol=0,
+                                   equal_nan=True, msg=f"op {op}")
+    fin = base[[0, 1, 3, 4], start:start + n].contiguous().to(DEV)   # rows without NaN
+    ff = base[[0, 1, 3, 4], start:start + n].float()
+    for op, fn in [(0, lambda t: t.sum(1, keepdim=True)), (1, lambda t: t.mean(1, keepdim=True))]:
+        got = _reduce(op, fin, [1], out_dtype=torch.float32)
+        torch.testing.assert_close(got.cpu(), fn(ff.double()).float(), rtol=1e-4, atol=1e-3)
+
+
 # ---------------------------------------------------------------------------
 # data movement
 # ---------------------------------------------------------------------------
@@ -1076,6 +1121,99 @@ def test_attention_decode_vs_oracle(b, mq, sk, dtype):
     got = _decode(qd, kd, vd, scale, dtype=dtype)
     want = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), scale)
     assert_close_fp(got, want, out_dtype=dtype, what="decode no mask", **tol)
+
+
+def _step_call(qkv, cs, sn, pos_d, err, kc, vc, H, Hkv, L, scale, v_dim_major, out, ws):
+    dt = DT[qkv.dtype]
+    if v_dim_major:  # vc [B, Hkv, 128, L]
+        vks, vds = 1, vc.stride(2)
+    else:            # vc [B, Hkv, L, 128]
+        vks, vds = vc.stride(2), 1
+    _capi.call("sph_decode_attention_step", dt, qkv.shape[0], H, Hkv, 128, _p(qkv),
+               qkv.stride(0), _p(cs), _p(sn), cs.stride(0), _p(pos_d), _p(err), _p(kc),
+               kc.stride(0), kc.stride(1), kc.stride(2), _p(vc), vc.stride(0), vc.stride(1),
+               vks, vds, L, scale, _p(out), out.stride(0), _p(ws), ws.numel(), _stream())
+    _sync()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,H,Hkv,L,v_dim_major", [(4, 32, 8, 1152, True), (4, 32, 8, 1152, False),
+                                                   (2, 8, 8, 200, True), (1, 16, 2, 65, False),
+                                                   (3, 24, 3, 130, False), (3, 24, 3, 136, True),
+                                                   (2, 16, 4, 70, True)])
+def test_decode_attention_step_vs_oracle(dtype, B, H, Hkv, L, v_dim_major):
+    """The fused decode step (RoPE of q / k at pos, cache append, attention
+    over keys 0..pos) against the oracle's restatement, for a sequence of
+    positions on the same caches (first key, chunk edges, the last slot):
+    out at 1e-2, the appended value bit-exact, the appended key within one
+    element-type step of the oracle's rounding, every other cache entry
+    unchanged; a position past the cache sets the error word and writes
+    nothing."""
+    from oracle import decoder as OD
+
+    _log(f"decode step B={B} H={H} Hkv={Hkv} L={L} vdm={v_dim_major} {dtype}")
+    D = 128
+    kc = randn((B, Hkv, L, D), k=81).to(dtype)     # earlier steps' contents
+    vc = randn((B, Hkv, L, D), k=82).to(dtype)
+    ang = torch.arange(L, dtype=torch.float32)[:, None] * \
+        (1e4 ** (-torch.arange(0, D, 2, dtype=torch.float32) / D))[None, :]
+    ang = torch.cat([ang, ang], -1)
+    cs, sn = ang.cos().to(dtype), ang.sin().to(dtype)
+    kcd = kc.to(DEV)
+    vcd = (vc.transpose(2, 3).contiguous() if v_dim_major else vc).to(DEV)
+    csd, snd = cs.to(DEV), sn.to(DEV)
+    scale = 1.0 / math.sqrt(D)
+    nws = _capi.lib().sph_decode_attention_step_workspace_bytes(B, H, Hkv, L)
+    ws = torch.empty(nws, dtype=torch.uint8, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = torch.empty(B, H * D, dtype=dtype, device=DEV)
+    want_k, want_v = kc.float().numpy(), vc.float().numpy()
+    act = np.float16 if dtype == torch.float16 else "bfloat16"
+    tol = dict(rtol=1e-2, atol=1e-2) if dtype == torch.float16 else dict(rtol=2e-2, atol=2e-2)
+    positions = sorted({0, 63, 64, min(1000, L - 2), L - 1})
+    for n, pos in enumerate(positions):
+        qkv = randn((B, (H + 2 * Hkv) * D), k=90 + n).to(dtype)
+        pos_d = torch.tensor([pos], dtype=torch.int64, device=DEV)
+        _step_call(qkv.to(DEV), csd, snd, pos_d, err, kcd, vcd, H, Hkv, L, scale, v_dim_major,
+                   out, ws)
+        o_want, want_k2, want_v2 = OD.decode_step_attention(
+            qkv.float().numpy(), cs.float().numpy(), sn.float().numpy(), pos, want_k, want_v,
+            H, Hkv, scale, act=act)
+        assert_close_fp(out, o_want, out_dtype=dtype, what=f"decode step out pos={pos}", **tol)
+        got_k = kcd.cpu().float().numpy()
+        got_v = vcd.cpu().float()
+        got_v = (got_v.transpose(2, 3) if v_dim_major else got_v).numpy()
+        # the appended value is a copy; the appended key is RoPE in fp32
+        # rounded once (one step of the element type apart at most)
+        assert np.array_equal(got_v[:, :, pos], want_v2[:, :, pos])
+        step = np.abs(want_k2[:, :, pos]) * (2.0 ** -10 if dtype == torch.float16 else 2.0 ** -7)
+        assert np.all(np.abs(got_k[:, :, pos] - want_k2[:, :, pos]) <= step + 1e-6)
+        others = np.ones(L, bool)
+        others[pos] = False
+        assert np.array_equal(got_k[:, :, others], want_k2[:, :, others])
+        assert np.array_equal(got_v[:, :, others], want_v2[:, :, others])
+        # later positions read what this call stored
+        want_k, want_v = got_k, got_v
+        assert int(err.cpu()[0]) == 0
+    # a position outside the cache: error word 2, caches untouched
+    before_k, before_v = kcd.clone(), vcd.clone()
+    for bad in (L, -1):
+        pos_d = torch.tensor([bad], dtype=torch.int64, device=DEV)
+        _step_call(qkv.to(DEV), csd, snd, pos_d, err, kcd, vcd, H, Hkv, L, scale, v_dim_major,
+                   out, ws)
+        assert int(err.cpu()[0]) == 2
+        err.zero_()
+        assert torch.equal(kcd, before_k) and torch.equal(vcd, before_v)
+    # and the next valid call still merges correctly (arrival counts intact)
+    pos = positions[-2]
+    qkv = randn((B, (H + 2 * Hkv) * D), k=99).to(dtype)
+    pos_d = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    _step_call(qkv.to(DEV), csd, snd, pos_d, err, kcd, vcd, H, Hkv, L, scale, v_dim_major, out,
+               ws)
+    o_want, _, _ = OD.decode_step_attention(qkv.float().numpy(), cs.float().numpy(),
+                                            sn.float().numpy(), pos, want_k, want_v, H, Hkv,
+                                            scale, act=act)
+    assert_close_fp(out, o_want, out_dtype=dtype, what="decode step after errors", **tol)
 
 
 def test_attention_decode_causal_and_empty_rows():

@@ -32,6 +32,10 @@ at::Tensor gemm_rmsnorm(const at::Tensor& x, const at::Tensor& norm_w, double ep
 at::Tensor attention_fwd(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                          const c10::optional<at::Tensor>& mask, double scale, int64_t causal_q,
                          int64_t causal_off);
+at::Tensor decode_attention_step(const at::Tensor& qkv, const at::Tensor& cos,
+                                 const at::Tensor& sin, const at::Tensor& pos,
+                                 at::Tensor& k_cache, at::Tensor& v_cache, int64_t n_heads,
+                                 int64_t n_kv_heads, double scale, bool v_dim_major);
 }  // namespace spyre
 
 PYBIND11_MODULE(_C, m) {
@@ -66,6 +70,13 @@ PYBIND11_MODULE(_C, m) {
         py::arg("mask"), py::arg("scale"), py::arg("causal_q") = 0, py::arg("causal_off") = 0,
         "softmax(scale * q k^T + mask) v on the spyre stream (q [B, mq, 128], k / v "
         "[B, sk, 128], mask [mq, sk] / [B or 1, mq, sk] or None; fp16 / bf16).");
+  m.def("decode_attention_step", &spyre::decode_attention_step, py::arg("qkv"), py::arg("cos"),
+        py::arg("sin"), py::arg("pos"), py::arg("k_cache"), py::arg("v_cache"),
+        py::arg("n_heads"), py::arg("n_kv_heads"), py::arg("scale"),
+        py::arg("v_dim_major") = false,
+        "One decode step of grouped-query attention: RoPE of the step's queries and key at "
+        "*pos, the key / value appended to the caches in place, attention over keys 0..pos "
+        "(qkv [B, (H + 2 Hkv) * 128]) -> [B, H * 128].");
   m.def("gemm_swiglu", &spyre::gemm_swiglu, py::arg("x"), py::arg("w"),
         "silu(x w[:n]^T) * (x w[n:]^T) on the spyre stream (x [M, K], w [2n, K]).");
   m.def("gemm_rmsnorm", &spyre::gemm_rmsnorm, py::arg("x"), py::arg("norm_w"), py::arg("eps"),

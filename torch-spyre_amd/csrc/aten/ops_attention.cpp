@@ -118,3 +118,83 @@ at::Tensor attention_fwd(const at::Tensor& q_in, const at::Tensor& k_in, const a
 }
 
 }  // namespace spyre
+
+namespace spyre {
+
+// One decode step of attention with its KV-cache append
+// (sph_decode_attention_step): qkv [B, (H + 2 Hkv) * 128] the step's
+// projection rows, cos / sin [max_len, 128] RoPE tables, pos a one-element
+// int64 spyre tensor holding the step's position, k_cache [B, Hkv, max_len,
+// 128] and v_cache [B, Hkv, max_len, 128], or with v_dim_major the
+// transposed buffer [B, Hkv, 128, max_len], updated in place; returns
+// [B, H * 128].  A position outside the caches raises at the next
+// synchronisation, as an out-of-range gather does.
+at::Tensor decode_attention_step(const at::Tensor& qkv_in, const at::Tensor& cos_in,
+                                 const at::Tensor& sin_in, const at::Tensor& pos,
+                                 at::Tensor& k_cache, at::Tensor& v_cache, int64_t n_heads,
+                                 int64_t n_kv_heads, double scale, bool v_dim_major) {
+  TORCH_CHECK(is_spyre(qkv_in) && is_spyre(cos_in) && is_spyre(sin_in) && is_spyre(pos) &&
+                  is_spyre(k_cache) && is_spyre(v_cache),
+              "spyre decode_attention: every argument must be a spyre tensor");
+  const at::ScalarType dt = qkv_in.scalar_type();
+  TORCH_CHECK(dt == at::kHalf || dt == at::kBFloat16,
+              "spyre decode_attention: dtype must be fp16 or bf16");
+  TORCH_CHECK(cos_in.scalar_type() == dt && sin_in.scalar_type() == dt &&
+                  k_cache.scalar_type() == dt && v_cache.scalar_type() == dt,
+              "spyre decode_attention: qkv, tables and caches must share one dtype");
+  TORCH_CHECK(pos.scalar_type() == at::kLong && pos.numel() == 1,
+              "spyre decode_attention: pos must be a one-element int64 tensor");
+  TORCH_CHECK(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0,
+              "spyre decode_attention: n_heads must be a multiple of n_kv_heads");
+  constexpr int64_t D = 128;
+  TORCH_CHECK(qkv_in.dim() == 2 && qkv_in.size(1) == (n_heads + 2 * n_kv_heads) * D,
+              "spyre decode_attention: qkv must be [batch, (n_heads + 2 n_kv_heads) * 128]");
+  const int64_t B = qkv_in.size(0);
+  TORCH_CHECK(k_cache.dim() == 4 && k_cache.size(0) == B && k_cache.size(1) == n_kv_heads &&
+                  k_cache.size(3) == D && k_cache.stride(3) == 1,
+              "spyre decode_attention: k_cache must be [batch, n_kv_heads, max_len, 128] with "
+              "unit dim stride");
+  const int64_t L = k_cache.size(2);
+  TORCH_CHECK(v_cache.dim() == 4 && v_cache.size(0) == B && v_cache.size(1) == n_kv_heads,
+              "spyre decode_attention: v_cache must be [batch, n_kv_heads, ...]");
+  TORCH_CHECK(v_dim_major ? (v_cache.size(2) == D && v_cache.size(3) == L && v_cache.stride(3) == 1)
+                          : (v_cache.size(2) == L && v_cache.size(3) == D && v_cache.stride(3) == 1),
+              "spyre decode_attention: v_cache must be [batch, n_kv_heads, max_len, 128], or "
+              "with v_dim_major [batch, n_kv_heads, 128, max_len], with unit last stride");
+  TORCH_CHECK(cos_in.dim() == 2 && cos_in.size(0) >= L && cos_in.size(1) == D &&
+                  sin_in.sizes() == cos_in.sizes(),
+              "spyre decode_attention: cos / sin must be [>= max_len, 128]");
+  at::Tensor qkv = qkv_in.stride(1) == 1 && (qkv_in.stride(0) % 8 == 0 || B == 1)
+                       ? qkv_in
+                       : contiguous_on_device(qkv_in);
+  at::Tensor cs = cos_in.stride(1) == 1 ? cos_in : contiguous_on_device(cos_in);
+  at::Tensor sn = sin_in.strides() == cs.strides() ? sin_in : contiguous_on_device(sin_in);
+  if (sn.strides() != cs.strides()) cs = contiguous_on_device(cs);
+  at::Tensor out = empty_spyre({B, n_heads * D}, dt, qkv.device());
+  if (B == 0) return out;
+  const int64_t v_ks = v_dim_major ? 1 : v_cache.stride(2);
+  const int64_t v_ds = v_dim_major ? v_cache.stride(2) : 1;
+  const int64_t ks[4] = {B, n_kv_heads, L, D};
+  const int64_t kst[4] = {k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), 1};
+  const int64_t vst[4] = {v_cache.stride(0), v_cache.stride(1), v_ks, v_ds};
+  check_extent(k_cache, k_cache.data_ptr(), 4, ks, kst, k_cache.element_size(), "k_cache");
+  check_extent(v_cache, v_cache.data_ptr(), 4, ks, vst, v_cache.element_size(), "v_cache");
+  const int64_t qs[2] = {B, qkv.size(1)}, qst[2] = {qkv.stride(0), 1};
+  check_extent(qkv, qkv.data_ptr(), 2, qs, qst, qkv.element_size(), "qkv");
+  const int64_t ts[2] = {L, D}, tst[2] = {cs.stride(0), 1};
+  check_extent(cs, cs.data_ptr(), 2, ts, tst, cs.element_size(), "cos");
+  check_extent(sn, sn.data_ptr(), 2, ts, tst, sn.element_size(), "sin");
+  const int64_t nws = sph_decode_attention_step_workspace_bytes(B, n_heads, n_kv_heads, L);
+  at::Tensor ws = empty_spyre({nws}, at::kByte, qkv.device());
+  c10::DeviceGuard guard(qkv.device());
+  const int dev = qkv.get_device();
+  SPYRE_SPH_CHECK(sph_decode_attention_step(
+      to_sph(dt), B, n_heads, n_kv_heads, D, qkv.data_ptr(), qkv.stride(0), cs.data_ptr(),
+      sn.data_ptr(), cs.stride(0), pos.data_ptr<int64_t>(), device_error_word(dev),
+      k_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+      v_cache.data_ptr(), v_cache.stride(0), v_cache.stride(1), v_ks, v_ds, L,
+      static_cast<float>(scale), out.data_ptr(), out.stride(0), ws.data_ptr(), nws, stream(dev)));
+  return out;
+}
+
+}  // namespace spyre

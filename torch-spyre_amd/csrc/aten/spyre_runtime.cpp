@@ -134,6 +134,9 @@ void check_device_errors(int device) {
     if (w == nullptr || *w == 0) continue;
     const int32_t code = *w;
     *w = 0;
+    if (code == 2)
+      TORCH_CHECK_INDEX(false, "spyre: decode attention position outside the KV cache on "
+                        "spyre:", d, " (code 2); the step wrote nothing");
     TORCH_CHECK_INDEX(false, "spyre: index out of range in a gather on spyre:", d,
                       " (index_select / embedding / an indexed load of a compiled kernel; "
                       "code ", code, "); the rows of out-of-range indices were zero-filled");

@@ -377,3 +377,385 @@ extern "C" int sph_attention_decode(sph_dtype dtype, int64_t batch, int64_t mq, 
   }
   return check_launch("sph_attention_decode");
 }
+
+// ---------------------------------------------------------------------------
+// One decode step of attention with its KV-cache append, for a model's
+// whole batch in one launch: for every (batch entry b, KV head h) "unit",
+// the unit's G query heads and its new key / value are read from the
+// projection row qkv[b] (query heads first, then the KV heads' keys, then
+// their values, 128 each), the queries and the new key are rotated by RoPE
+// at position P = *pos (rotate-half: x cos + rot(x) sin, rot(x) = (-x2, x1),
+// tables cos / sin [max_len, 128]), the key and value are written into the
+// caches at P, and O = softmax(scale q K[0..P]^T) V[0..P] is written to
+// out[b] (query head j at columns j * 128).
+//
+// Layout: K cache [.., max_len, 128] key-major (dim stride 1); V cache
+// key-major or dim-major ([.., 128, max_len], key stride 1, the layout the
+// decoder's caches keep).  Each workgroup takes one unit and one 64-key
+// chunk (grid = chunks of max_len x units; P is only known on the device,
+// so chunks past P do nothing but report), stages the chunk's K and V in
+// LDS while the queries are rotated, computes the G x 64 scores (one key
+// per lane, one query head per wave), their softmax state (max, sum) and
+// the unnormalised G x 128 output and writes that partial to the
+// workspace (a chunk past P writes a neutral one); a second kernel merges
+// each unit's partials and writes O.  (Merging in the last workgroup of a unit to arrive,
+// behind an atomic count, needs a device-scope release per workgroup: on
+// this 8-XCD part each one writes back the XCD's L2, and 576 of them took
+// 87 us against a few for the two launches.)  The chunk holding P takes the
+// new key and value from the rotated registers, not from the cache it
+// writes in the same launch.
+//
+// Rounding: rotated q and k round once to the element type (k as it is
+// stored); scores, softmax and the output sums are fp32; O rounds once.
+// ---------------------------------------------------------------------------
+namespace sph {
+namespace {
+
+constexpr int SG = 8;              // max query heads per KV head
+constexpr int SKC = 64;            // keys per chunk
+constexpr int kStepThreads = 256;  // 4 waves
+constexpr int kMaxUnits = 4096;    // batch x KV heads per launch
+constexpr int kStepPart = 2 + DD;  // m, l, o[128] per query head
+constexpr int32_t kStepBadPos = 2;  // error code: position outside [0, max_len)
+
+struct StepArgs {
+  const void* qkv;
+  int64_t ld_qkv;
+  const void* cos;
+  const void* sin;
+  int64_t ld_rope;
+  const int64_t* pos;
+  int32_t* err;  // device error word: set to kStepBadPos for P outside the cache
+  void* kc;
+  int64_t k_sb, k_sh, k_ss;
+  void* vc;
+  int64_t v_sb, v_sh, v_ks, v_ds;
+  int v_al;  // dim-major V rows 16-byte aligned (else read element by element)
+  int64_t max_len;
+  int n_heads, n_kv, g, nchunks;
+  float scale_log2;
+  void* out;
+  int64_t ld_out;
+  float* part;  // [units][nchunks][g][kStepPart]
+};
+
+__device__ inline u32x4 zero_chunk() {
+  u32x4 z = {0u, 0u, 0u, 0u};
+  return z;
+}
+
+
+template <typename T, bool VT>
+__global__ void __launch_bounds__(kStepThreads) attn_decode_step_kernel(const StepArgs p) {
+  __shared__ __attribute__((aligned(16))) T ks[SKC][KPITCH];
+  __shared__ __attribute__((aligned(16))) T vs[VT ? DD : SKC][VT ? VPITCH_T : KPITCH];
+  __shared__ __attribute__((aligned(16))) float qs[SG][DD];
+  __shared__ __attribute__((aligned(16))) float ps[SG][SKC];
+  __shared__ float mrow[SG], lrow[SG];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int unit = blockIdx.y, chunk = blockIdx.x;
+  const int b = unit / p.n_kv, h = unit % p.n_kv, G = p.g;
+  const int64_t kbase = static_cast<int64_t>(chunk) * SKC;
+  T* Kc = static_cast<T*>(p.kc) + b * p.k_sb + h * p.k_sh;
+  T* Vc = static_cast<T*>(p.vc) + b * p.v_sb + h * p.v_sh;
+  const T* row = static_cast<const T*>(p.qkv) + b * p.ld_qkv;
+  // The chunk's K / V (speculatively: the whole chunk, before P is known;
+  // every address is inside the cache) and P itself are loaded together.
+  const int64_t P = *p.pos;
+  const int kmax = static_cast<int>(min<int64_t>(SKC, p.max_len - kbase));
+  u32x4 kr[4], vr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int x = t + kStepThreads * i, key = x >> 4, cc = (x & 15) * 8;
+    kr[i] = key < kmax ? *reinterpret_cast<const u32x4*>(Kc + (kbase + key) * p.k_ss + cc)
+                       : zero_chunk();
+    if constexpr (VT) {
+      const int dm = x >> 3, kc = (x & 7) * 8;
+      const T* src = Vc + dm * p.v_ds + kbase + kc;
+      if (p.v_al && kc + 8 <= kmax) {
+        vr[i] = *reinterpret_cast<const u32x4*>(src);
+      } else {
+        // the cache's last, partial chunk, or rows that are not 16-byte
+        // aligned: element loads, zeros past the cache
+        const uint16_t* s16 = reinterpret_cast<const uint16_t*>(src);
+        uint32_t e[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) e[j] = kc + j < kmax ? s16[j] : 0u;
+        vr[i] = u32x4{e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16),
+                      e[6] | (e[7] << 16)};
+      }
+    } else {
+      vr[i] = key < kmax ? *reinterpret_cast<const u32x4*>(Vc + (kbase + key) * p.v_ks + cc)
+                         : zero_chunk();
+    }
+  }
+  // The step's queries (element d and its rotate-half partner) and the new
+  // key / value do not depend on P either.
+  constexpr int QR = SG * DD / kStepThreads;  // query elements per thread
+  const int dq = t & (DD - 1), dpart = dq < DD / 2 ? dq + DD / 2 : dq - DD / 2;
+  float qa[QR], qb[QR];
+#pragma unroll
+  for (int r = 0; r < QR; ++r) {
+    const int i = (t + kStepThreads * r) / DD;
+    const T* q = row + static_cast<int64_t>(h * G + (i < G ? i : 0)) * DD;
+    qa[r] = Num<T>::to_f(q[dq]);
+    qb[r] = Num<T>::to_f(q[dpart]);
+  }
+  const T* knew = row + static_cast<int64_t>(p.n_heads + h) * DD;
+  const T* vnew = row + static_cast<int64_t>(p.n_heads + p.n_kv + h) * DD;
+  const float ka = Num<T>::to_f(knew[dq]), kb = Num<T>::to_f(knew[dpart]);
+  const T vv = vnew[dq];
+  if (P < 0 || P >= p.max_len) {
+    // nothing is written (every workgroup sees the same P); the caller's
+    // error word reports it
+    if (t == 0 && chunk == 0 && unit == 0 && p.err != nullptr) *p.err = kStepBadPos;
+    return;
+  }
+  const bool active = kbase <= P;
+  float* part = p.part + (static_cast<int64_t>(unit) * p.nchunks + chunk) * G * kStepPart;
+  if (!active) {
+    // a chunk past P: a neutral partial (m = -inf; the merge skips it)
+    if (t < G) {
+      part[t * kStepPart] = -INFINITY;
+      part[t * kStepPart + 1] = 0.f;
+    }
+    return;
+  }
+  {
+    const int nkeys = static_cast<int>(min<int64_t>(SKC, P + 1 - kbase));
+    const T* cs = static_cast<const T*>(p.cos) + P * p.ld_rope;
+    const T* sn = static_cast<const T*>(p.sin) + P * p.ld_rope;
+    const float cd = Num<T>::to_f(cs[dq]), sd = Num<T>::to_f(sn[dq]);
+    const float sgn = dq < DD / 2 ? -1.f : 1.f;  // rot(x)[d] = -x[d + 64] | x[d - 64]
+    // rotated queries (rounded as a stored tensor would be), scaled into
+    // log2 units
+#pragma unroll
+    for (int r = 0; r < QR; ++r) {
+      const int i = (t + kStepThreads * r) / DD;
+      if (i < G) {
+        const float rq = Num<T>::to_f(Num<T>::from_f(qa[r] * cd + sgn * qb[r] * sd));
+        qs[i][dq] = rq * p.scale_log2;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int x = t + kStepThreads * i, key = x >> 4, cc = (x & 15) * 8;
+      *reinterpret_cast<u32x4*>(&ks[key][cc]) = kr[i];
+      if constexpr (VT) {
+        const int dm = x >> 3, kc = (x & 7) * 8;
+        *reinterpret_cast<u32x4*>(&vs[dm][kc]) = vr[i];
+      } else {
+        *reinterpret_cast<u32x4*>(&vs[key][cc]) = vr[i];
+      }
+    }
+    const int own = static_cast<int>(P - kbase);  // the new key's slot, if here
+    __syncthreads();  // chunk staged: the new key / value replace slot `own`
+    if (own < SKC && t < DD) {
+      const T kr_ = Num<T>::from_f(ka * cd + sgn * kb * sd);
+      const T vr_ = vv;
+      ks[own][t] = kr_;
+      if constexpr (VT) vs[t][own] = vr_;
+      else vs[own][t] = vr_;
+      Kc[P * p.k_ss + t] = kr_;
+      if constexpr (VT) Vc[t * p.v_ds + P] = vr_;
+      else Vc[P * p.v_ks + t] = vr_;
+    }
+    __syncthreads();
+    // scores: key `lane`, query head i = wave, wave + 4
+    for (int i = wave; i < G; i += kStepThreads / 64) {
+      float s = 0.f;
+#pragma unroll
+      for (int cc = 0; cc < DD; cc += 8) {
+        const u32x4 kw = *reinterpret_cast<const u32x4*>(&ks[lane][cc]);
+        const T* ke = reinterpret_cast<const T*>(&kw);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s = fmaf(qs[i][cc + e], Num<T>::to_f(ke[e]), s);
+      }
+      s = lane < nkeys ? s : -INFINITY;
+      float mx = s;
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      const float pj = __builtin_amdgcn_exp2f(s - mx);  // key 0 of the chunk is visible
+      float sum = pj;
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+      ps[i][lane] = pj;
+      if (lane == 0) {
+        mrow[i] = mx;
+        lrow[i] = sum;
+      }
+    }
+    __syncthreads();
+    // unnormalised P V: column d, query heads i = t / 128, + 2, ...
+    const int d = t & (DD - 1);
+    for (int i = t >> 7; i < G; i += kStepThreads / DD) {
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < SKC; j += 8) {
+        float vf[8];
+        if constexpr (VT) {
+          const u32x4 vw = *reinterpret_cast<const u32x4*>(&vs[d][j]);
+          const T* ve = reinterpret_cast<const T*>(&vw);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vf[e] = Num<T>::to_f(ve[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vf[e] = Num<T>::to_f(vs[j + e][d]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = fmaf(ps[i][j + e], vf[e], acc);
+      }
+      part[i * kStepPart + 2 + d] = acc;
+      if (d == 0) {
+        part[i * kStepPart] = mrow[i];
+        part[i * kStepPart + 1] = lrow[i];
+      }
+    }
+  }
+}
+
+// Merge of one unit (blockIdx.x): the partials of the chunks holding keys
+// 0..P, O = sum_c 2^(m_c - M) o_c / sum_c 2^(m_c - M) l_c, M = max m_c.
+template <typename T>
+__global__ void __launch_bounds__(kStepThreads) attn_decode_step_merge(const StepArgs p) {
+  const int t = threadIdx.x, unit = blockIdx.x;
+  const int b = unit / p.n_kv, h = unit % p.n_kv, G = p.g;
+  // every chunk has a partial (those past P with m = -inf); P is read
+  // alongside them, only to write nothing when the step kernel refused it
+  const int nvis = p.nchunks;
+  const int64_t P = *p.pos;
+  const float* up = p.part + static_cast<int64_t>(unit) * p.nchunks * G * kStepPart;
+  T* O = static_cast<T*>(p.out) + b * p.ld_out + static_cast<int64_t>(h * G) * DD;
+  constexpr int NB = 16;  // partials loaded together (all loads in flight)
+  for (int x = t; x < G * DD; x += kStepThreads) {
+    const int i = x / DD, d = x % DD;
+    float M = -INFINITY, l = 0.f, acc = 0.f;
+    for (int c0 = 0; c0 < nvis; c0 += NB) {
+      float mm[NB], ll[NB], oo[NB];
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const int c = c0 + j < nvis ? c0 + j : nvis - 1;  // a valid partial
+        const float* pc = up + (c * G + i) * kStepPart;
+        const bool in = c0 + j < nvis;
+        mm[j] = in ? pc[0] : -INFINITY;
+        ll[j] = in ? pc[1] : 0.f;
+        oo[j] = in ? pc[2 + d] : 0.f;
+      }
+      float bm = M;
+#pragma unroll
+      for (int j = 0; j < NB; ++j) bm = fmaxf(bm, mm[j]);
+      // chunk 0 holds key 0, so bm is finite from the first batch on
+      const float sc = __builtin_amdgcn_exp2f(M - bm);
+      l *= sc;
+      acc *= sc;
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        // a neutral partial (m = -inf) carries no output sums
+        const bool live = mm[j] != -INFINITY;
+        const float w = __builtin_amdgcn_exp2f(mm[j] - bm);
+        l = live ? fmaf(ll[j], w, l) : l;
+        acc = live ? fmaf(oo[j], w, acc) : acc;
+      }
+      M = bm;
+    }
+    if (P >= 0 && P < p.max_len) O[static_cast<int64_t>(i) * DD + d] = Num<T>::from_f(acc / l);
+  }
+}
+
+}  // namespace
+}  // namespace sph
+
+extern "C" int64_t sph_decode_attention_step_workspace_bytes(int64_t batch, int64_t n_heads,
+                                                              int64_t n_kv_heads,
+                                                              int64_t max_len) {
+  if (batch <= 0 || n_kv_heads <= 0 || n_heads <= 0 || max_len <= 0) return 0;
+  const int64_t g = n_heads / n_kv_heads;
+  return batch * n_kv_heads * ((max_len + SKC - 1) / SKC) * g * kStepPart * 4;
+}
+
+extern "C" int sph_decode_attention_step(
+    sph_dtype dtype, int64_t batch, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+    const void* qkv, int64_t ld_qkv, const void* cos, const void* sin, int64_t ld_rope,
+    const int64_t* pos, int32_t* error_word, void* k_cache, int64_t k_stride_b, int64_t k_stride_h,
+    int64_t k_stride_s, void* v_cache, int64_t v_stride_b, int64_t v_stride_h,
+    int64_t v_key_stride, int64_t v_dim_stride, int64_t max_len, float scale, void* out,
+    int64_t ld_out, void* workspace, int64_t workspace_bytes, sph_stream_t stream) {
+  SPH_REQUIRE(dtype == SPH_F16 || dtype == SPH_BF16, SPH_ERR_UNSUPPORTED,
+              "decode attention step: dtype must be F16 or BF16");
+  SPH_REQUIRE(head_dim == DD, SPH_ERR_UNSUPPORTED, "decode attention step: head_dim must be 128");
+  SPH_REQUIRE(batch >= 0 && n_heads > 0 && n_kv_heads > 0 && max_len > 0, SPH_ERR_INVALID_ARG,
+              "decode attention step: bad sizes");
+  if (batch == 0) return SPH_OK;
+  SPH_REQUIRE(n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= SG, SPH_ERR_UNSUPPORTED,
+              "decode attention step: query heads per KV head must divide and be <= 8");
+  SPH_REQUIRE(batch * n_kv_heads <= kMaxUnits && max_len < (1LL << 30), SPH_ERR_TOO_LARGE,
+              "decode attention step: at most 4096 (batch x KV heads) and 2^30 positions");
+  SPH_REQUIRE(scale > 0.f && scale < INFINITY, SPH_ERR_INVALID_ARG,
+              "decode attention step: scale must be positive and finite");
+  SPH_REQUIRE(pos != nullptr && qkv != nullptr && k_cache != nullptr && v_cache != nullptr &&
+                  out != nullptr,
+              SPH_ERR_INVALID_ARG, "decode attention step: null pointer");
+  SPH_REQUIRE((v_dim_stride == 1 && v_key_stride >= DD) ||
+                  (v_key_stride == 1 && v_dim_stride >= max_len),
+              SPH_ERR_INVALID_ARG,
+              "decode attention step: V cache must be key-major or dim-major");
+  const bool vt = v_key_stride == 1 && v_dim_stride != 1;
+  SPH_REQUIRE(ld_qkv >= (n_heads + 2 * n_kv_heads) * DD && ld_rope >= DD && k_stride_s >= DD &&
+                  ld_out >= n_heads * DD,
+              SPH_ERR_INVALID_ARG, "decode attention step: leading dimension too small");
+  SPH_REQUIRE(al16d(k_cache) && k_stride_s % 8 == 0 && k_stride_h % 8 == 0 &&
+                  k_stride_b % 8 == 0,
+              SPH_ERR_INVALID_ARG, "decode attention step: K cache rows must be 16-byte aligned");
+  // V rows: key-major ones are read as 16-byte chunks and must be aligned;
+  // dim-major ones (max_len keys each) may have any length
+  const bool v_al = al16d(v_cache) && v_stride_b % 8 == 0 && v_stride_h % 8 == 0 &&
+                    (vt ? v_dim_stride : v_key_stride) % 8 == 0;
+  SPH_REQUIRE(vt || v_al, SPH_ERR_INVALID_ARG,
+              "decode attention step: key-major V cache rows must be 16-byte aligned");
+  SPH_REQUIRE((reinterpret_cast<uintptr_t>(v_cache) & 1u) == 0, SPH_ERR_INVALID_ARG,
+              "decode attention step: V cache must be 2-byte aligned");
+  const int64_t need =
+      sph_decode_attention_step_workspace_bytes(batch, n_heads, n_kv_heads, max_len);
+  SPH_REQUIRE(workspace != nullptr && workspace_bytes >= need, SPH_ERR_INVALID_ARG,
+              "decode attention step: workspace too small");
+  StepArgs p{};
+  p.qkv = qkv;
+  p.ld_qkv = ld_qkv;
+  p.cos = cos;
+  p.sin = sin;
+  p.ld_rope = ld_rope;
+  p.pos = pos;
+  p.err = error_word;
+  p.kc = k_cache;
+  p.k_sb = k_stride_b;
+  p.k_sh = k_stride_h;
+  p.k_ss = k_stride_s;
+  p.vc = v_cache;
+  p.v_sb = v_stride_b;
+  p.v_sh = v_stride_h;
+  p.v_ks = v_key_stride;
+  p.v_ds = v_dim_stride;
+  p.v_al = v_al ? 1 : 0;
+  p.max_len = max_len;
+  p.n_heads = static_cast<int>(n_heads);
+  p.n_kv = static_cast<int>(n_kv_heads);
+  p.g = static_cast<int>(n_heads / n_kv_heads);
+  p.nchunks = static_cast<int>((max_len + SKC - 1) / SKC);
+  p.scale_log2 = scale * kLog2eD;
+  p.out = out;
+  p.ld_out = ld_out;
+  p.part = static_cast<float*>(workspace);
+  hipStream_t st = as_stream(stream);
+  dim3 grid(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(batch * n_kv_heads));
+  const dim3 mgrid(static_cast<unsigned>(batch * n_kv_heads));
+  if (dtype == SPH_F16) {
+    if (vt) attn_decode_step_kernel<half_t, true><<<grid, kStepThreads, 0, st>>>(p);
+    else attn_decode_step_kernel<half_t, false><<<grid, kStepThreads, 0, st>>>(p);
+    attn_decode_step_merge<half_t><<<mgrid, kStepThreads, 0, st>>>(p);
+  } else {
+    if (vt) attn_decode_step_kernel<bf16_t, true><<<grid, kStepThreads, 0, st>>>(p);
+    else attn_decode_step_kernel<bf16_t, false><<<grid, kStepThreads, 0, st>>>(p);
+    attn_decode_step_merge<bf16_t><<<mgrid, kStepThreads, 0, st>>>(p);
+  }
+  return check_launch("sph_decode_attention_step");
+}

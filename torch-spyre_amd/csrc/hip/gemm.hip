@@ -1323,9 +1323,9 @@ int launch_skinny(const GemmArgs& p, int64_t batch, hipStream_t st) {
 
 // ---------------------------------------------------------------------------
 // Decode-shaped products (M <= 8 activation rows against a weight matrix
-// W[N, K] read once; batch 1, K from 1024 to 8192): the weight stream is
+// W[N, K] read once; batch 1, K from 1024 to 16384): the weight stream is
 // the whole cost, so the kernel is built to keep as many weight bytes in
-// flight as the CU allows.
+// flight as the CU allows and to give every wave the same share of them.
 //   * One 1024-thread workgroup per CU (persistent over the rows): the M x K
 //     activations are staged into LDS once and read from there (16-byte
 //     chunks, a wave's 64 lanes on 1 KB of consecutive bytes).
@@ -1334,9 +1334,17 @@ int launch_skinny(const GemmArgs& p, int64_t batch, hipStream_t st) {
 //     a flat sequence of (row, segment) items and loads item i+1 into one
 //     register buffer while it computes item i from the other, so loads of
 //     the next row are in flight while a row's sums are reduced and stored.
-//   * Rows go round-robin over all waves of the grid; at the end of a row the
-//     64 lane sums per activation row are reduced by butterflies and one lane
-//     writes the M outputs (with the epilogue: alpha, beta*C, activation).
+//   * Rows go round-robin over all W waves of the grid for the N / W whole
+//     rounds.  The N % W rows left over would leave most waves idle for a
+//     whole row time (gate/up of a 4096-wide model: 12800 rows = 3.125
+//     rounds of 4096), so each of them is split along K between Q waves of
+//     one workgroup (Q = 16 / the workgroup's leftover rows, rounded to a
+//     power of two): the slice is the last item of each of those waves, and
+//     after one workgroup barrier the first wave of each group adds the Q
+//     partial sums from LDS and writes the outputs.
+//   * At the end of a row the 64 lane sums per activation row are reduced by
+//     butterflies and one lane writes the M outputs (with the epilogue:
+//     alpha, beta*C, activation).
 // ---------------------------------------------------------------------------
 namespace gv {
 constexpr int WAVES = 16, THREADS = WAVES * 64, SEG = 8;
@@ -1355,16 +1363,41 @@ __global__ void __launch_bounds__(gv::THREADS) gemm_stream_kernel(const GemmArgs
   constexpr int NR = SWIGLU ? 2 : 1, SEGK = SEG / NR;  // rows per item, chunks per row
   __shared__ __attribute__((aligned(16))) uint16_t As[MT * KMAX];
   __shared__ float lds_ss[NORM ? WAVES * MT : 1];
+  __shared__ float lds_part[WAVES * NR * MT];  // partial sums of split rows
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nc = static_cast<int>(p.k / 8);           // 16-byte chunks per row
   const int mrows = static_cast<int>(p.m);
   const uint16_t* A = static_cast<const uint16_t*>(p.a);
   const uint16_t* B = static_cast<const uint16_t*>(p.b);
   T* D = static_cast<T*>(p.d);
-  const int cpl = (nc + 63) / 64;                      // chunks per lane
-  const int nseg = (cpl + SEGK - 1) / SEGK;            // segments per row
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * WAVES;
-  int64_t n = static_cast<int64_t>(blockIdx.x) * WAVES + wave;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * WAVES;  // W
+  const int64_t rounds = p.n / stride;                 // whole rounds
+  const int64_t main_end = rounds * stride;            // rows [0, main_end) whole
+  const int64_t left = p.n - main_end;                 // rows split along K
+  // This wave's slice of a split row: group `slot` of `qn` waves shares
+  // leftover row main_end + slot * gridDim.x + blockIdx.x; this wave holds
+  // chunks [tcb, tcb + tcn) of it.
+  int qn = 1, q = 0, slot = 0, tcb = 0, tcn = 0;
+  int64_t trow = -1;
+  if (left > 0) {
+    const int64_t G = gridDim.x;
+    const int rpw = static_cast<int>((left + G - 1) / G);  // <= WAVES
+    int p2 = 1;
+    while (p2 < rpw) p2 <<= 1;
+    qn = WAVES / p2;
+    while (qn > 1 && nc / qn < 64) qn >>= 1;  // at least one chunk per lane
+    slot = wave / qn;
+    q = wave % qn;
+    const int64_t t = static_cast<int64_t>(slot) * G + blockIdx.x;
+    if (slot < rpw && t < left) {
+      trow = main_end + t;
+      const int cs = (nc + qn - 1) / qn;
+      tcb = q * cs;
+      tcn = nc - tcb < cs ? nc - tcb : cs;
+    }
+  }
+  const int nseg = ((nc + 63) / 64 + SEGK - 1) / SEGK;            // segments of a row
+  const int tseg = ((tcn + 63) / 64 + SEGK - 1) / SEGK;           // of this wave's slice
   u32x4 wa[SEG], wb[SEG];
   float acc[NR][MT];
 #pragma unroll
@@ -1372,26 +1405,26 @@ __global__ void __launch_bounds__(gv::THREADS) gemm_stream_kernel(const GemmArgs
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[r][m] = 0.f;
 
-// Weight chunks of (ROW_, SEG_) into register buffer W_ (row r of the item
-// in entries r * SEGK ..; chunks past the row read a valid chunk that is
-// not summed).
-#define SPH_GV_LOAD(W_, ROW_, SEG_)                                                         \
+// Weight chunks of item (ROW_, chunks from CB_, segment SEG_) into register
+// buffer W_ (row r of the item in entries r * SEGK ..; chunks past the
+// range read a valid chunk that is not summed).
+#define SPH_GV_LOAD(W_, ROW_, CB_, SEG_)                                                    \
   do {                                                                                      \
     _Pragma("unroll") for (int r_ = 0; r_ < NR; ++r_) {                                     \
       const uint16_t* rp_ = B + ((ROW_) + r_ * p.n) * p.ldb;                                \
       _Pragma("unroll") for (int j_ = 0; j_ < SEGK; ++j_) {                                 \
-        int c_ = ((SEG_) * SEGK + j_) * 64 + lane;                                          \
+        int c_ = (CB_) + ((SEG_) * SEGK + j_) * 64 + lane;                                  \
         c_ = c_ < nc ? c_ : nc - 1;                                                         \
         W_[r_ * SEGK + j_] =                                                                \
             __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rp_ + c_ * 8));       \
       }                                                                                     \
     }                                                                                       \
   } while (0)
-#define SPH_GV_COMPUTE(W_, SEG_)                                                            \
+#define SPH_GV_COMPUTE(W_, CB_, CE_, SEG_)                                                  \
   do {                                                                                      \
     _Pragma("unroll") for (int j_ = 0; j_ < SEGK; ++j_) {                                   \
-      const int c_ = ((SEG_) * SEGK + j_) * 64 + lane;                                      \
-      if (c_ < nc) {                                                                        \
+      const int c_ = (CB_) + ((SEG_) * SEGK + j_) * 64 + lane;                              \
+      if (c_ < (CE_)) {                                                                     \
         _Pragma("unroll") for (int m_ = 0; m_ < MT; ++m_) {                                 \
           const u32x4 a_ = *reinterpret_cast<const u32x4*>(As + (m_ * nc + c_) * 8);        \
           _Pragma("unroll") for (int r_ = 0; r_ < NR; ++r_)                                 \
@@ -1400,29 +1433,53 @@ __global__ void __launch_bounds__(gv::THREADS) gemm_stream_kernel(const GemmArgs
       }                                                                                     \
     }                                                                                       \
   } while (0)
-// End of row ROW_: butterflies, lane m < M writes output (m, ROW_).
-#define SPH_GV_FINISH(ROW_)                                                                 \
+#define SPH_GV_REDUCE()                                                                     \
+  _Pragma("unroll") for (int r_ = 0; r_ < NR; ++r_)                                         \
+    _Pragma("unroll") for (int m_ = 0; m_ < MT; ++m_)                                       \
+      _Pragma("unroll") for (int o_ = 32; o_ > 0; o_ >>= 1)                                 \
+          acc[r_][m_] += __shfl_xor(acc[r_][m_], o_, 64)
+// Output of row ROW_ from its two (SWIGLU) or one sums S0_(m), S1_(m):
+// lane m < M writes element (m, ROW_).
+#define SPH_GV_STORE(ROW_, S0_, S1_)                                                        \
   do {                                                                                      \
-    _Pragma("unroll") for (int r_ = 0; r_ < NR; ++r_)                                       \
-      _Pragma("unroll") for (int m_ = 0; m_ < MT; ++m_)                                     \
-        _Pragma("unroll") for (int o_ = 32; o_ > 0; o_ >>= 1)                               \
-            acc[r_][m_] += __shfl_xor(acc[r_][m_], o_, 64);                                 \
     float v_ = 0.f;                                                                         \
     _Pragma("unroll") for (int m_ = 0; m_ < MT; ++m_) {                                     \
-      const float g_ = acc[0][m_] * rs[m_];                                                 \
-      const float x_ = SWIGLU ? silu(g_) * (acc[NR - 1][m_] * rs[m_]) : g_;                 \
+      const float g_ = (S0_) * rs[m_];                                                      \
+      const float x_ = SWIGLU ? silu(g_) * ((S1_) * rs[m_]) : g_;                           \
       v_ = lane == m_ ? x_ : v_;                                                            \
     }                                                                                       \
     if (lane < MT && lane < mrows)                                                          \
       D[lane * p.ldd + (ROW_)] = Num<T>::from_f(                                            \
           SWIGLU ? v_ : skinny_epilogue<T>(p, v_, 0, lane, (ROW_)));                        \
+  } while (0)
+// End of item (ROW_, SEG_) when it completes a row or a slice.
+#define SPH_GV_FINISH(ROW_, TAIL_)                                                          \
+  do {                                                                                      \
+    SPH_GV_REDUCE();                                                                        \
+    if (TAIL_) {                                                                            \
+      if (lane == 0) {                                                                      \
+        _Pragma("unroll") for (int r_ = 0; r_ < NR; ++r_)                                   \
+          _Pragma("unroll") for (int m_ = 0; m_ < MT; ++m_)                                 \
+            lds_part[(wave * NR + r_) * MT + m_] = acc[r_][m_];                             \
+      }                                                                                     \
+    } else {                                                                                \
+      SPH_GV_STORE(ROW_, acc[0][m_], acc[NR - 1][m_]);                                      \
+    }                                                                                       \
     _Pragma("unroll") for (int r_ = 0; r_ < NR; ++r_)                                       \
       _Pragma("unroll") for (int m_ = 0; m_ < MT; ++m_) acc[r_][m_] = 0.f;                  \
   } while (0)
 
+  // This wave's item sequence: segments 0..nseg-1 of rows n0, n0 + W, ...
+  // below main_end, then segments 0..tseg-1 of its split-row slice.
+  int64_t n = static_cast<int64_t>(blockIdx.x) * WAVES + wave;
+  int cb = 0, ce = nc, ns = nseg, s = 0;
+  bool tail = false, have = n < main_end;
+  if (!have && trow >= 0) {
+    n = trow, cb = tcb, ce = tcb + tcn, ns = tseg, tail = true, have = true;
+  }
   // The first weight loads go out before the activations are staged, so
   // the two latencies overlap.
-  if (n < p.n) SPH_GV_LOAD(wa, n, 0);
+  if (have) SPH_GV_LOAD(wa, n, cb, 0);
   // Stage the activations ([m][chunk], rows past M as zeros).
   float rs[MT];  // row scales of the RMSNorm prologue (1 without it)
 #pragma unroll
@@ -1461,55 +1518,101 @@ __global__ void __launch_bounds__(gv::THREADS) gemm_stream_kernel(const GemmArgs
 #pragma unroll
     for (int m = 0; m < MT; ++m) rs[m] = 1.f;
   }
-  if (n >= p.n) return;  // no barrier follows
-  // Items (row, segment) in order; item i+1 loads while item i computes.
-  int s = 0;
-  while (true) {
-    int64_t n2 = s + 1 == nseg ? n + stride : n;
-    int s2 = s + 1 == nseg ? 0 : s + 1;
-    const bool more = n2 < p.n;
-    if (more) SPH_GV_LOAD(wb, n2, s2);
-    SPH_GV_COMPUTE(wa, s);
-    if (s == nseg - 1) SPH_GV_FINISH(n);
-    if (!more) break;
-    n = n2;
-    s = s2;
-    n2 = s + 1 == nseg ? n + stride : n;
-    s2 = s + 1 == nseg ? 0 : s + 1;
-    const bool more2 = n2 < p.n;
-    if (more2) SPH_GV_LOAD(wa, n2, s2);
-    SPH_GV_COMPUTE(wb, s);
-    if (s == nseg - 1) SPH_GV_FINISH(n);
-    if (!more2) break;
-    n = n2;
-    s = s2;
+  // Items in order; item i+1 loads while item i computes.  (The next item
+  // of the last segment of a row: the next whole row, else the slice.)
+#define SPH_GV_NEXT(N2_, CB2_, CE2_, NS2_, S2_, T2_, MORE_)                                  \
+  do {                                                                                      \
+    N2_ = n, CB2_ = cb, CE2_ = ce, NS2_ = ns, S2_ = s + 1, T2_ = tail, MORE_ = true;        \
+    if (S2_ == ns) {                                                                        \
+      S2_ = 0;                                                                              \
+      if (!tail && n + stride < main_end) {                                                 \
+        N2_ = n + stride;                                                                   \
+      } else if (!tail && trow >= 0) {                                                      \
+        N2_ = trow, CB2_ = tcb, CE2_ = tcb + tcn, NS2_ = tseg, T2_ = true;                  \
+      } else {                                                                              \
+        MORE_ = false;                                                                      \
+      }                                                                                     \
+    }                                                                                       \
+  } while (0)
+  if (have) {
+    while (true) {
+      int64_t n2;
+      int cb2, ce2, ns2, s2;
+      bool t2, more;
+      SPH_GV_NEXT(n2, cb2, ce2, ns2, s2, t2, more);
+      if (more) SPH_GV_LOAD(wb, n2, cb2, s2);
+      SPH_GV_COMPUTE(wa, cb, ce, s);
+      if (s == ns - 1) SPH_GV_FINISH(n, tail);
+      if (!more) break;
+      n = n2, cb = cb2, ce = ce2, ns = ns2, s = s2, tail = t2;
+      SPH_GV_NEXT(n2, cb2, ce2, ns2, s2, t2, more);
+      if (more) SPH_GV_LOAD(wa, n2, cb2, s2);
+      SPH_GV_COMPUTE(wb, cb, ce, s);
+      if (s == ns - 1) SPH_GV_FINISH(n, tail);
+      if (!more) break;
+      n = n2, cb = cb2, ce = ce2, ns = ns2, s = s2, tail = t2;
+    }
   }
+  if (left > 0) {
+    // uniform: `left` is the same for every wave of the grid
+    __syncthreads();
+    if (trow >= 0 && q == 0) {
+      float s0[MT], s1[MT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) s0[m] = s1[m] = 0.f;
+      for (int qq = 0; qq < qn; ++qq) {
+        const int w = slot * qn + qq;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          s0[m] += lds_part[(w * NR) * MT + m];
+          s1[m] += lds_part[(w * NR + NR - 1) * MT + m];
+        }
+      }
+      SPH_GV_STORE(trow, s0[m_], s1[m_]);
+    }
+  }
+#undef SPH_GV_NEXT
 #undef SPH_GV_LOAD
 #undef SPH_GV_COMPUTE
+#undef SPH_GV_REDUCE
+#undef SPH_GV_STORE
 #undef SPH_GV_FINISH
 }
 
 // Streaming kernel fit: batch 1, M <= 8, K-contiguous 16-byte aligned rows,
-// K % 8 == 0 within the LDS staging size, and at least 32 M weights
-// (64 MB of fp16).  Measured on MI355X with cold weights, x[4, 4096]: W
-// [25600, 4096] 43.6 -> 37.9 us, [49155, 4096] 68.3 -> 65.0 us against the
-// small-M kernel; at 32-50 MB of weights both are set by fixed latency and
-// within noise of each other, so those stay on the small-M kernel.
+// K % 8 == 0 within the LDS staging size (16384 for M <= 4, else 8192),
+// and at least 8 M weights (16 MB of fp16): with the leftover rows split
+// along K every wave streams the same share, which beats the small-M
+// kernel's many short workgroups from the decode step's 32 MB O projection
+// up (measured on MI355X, x[4, 4096] and x[4, 12800]).
+constexpr int64_t kStreamMinWeights = 8LL << 20;
+
 inline bool stream_fits(const GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont) {
   return batch == 1 && p.m >= 1 && p.m <= 8 && a_kcont && b_kcont && p.vec_a && p.vec_b &&
-         p.k >= 1024 && p.k % 8 == 0 && p.k <= 8192 && p.n >= 1024 &&
-         p.n < (1LL << 40) && p.n * p.k >= (32LL << 20);
+         p.k >= 1024 && p.k % 8 == 0 && p.k <= (p.m <= 4 ? 16384 : 8192) && p.n >= 1024 &&
+         p.n < (1LL << 40) && p.n * p.k >= kStreamMinWeights;
+}
+
+inline unsigned stream_grid(int64_t n) {
+  constexpr int64_t kCUs = 256;  // one workgroup per MI355X compute unit
+  const int64_t wgs = ceil_div(n, gv::WAVES);
+  return static_cast<unsigned>(wgs < kCUs ? wgs : kCUs);
+}
+
+template <typename T, bool SWIGLU = false, bool NORM = false>
+void launch_stream_t(const GemmArgs& p, hipStream_t st) {
+  const unsigned grid = stream_grid(p.n);
+  if (p.m <= 4 && p.k > 8192)
+    gemm_stream_kernel<T, 4, 16384, SWIGLU, NORM><<<grid, dim3(gv::THREADS), 0, st>>>(p);
+  else if (p.m <= 4)
+    gemm_stream_kernel<T, 4, 8192, SWIGLU, NORM><<<grid, dim3(gv::THREADS), 0, st>>>(p);
+  else
+    gemm_stream_kernel<T, 8, 8192, SWIGLU, NORM><<<grid, dim3(gv::THREADS), 0, st>>>(p);
 }
 
 template <typename T>
 int launch_stream(const GemmArgs& p, hipStream_t st) {
-  constexpr int64_t kCUs = 256;  // one workgroup per MI355X compute unit
-  const int64_t wgs = ceil_div(p.n, gv::WAVES);
-  const unsigned grid = static_cast<unsigned>(wgs < kCUs ? wgs : kCUs);
-  if (p.m <= 4)
-    gemm_stream_kernel<T, 4, 8192><<<grid, dim3(gv::THREADS), 0, st>>>(p);
-  else
-    gemm_stream_kernel<T, 8, 8192><<<grid, dim3(gv::THREADS), 0, st>>>(p);
+  launch_stream_t<T>(p, st);
   return check_launch("sph_gemm (stream)");
 }
 

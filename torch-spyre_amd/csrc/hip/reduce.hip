@@ -247,6 +247,93 @@ __global__ void __launch_bounds__(kBlockRed) reduce_block(const RedArgs p) {
   }
 }
 
+// One 1024-thread workgroup per output for contiguous rows of 16-bit or
+// fp32 floats with the op fixed at compile time: every thread issues its
+// 16-byte loads U at a time before folding them, so a long row (an LM
+// head's 49155 logits) costs a few load round trips instead of one per
+// element.  Elements before the row's first 16-byte boundary and after
+// its last whole chunk are folded one by one.  A thread's elements come in
+// increasing index order, so the fold's tie and NaN rules (first index
+// wins) carry over unchanged.
+template <typename T>
+__device__ inline float as_f(T v) {
+  if constexpr (__is_same(T, float)) return v;
+  else return Num<T>::to_f(v);
+}
+
+template <typename T, int OP>
+__global__ void __launch_bounds__(kBlockRed) reduce_rows_vec(const RedArgs p) {
+  constexpr int VE = 16 / sizeof(T), U = 4;
+  __shared__ float sv[kBlockRed / 64];
+  __shared__ int64_t si[kBlockRed / 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t n = p.inner_numel;
+  for (int64_t o = blockIdx.x; o < p.outer_numel; o += gridDim.x) {
+    int64_t in_off, out_off;
+    outer_offsets(p, o, in_off, out_off);
+    const T* row = static_cast<const T*>(p.in) + in_off;
+    const int64_t mis = (reinterpret_cast<uintptr_t>(row) & 15) / sizeof(T);
+    const int64_t head = mis == 0 ? 0 : (VE - mis < n ? VE - mis : n);
+    const int64_t nchunks = (n - head) / VE;
+    const int64_t tail0 = head + nchunks * VE;
+    Acc<float> a = init_acc<float>(OP);
+    if (threadIdx.x < head) fold<float>(OP, a, as_f<T>(row[threadIdx.x]), threadIdx.x);
+    const u32x4* body = reinterpret_cast<const u32x4*>(row + head);
+    for (int64_t c0 = threadIdx.x; c0 < nchunks; c0 += static_cast<int64_t>(kBlockRed) * U) {
+      u32x4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t c = c0 + static_cast<int64_t>(u) * kBlockRed;
+        v[u] = body[c < nchunks ? c : c0];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t c = c0 + static_cast<int64_t>(u) * kBlockRed;
+        if (c < nchunks) {
+          const T* e = reinterpret_cast<const T*>(&v[u]);
+#pragma unroll
+          for (int j = 0; j < VE; ++j) fold<float>(OP, a, as_f<T>(e[j]), head + c * VE + j);
+        }
+      }
+    }
+    if (tail0 + threadIdx.x < n)
+      fold<float>(OP, a, as_f<T>(row[tail0 + threadIdx.x]), tail0 + threadIdx.x);
+    // the head and tail elements may carry a larger index than the body's:
+    // combine() orders ties by index, so the order of folding does not matter
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      Acc<float> b = shfl_acc<float>(a, off);
+      combine<float>(OP, a, b);
+    }
+    if (lane == 0) {
+      sv[wave] = a.v;
+      si[wave] = a.idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      Acc<float> r{sv[0], si[0]};
+      for (int w = 1; w < kBlockRed / 64; ++w) {
+        Acc<float> b{sv[w], si[w]};
+        combine<float>(OP, r, b);
+      }
+      finish<float>(p, out_off, r);
+    }
+    __syncthreads();
+  }
+}
+
+template <typename T>
+void launch_rows_vec(const RedArgs& p, unsigned g, hipStream_t st) {
+  switch (p.op) {
+    case SPH_RED_ARGMAX: reduce_rows_vec<T, SPH_RED_ARGMAX><<<g, kBlockRed, 0, st>>>(p); break;
+    case SPH_RED_ARGMIN: reduce_rows_vec<T, SPH_RED_ARGMIN><<<g, kBlockRed, 0, st>>>(p); break;
+    case SPH_RED_MAX: reduce_rows_vec<T, SPH_RED_MAX><<<g, kBlockRed, 0, st>>>(p); break;
+    case SPH_RED_MIN: reduce_rows_vec<T, SPH_RED_MIN><<<g, kBlockRed, 0, st>>>(p); break;
+    case SPH_RED_SUM: reduce_rows_vec<T, SPH_RED_SUM><<<g, kBlockRed, 0, st>>>(p); break;
+    default: reduce_rows_vec<T, SPH_RED_MEAN><<<g, kBlockRed, 0, st>>>(p); break;
+  }
+}
+
 // One thread per output.
 template <typename A>
 __global__ void __launch_bounds__(256) reduce_thread(const RedArgs p) {
@@ -318,7 +405,20 @@ extern "C" int sph_reduce(int op, const sph_operand* in, const sph_operand* out,
     if (g > 65536) g = 65536;
     return static_cast<unsigned>(g < 1 ? 1 : g);
   };
-  if (inner_contig && p.inner_numel >= 8192 && p.outer_numel < 2048) {
+  // the vector path: one contiguous reduced dim of a 16-bit or fp32 float
+  // input, an op whose fp32 accumulation matches the generic path's
+  const bool vec_op = op == SPH_RED_ARGMAX || op == SPH_RED_ARGMIN || op == SPH_RED_MAX ||
+                      op == SPH_RED_MIN || op == SPH_RED_SUM || op == SPH_RED_MEAN;
+  const bool vec_in = in->dtype == SPH_F16 || in->dtype == SPH_BF16 || in->dtype == SPH_F32;
+  const bool vec_out = arg || out->dtype == SPH_F16 || out->dtype == SPH_BF16 ||
+                       out->dtype == SPH_F32;
+  if (inner_contig && p.n_inner == 1 && vec_op && vec_in && vec_out &&
+      p.inner_numel >= 8192 && p.outer_numel < 2048) {
+    const unsigned g = static_cast<unsigned>(p.outer_numel);
+    if (in->dtype == SPH_F16) launch_rows_vec<half_t>(p, g, st);
+    else if (in->dtype == SPH_BF16) launch_rows_vec<bf16_t>(p, g, st);
+    else launch_rows_vec<float>(p, g, st);
+  } else if (inner_contig && p.inner_numel >= 8192 && p.outer_numel < 2048) {
     const unsigned g = static_cast<unsigned>(p.outer_numel < 65536 ? p.outer_numel : 65536);
     if (f64) reduce_block<double><<<g, kBlockRed, 0, st>>>(p);
     else if (ints) reduce_block<int64_t><<<g, kBlockRed, 0, st>>>(p);

@@ -74,6 +74,10 @@ _SIGS = {
                               c_i64, vp, c_i64, c_i64, c_i64, vp, c_i64, c_i64, c_i64, c_i64,
                               c_f32, vp, c_i64, c_i64, vp, c_i64, vp], c_int),
     "sph_attention_decode_workspace_bytes": ([c_i64, c_i64, c_i64], c_i64),
+    "sph_decode_attention_step": ([c_int, c_i64, c_i64, c_i64, c_i64, vp, c_i64, vp, vp, c_i64,
+                                   vp, vp, vp, c_i64, c_i64, c_i64, vp, c_i64, c_i64, c_i64,
+                                   c_i64, c_i64, c_f32, vp, c_i64, vp, c_i64, vp], c_int),
+    "sph_decode_attention_step_workspace_bytes": ([c_i64, c_i64, c_i64, c_i64], c_i64),
     "sph_attention_fwd_noalloc": ([c_int, c_i64, c_i64, c_i64, c_i64, vp, c_i64, c_i64, vp,
                                    c_i64, c_i64, vp, c_i64, c_i64, vp, c_i64, c_i64, c_i64, c_i64,
                                    c_f32, vp, c_i64, c_i64, vp], c_int),

@@ -333,3 +333,66 @@ def _(x, norm_w, eps, w, swiglu):
 @rms_norm_mm.register_fake
 def _(x, norm_w, eps, w, swiglu):
     return x.new_empty((x.shape[0], w.shape[0] // 2 if swiglu else w.shape[0]))
+
+
+# ---- decode-step attention with its KV-cache append ------------------------
+
+@torch.library.custom_op("spyre::decode_attention", mutates_args=("k_cache", "v_cache"))
+def decode_attention(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                     pos: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                     n_heads: int, n_kv_heads: int, scale: float,
+                     v_dim_major: bool) -> torch.Tensor:
+    """One decode step of grouped-query attention for qkv [B, (H + 2 Hkv) *
+    D] (the step's query heads, then its keys, then its values): RoPE
+    (rotate-half, tables cos / sin [max_len, D]) of the queries and keys at
+    position pos (a one-element int64 tensor), the keys and values written
+    into k_cache [B, Hkv, max_len, D] and v_cache ([B, Hkv, max_len, D], or
+    [B, Hkv, D, max_len] with v_dim_major) at pos, then softmax(scale q
+    K[0..pos]^T) V[0..pos] per query head (head j reads KV head j // (H /
+    Hkv)); returns [B, H * D].  On other devices it runs as the op-by-op
+    chain (pointwise RoPE, index_copy_, bmm -> masked softmax -> bmm) the
+    reference would run (codegen/inputs/spyre_torch_ops.cpp:297-377,
+    Metadata.yaml:275-277); on spyre as one kernel
+    (sph_decode_attention_step)."""
+    B = qkv.shape[0]
+    D = k_cache.shape[-1]
+    H, Hkv = n_heads, n_kv_heads
+    L = k_cache.shape[2]
+    q = qkv[:, :H * D].reshape(B, H, D)
+    k = qkv[:, H * D:(H + Hkv) * D].reshape(B, Hkv, D)
+    v = qkv[:, (H + Hkv) * D:].reshape(B, Hkv, D)
+    c, s = cos.index_select(0, pos), sin.index_select(0, pos)  # [1, D]
+
+    def rope(x):
+        half = D // 2
+        rot = torch.cat([-x[..., half:], x[..., :half]], dim=-1)
+        return x * c + rot * s
+
+    q, k = rope(q), rope(k)
+    k_cache.index_copy_(2, pos, k.unsqueeze(2))
+    if v_dim_major:
+        v_cache.index_copy_(3, pos, v.unsqueeze(3))
+        vv = v_cache.transpose(2, 3)
+    else:
+        v_cache.index_copy_(2, pos, v.unsqueeze(2))
+        vv = v_cache
+    keys = torch.arange(L, device=qkv.device)
+    mask = torch.where(keys <= pos, 0.0, float("-inf")).to(qkv.dtype)
+    qg = q.reshape(B * Hkv, H // Hkv, D)
+    sc = torch.bmm(qg, k_cache.reshape(B * Hkv, L, D).transpose(1, 2)) * scale + mask
+    p = torch.softmax(sc.float(), dim=-1).to(qkv.dtype)
+    o = torch.bmm(p, vv.reshape(B * Hkv, L, D).contiguous())
+    return o.reshape(B, H * D)
+
+
+@decode_attention.register_kernel("spyre")
+def _(qkv, cos, sin, pos, k_cache, v_cache, n_heads, n_kv_heads, scale, v_dim_major):
+    from torch_spyre import _C
+
+    return _C.decode_attention_step(qkv, cos, sin, pos, k_cache, v_cache, int(n_heads),
+                                    int(n_kv_heads), float(scale), bool(v_dim_major))
+
+
+@decode_attention.register_fake
+def _(qkv, cos, sin, pos, k_cache, v_cache, n_heads, n_kv_heads, scale, v_dim_major):
+    return qkv.new_empty((qkv.shape[0], n_heads * k_cache.shape[-1]))

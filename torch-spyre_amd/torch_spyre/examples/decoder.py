@@ -28,6 +28,8 @@ from typing import Optional
 import torch
 import torch.nn.functional as F
 
+import torch_spyre._inductor.customops  # noqa: F401  (torch.ops.spyre.decode_attention)
+
 
 @dataclasses.dataclass(frozen=True)
 class DecoderConfig:
@@ -243,11 +245,19 @@ def decode_step(tokens, pos: int, params: dict, cos, sin, cache, cfg: DecoderCon
     return lm_logits(h[:, 0], params, cfg)
 
 
-def decode_step_static(tokens, pos, params: dict, cos, sin, cache, cfg: DecoderConfig):
+def decode_step_static(tokens, pos, params: dict, cos, sin, cache, cfg: DecoderConfig,
+                       fused_attention: bool = True):
     """decode_step with every shape fixed, for torch.compile: `pos` is a
     one-element int64 tensor on the device, the new K/V are scattered into
-    the cache at `pos` and attention runs over the whole cache length with
-    keys after `pos` masked out, so one compiled graph serves every step."""
+    the cache at `pos` and attention runs over the cache with keys after
+    `pos` masked out, so one compiled graph serves every step.
+
+    With `fused_attention` (and a fused Q/K/V weight) RoPE, the cache
+    append and attention of a layer are one call of the spyre op
+    torch.ops.spyre.decode_attention (on spyre one kernel that reads only
+    the keys up to `pos`; elsewhere the same op-by-op chain as below);
+    otherwise they are written out as plain torch ops over the whole cache
+    length."""
     B = tokens.shape[0]
     L = cache[0][0].shape[2]  # K buffer [B, 8, max_len, D]
     h = F.embedding(tokens, params["embed"]).view(B, 1, cfg.hidden)
@@ -256,6 +266,16 @@ def decode_step_static(tokens, pos, params: dict, cos, sin, cache, cfg: DecoderC
     mask = torch.where(keys <= pos, 0.0, float("-inf")).to(h.dtype)
     for i, w in enumerate(params["layers"]):
         x = F.rms_norm(h, (cfg.hidden,), w["attn_norm"], cfg.eps)
+        if fused_attention and "wqkv" in w and cfg.head_dim == 128:
+            kc, vc = cache[i]
+            qkv = F.linear(x, w["wqkv"]).view(B, -1)
+            a = torch.ops.spyre.decode_attention(qkv, cos, sin, pos, kc, vc, cfg.n_heads,
+                                                 cfg.n_kv_heads, 1.0 / math.sqrt(cfg.head_dim),
+                                                 True)
+            h = h + F.linear(a, w["wo"]).view(B, 1, cfg.hidden)
+            x = F.rms_norm(h, (cfg.hidden,), w["mlp_norm"], cfg.eps)
+            h = h + _mlp(x, w, cfg)
+            continue
         q, k, v = _qkv(x, w, cfg)
         q = apply_rope(q.reshape(B, 1, cfg.n_heads, cfg.head_dim), c, s)
         k = apply_rope(k.reshape(B, 1, cfg.n_kv_heads, cfg.head_dim), c, s)
