@@ -7,6 +7,8 @@
 // 1 KiB per wave instruction), reduced with wave64 butterflies (+ one LDS
 // exchange when a row spans several waves) and written once.  A row of up to
 // 64K elements stays in registers; longer rows use a two-pass looped kernel.
+#include <type_traits>
+
 #include "sph_common.h"
 
 namespace sph {
@@ -516,7 +518,11 @@ gelu_rowsum_regs(const T* __restrict__ x, const T* __restrict__ sv,
 // one block reduction.  Rows past the end are clamped for loading and not
 // stored.  Plain (cached) loads: the non-temporal form measured 10-15 %
 // slower here.
-template <typename T, int NT, int VPT, int RPW>
+// SBV: s and b are both vectors; they then stay in the element type and,
+// for fp16, the compiler forms x * s + b as one mixed-precision FMA from
+// the three 16-bit values (no separate conversions).  Otherwise they are
+// widened to fp32 once (scalars are used as given, in fp32).
+template <typename T, int NT, int VPT, int RPW, bool SBV>
 __global__ void __launch_bounds__(NT)
 gelu_rowsum_rows(const T* __restrict__ x, const T* __restrict__ sv, const T* __restrict__ bv,
                  float s0, float b0, T* __restrict__ y, T* __restrict__ rowsum, int64_t rows) {
@@ -524,21 +530,27 @@ gelu_rowsum_rows(const T* __restrict__ x, const T* __restrict__ sv, const T* __r
   __shared__ float red[NWAVE][RPW];
   const int t = threadIdx.x;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * RPW;
-  float s[VPT][8], b[VPT][8];
+  using SB = typename std::conditional<SBV, T, float>::type;
+  SB s[VPT][8], b[VPT][8];
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int c0 = (i * NT + t) * 8;
-    if (sv) {
-      load8<T>(sv + c0, s[i]);
+    if constexpr (SBV) {
+      *reinterpret_cast<u32x4*>(s[i]) = *reinterpret_cast<const u32x4*>(sv + c0);
+      *reinterpret_cast<u32x4*>(b[i]) = *reinterpret_cast<const u32x4*>(bv + c0);
     } else {
+      if (sv) {
+        load8<T>(sv + c0, s[i]);
+      } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) s[i][j] = s0;
-    }
-    if (bv) {
-      load8<T>(bv + c0, b[i]);
-    } else {
+        for (int j = 0; j < 8; ++j) s[i][j] = s0;
+      }
+      if (bv) {
+        load8<T>(bv + c0, b[i]);
+      } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) b[i][j] = b0;
+        for (int j = 0; j < 8; ++j) b[i][j] = b0;
+      }
     }
   }
   u32x4 raw[RPW][VPT];
@@ -560,7 +572,10 @@ gelu_rowsum_rows(const T* __restrict__ x, const T* __restrict__ sv, const T* __r
       float g[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        g[j] = gelu_erf(fmaf(Num<T>::to_f(e[j]), s[i][j], b[i][j]));
+        if constexpr (SBV)
+          g[j] = gelu_erf(fmaf(Num<T>::to_f(e[j]), Num<T>::to_f(s[i][j]), Num<T>::to_f(b[i][j])));
+        else
+          g[j] = gelu_erf(fmaf(Num<T>::to_f(e[j]), s[i][j], b[i][j]));
         acc[r] += g[j];
       }
       if (y && row < rows) store8<T>(y + row * COLS + (i * NT + t) * 8, g);
@@ -727,15 +742,24 @@ int gelu_impl(const void* x, const void* s, const void* b, float s0, float b0,
     const unsigned grid = static_cast<unsigned>(ceil_div(rows, RPW));
     if (vec && rows <= 0x7fffffffLL * RPW) {
       if (cols == 2048) {
-        gelu_rowsum_rows<T, 256, 1, RPW><<<grid, 256, 0, st>>>(xi, si, bi, s0, b0, yo, ro, rows);
+        if (si && bi)
+          gelu_rowsum_rows<T, 256, 1, RPW, true><<<grid, 256, 0, st>>>(xi, si, bi, s0, b0, yo, ro, rows);
+        else
+          gelu_rowsum_rows<T, 256, 1, RPW, false><<<grid, 256, 0, st>>>(xi, si, bi, s0, b0, yo, ro, rows);
         return check_launch("sph_gelu_affine_rowsum");
       }
       if (cols == 4096) {
-        gelu_rowsum_rows<T, 512, 1, RPW><<<grid, 512, 0, st>>>(xi, si, bi, s0, b0, yo, ro, rows);
+        if (si && bi)
+          gelu_rowsum_rows<T, 512, 1, RPW, true><<<grid, 512, 0, st>>>(xi, si, bi, s0, b0, yo, ro, rows);
+        else
+          gelu_rowsum_rows<T, 512, 1, RPW, false><<<grid, 512, 0, st>>>(xi, si, bi, s0, b0, yo, ro, rows);
         return check_launch("sph_gelu_affine_rowsum");
       }
       if (cols == 8192) {
-        gelu_rowsum_rows<T, 512, 2, RPW><<<grid, 512, 0, st>>>(xi, si, bi, s0, b0, yo, ro, rows);
+        if (si && bi)
+          gelu_rowsum_rows<T, 512, 2, RPW, true><<<grid, 512, 0, st>>>(xi, si, bi, s0, b0, yo, ro, rows);
+        else
+          gelu_rowsum_rows<T, 512, 2, RPW, false><<<grid, 512, 0, st>>>(xi, si, bi, s0, b0, yo, ro, rows);
         return check_launch("sph_gelu_affine_rowsum");
       }
     }

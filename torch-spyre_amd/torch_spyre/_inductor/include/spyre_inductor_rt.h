@@ -129,22 +129,21 @@ __device__ inline float erf_fast(float x) {
 }
 
 // GELU, erf form: x Phi(x) = max(x, 0) - |x| h(|x|) with h(a) = erfc(a/sqrt 2)/2
-// the Gaussian tail.  log2 h on [0, 5.5] is the degree-7 least-squares
-// polynomial (fit in float64 on 200001 points in the Chebyshev basis,
-// converted to monomials); past 5.5, h < 1.9e-8 and is taken as 0.
-// Absolute error below 5.3e-7 for every finite x (float32, against float64
-// erfc); +-inf and NaN give NaN.
+// the Gaussian tail.  h = 2^p(a) on [0, 9), p the degree-6 polynomial fit
+// to log2 h there (iteratively reweighted least squares in float64 toward
+// equal ripple of the absolute error of a h, converted to monomials); from
+// 9 on h < 1.2e-19 and is taken as 0.  Absolute error below 1e-6 for every
+// finite x (float32, against float64 erfc); +-inf and NaN give NaN.
 __device__ inline float gelu_erf(float x) {
   const float ax = fabsf(x);
-  const float a = fminf(ax, 5.5f);
-  float p = fmaf(-1.9959244095426196e-06f, a, 6.483463872904686e-05f);
-  p = fmaf(p, a, -0.0009561956288912488f);
-  p = fmaf(p, a, 0.00860984128475729f);
-  p = fmaf(p, a, -0.054171898352491525f);
-  p = fmaf(p, a, -0.45824610324983095f);
-  p = fmaf(p, a, -1.1513446909430594f);
-  p = fmaf(p, a, -0.9999850572286579f);
-  const float h = ax < 5.5f ? __builtin_amdgcn_exp2f(p) : 0.f;
+  const float a = fminf(ax, 9.0f);
+  float p = fmaf(3.30928342e-05f, a, -0.000769219827f);
+  p = fmaf(p, a, 0.00808071718f);
+  p = fmaf(p, a, -0.0534121059f);
+  p = fmaf(p, a, -0.458770961f);
+  p = fmaf(p, a, -1.15120173f);
+  p = fmaf(p, a, -0.999993086f);
+  const float h = ax < 9.0f ? __builtin_amdgcn_exp2f(p) : 0.f;
   return fmaf(-ax, h, fmaxf(x, 0.f));
 }
 
