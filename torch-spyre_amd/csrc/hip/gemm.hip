@@ -1925,9 +1925,7 @@ extern "C" int sph_gemm_swiglu(sph_dtype dtype, int64_t m, int64_t n, int64_t k,
     q.d = d;
     q.ldd = ldd;
     q.alpha = 1.f;
-    constexpr int64_t kCUs = 256;
-    const int64_t wgs = ceil_div(n, gv::WAVES);
-    const unsigned grid = static_cast<unsigned>(wgs < kCUs ? wgs : kCUs);
+    const unsigned grid = stream_grid(n);
     hipStream_t st = as_stream(stream);
 #define SPH_SW_STREAM(T_)                                                                       \
   do {                                                                                          \
@@ -2007,8 +2005,7 @@ extern "C" int sph_gemm_rmsnorm(sph_dtype dtype, int64_t m, int64_t n, int64_t k
   q.norm_w = norm_w;
   q.norm_eps = eps;
   hipStream_t st = as_stream(stream);
-  constexpr int64_t kCUs = 256;
-  const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(n, gv::WAVES), kCUs));
+  const unsigned grid = stream_grid(n);
 #define SPH_RN_STREAM(T_, SW_)                                                              \
   do {                                                                                      \
     if (m <= 4)                                                                             \
