@@ -135,6 +135,9 @@ template <int N>
 __device__ inline void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// s_waitcnt immediate for vmcnt(0) alone (gfx9 fields: vmcnt [3:0] and
+// [15:14], expcnt [6:4], lgkmcnt [11:8]; the others at their maximum).
+constexpr int kWaitVmcnt0 = 0x0F70;
 
 // Mask block classes (values of the pre-pass's bytes).
 constexpr uint8_t MB_ZERO = 0, MB_MIXED = 1, MB_NEGINF = 2;
@@ -384,16 +387,12 @@ attn_fwd_kernel(const AttnArgs p) {
     const bool v0 = nit > 0 && valid(blk_of(0)), v1 = nit > 1 && valid(blk_of(1));
     if (v0) issue(blk_of(0), 0);
     if (v1) issue(blk_of(1), 1);
-    // block 0 landed: wave wq issued KLW (wq == 0) or KLW - 1 K lines and
-    // VLW V lines per block
-    if (v0 && v1) {
-      if (wq == 0)
-        wait_vmcnt<KLW + VLW>();
-      else
-        wait_vmcnt<KLW - 1 + VLW>();
-    } else {
-      wait_vmcnt<0>();
-    }
+    // Q fragments and both blocks landed.  The wait is the builtin (which
+    // the compiler's wait-count pass sees), not inline asm: the pass does
+    // not count the DMA and would otherwise place waits for the Q loads at
+    // their uses inside the loop, where the hardware counter also holds the
+    // DMA of a later block - every block would then wait for that DMA.
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   }
   __syncthreads();
   for (int it = 0; it < nit; ++it) {
