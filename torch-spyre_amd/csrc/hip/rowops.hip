@@ -62,14 +62,14 @@ __device__ inline void load_row(const T* __restrict__ row, int64_t cols,
   for (int i = 0; i < VPT; ++i) load_chunk<T, VEC>(row, cols, chunk_col<TPR>(i, t), fill, v[i]);
 }
 
-template <typename T, int TPR, int VPT, bool VEC>
+template <typename T, int TPR, int VPT, bool VEC, bool NT = false>
 __device__ inline void store_row(T* __restrict__ row, int64_t cols, int t,
                                  const float (&v)[VPT][8]) {
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int64_t c0 = chunk_col<TPR>(i, t);
     if (VEC && c0 + 8 <= cols) {
-      store8<T>(row + c0, v[i]);
+      store8<T, NT>(row + c0, v[i]);
     } else {
       const int64_t n = cols - c0;
       if (n > 0) store8_partial<T>(row + c0, n > 8 ? 8 : static_cast<int>(n), v[i]);
@@ -371,7 +371,7 @@ norm_regs(const T* __restrict__ x, const T* __restrict__ res,
       for (int j = 0; j < 8; ++j)  // round the sum to T, as an eager add would
         v[i][j] = Num<T>::to_f(Num<T>::from_f(v[i][j] + r[j]));
     }
-    if (valid && h != nullptr) store_row<T, TPR, VPT, VEC>(h + rr * cols, cols, t, v);
+    if (valid && h != nullptr) store_row<T, TPR, VPT, VEC, true>(h + rr * cols, cols, t, v);
   }
   const float inv_n = 1.0f / static_cast<float>(cols);
   float mean = 0.f;
@@ -418,7 +418,7 @@ norm_regs(const T* __restrict__ x, const T* __restrict__ res,
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[i][j] = fmaf((v[i][j] - mean) * rstd, wv[j], bv[j]);
   }
-  store_row<T, TPR, VPT, VEC>(y + row * cols, cols, t, v);
+  store_row<T, TPR, VPT, VEC, true>(y + row * cols, cols, t, v);
 }
 
 template <typename T, typename W, bool LAYER>
@@ -506,7 +506,7 @@ gelu_rowsum_regs(const T* __restrict__ x, const T* __restrict__ sv,
   }
   if (rowsum) acc = group_reduce<SumOp, TPR>(acc, lds);
   if (!valid) return;
-  if (y) store_row<T, TPR, VPT, VEC>(y + row * cols, cols, t, v);
+  if (y) store_row<T, TPR, VPT, VEC, true>(y + row * cols, cols, t, v);
   if (rowsum && t == 0) rowsum[row] = Num<T>::from_f(acc);
 }
 
@@ -578,7 +578,7 @@ gelu_rowsum_rows(const T* __restrict__ x, const T* __restrict__ sv, const T* __r
           g[j] = gelu_erf(fmaf(Num<T>::to_f(e[j]), s[i][j], b[i][j]));
         acc[r] += g[j];
       }
-      if (y && row < rows) store8<T>(y + row * COLS + (i * NT + t) * 8, g);
+      if (y && row < rows) store8<T, true>(y + row * COLS + (i * NT + t) * 8, g);
     }
   }
   if (!rowsum) return;
