@@ -76,6 +76,8 @@ MAX_CACHED_TRIPS = 8
 # workgroups: EPT independent loads in flight per thread instead of one.
 PW_BLOCK = 256
 VEC = 8
+# Row elements per thread the row-reduction block is sized for.
+ROW_EPT = 16
 
 
 def _next_pow2(n: int) -> int:
@@ -493,10 +495,13 @@ class SpyreKernel(SIMDKernel):
         return n
 
     def _block(self) -> int:
-        # Row reductions: about 8 elements per thread (fewer, larger
-        # workgroups amortise the block reductions' barriers), 64 .. 512.
+        # Row reductions: about 16 elements per thread (two VEC trips;
+        # fewer, larger workgroups amortise the block reductions' barriers),
+        # 64 .. 512.  Against 8 per thread, measured on the compiled c1 / c3
+        # kernels (rows of 4096): GELU chain + row-sum 24.1 -> 22.1 us,
+        # softmax 4.9 -> 4.5 us, add + RMSNorm / LayerNorm 0.5 % faster.
         if self.inside_reduction or self.features.is_reduction():
-            return min(MAX_BLOCK, max(64, _next_pow2(self._rnumel()) // 8))
+            return min(MAX_BLOCK, max(64, _next_pow2(self._rnumel()) // ROW_EPT))
         return PW_BLOCK
 
     def _rvec(self) -> int:
