@@ -77,6 +77,15 @@ __device__ inline T cvt(V v) {
   return Cvt<T>::from(v);
 }
 
+// Streaming (non-temporal) store, for outputs too large to stay in the
+// caches for their consumer.
+template <typename T>
+__device__ inline void store_nt(T* p, T v) { __builtin_nontemporal_store(v, p); }
+template <>
+__device__ inline void store_nt<bfloat16>(bfloat16* p, bfloat16 v) {
+  __builtin_nontemporal_store(v.bits, &p->bits);
+}
+
 // Rounds an fp32 value to the precision of a narrower dtype (to_dtype).
 __device__ inline float round_half(float v) { return static_cast<float>(static_cast<_Float16>(v)); }
 __device__ inline float round_bf16(float v) { return to_f(Cvt<bfloat16>::from(v)); }

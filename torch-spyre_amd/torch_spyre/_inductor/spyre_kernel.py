@@ -78,6 +78,12 @@ PW_BLOCK = 256
 VEC = 8
 # Row elements per thread the row-reduction block is sized for.
 ROW_EPT = 16
+# Outputs of at least this many bytes are written with streaming stores: they
+# do not fit in the caches for their consumer anyway, and the streaming form
+# measured 3-5 % faster on the [8192, 4096] row kernels.  Smaller outputs
+# (a decoder layer's activations) keep plain stores, so the next kernel can
+# find them in the caches.
+NT_STORE_BYTES = 64 << 20
 
 
 def _next_pow2(n: int) -> int:
@@ -635,7 +641,11 @@ class SpyreKernel(SIMDKernel):
         dtype = V.graph.get_dtype(name)
         self._record_extent(str(var), index, False)
         ctype = self.dtype_to_str(dtype)
-        line = f"{var}[{self.index_to_str(index)}] = spy::cvt<{ctype}>({value});"
+        if self._streaming_output(name, dtype):
+            line = (f"spy::store_nt(&{var}[{self.index_to_str(index)}], "
+                    f"spy::cvt<{ctype}>({value}));")
+        else:
+            line = f"{var}[{self.index_to_str(index)}] = spy::cvt<{ctype}>({value});"
         if self.inside_reduction:
             self.compute.writeline(DeferredLine(name, line))
             if self._cacheable_row_load(index):
@@ -654,6 +664,14 @@ class SpyreKernel(SIMDKernel):
                                        f"{f'spy::to_f({stored})' if fl else stored};")
         else:
             self.stores.writeline(DeferredLine(name, line))
+
+    @staticmethod
+    def _streaming_output(name: str, dtype: torch.dtype) -> bool:
+        try:
+            numel = int(V.graph.get_numel(name))
+        except (TypeError, ValueError):
+            return False
+        return numel * dtype.itemsize >= NT_STORE_BYTES
 
     def store_reduction(self, name: str, index: sympy.Expr, value: CSEVariable) -> None:
         var = self.args.output(name)
