@@ -695,7 +695,13 @@ class SpyreKernel(SIMDKernel):
         e = str(expr)
         n = self.index_to_str(size)
         self._needs_error_word = True
-        self.compute.writeline(f"if ({e} < 0 || {e} >= {n}) {{ *spy_err = 1; {e} = 0; }}")
+        # Branch-free: the flag collects in a register and the error word is
+        # written once at the end of the kernel.  (A store to the volatile
+        # error word inside the row loop split every element into its own
+        # block, so the row's loads and stores did not merge into 16-byte
+        # accesses and the index was reloaded per element.)
+        self.compute.writeline(f"{{ const bool spy_c = {e} < 0 || {e} >= {n}; "
+                               f"spy_bad |= spy_c; {e} = spy_c ? 0 : {e}; }}")
 
     # -- reductions ---------------------------------------------------------------
     def _acc(self, decl: str) -> str:
@@ -832,7 +838,10 @@ class SpyreKernel(SIMDKernel):
         with code.indent():
             code.writeline(",\n".join(params) if params else "")
         code.writeline(") {")
+        needs_err = getattr(self, "_needs_error_word", False)
         with code.indent():
+            if needs_err:
+                code.writeline("bool spy_bad = false;")
             if is_red:
                 code.writeline(f"__shared__ float spy_lds[3 * {max(1, block // 64)}];")
                 code.writeline(f"__shared__ int64_t spy_lds_i[{max(1, block // 64)}];")
@@ -877,6 +886,8 @@ class SpyreKernel(SIMDKernel):
                         code.writeline("}")
                     code.writeline("}")
                 code.writeline("}")
+            if needs_err:
+                code.writeline("if (spy_bad) *spy_err = 1;")
         code.writeline("}")
         src = code.getvalue()
         if grid <= 0 or grid >= 2**31:
