@@ -62,3 +62,43 @@ def test_innermost_kept_stays_with_inductor():
 def test_spyre_wrapper_calls_transpose_copy(fake_device):
     code = _compile(lambda x: x.t().contiguous(), [((1088, 320), torch.float16)])
     assert "torch.ops.spyre.transpose_copy.default(" in code
+
+
+def test_permute_chain_composes():
+    # two permutes whose composition moves the innermost dimension
+    x = torch.randn(2, 6, 4, 8)
+    fn = lambda x: x.permute(0, 2, 1, 3).permute(0, 1, 3, 2).contiguous()  # noqa: E731
+    out, n = _run(fn, x)
+    assert n == 1
+    assert torch.equal(out, fn(x))
+
+
+def test_copy_of_transposed_tensor_into_a_slice():
+    # the decoder's prefill writes V transposed into a slice of a dim-major
+    # cache: cache[:, :, :, :S].copy_(v.transpose(1, 2).transpose(2, 3))
+    g = torch.Generator().manual_seed(7)
+    B, S, H, D, L = 2, 40, 3, 16, 48
+    v = torch.randn(B, S, H, D, generator=g).half()
+
+    def fn(v, cache):
+        cache[:, :, :, :S].copy_(v.transpose(1, 2).transpose(2, 3))
+        return cache.sum()
+
+    cache = torch.zeros(B, H, D, L).half()
+    want_cache = cache.clone()
+    want = fn(v, want_cache)
+    out, n = _run(fn, v, cache)
+    assert n == 1
+    assert torch.equal(cache, want_cache) and torch.equal(out, want)
+
+
+def test_copy_keeping_innermost_is_left_alone():
+    v = torch.randn(2, 40, 3, 16)
+
+    def fn(v, cache):
+        cache[:, :, :40].copy_(v.transpose(1, 2))
+        return cache.sum()
+
+    cache = torch.zeros(2, 3, 48, 16)
+    out, n = _run(fn, v, cache)
+    assert n == 0

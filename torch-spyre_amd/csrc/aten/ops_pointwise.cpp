@@ -120,7 +120,12 @@ bool transpose_copy(const at::Tensor& dst, const at::Tensor& src) {
     bdst[nb] = dst.stride(d);
     ++nb;
   }
-  if (at::get_overlap_status(dst, src) != at::MemOverlapStatus::No) return false;
+  // (get_overlap_status answers TooHard for any source that is not dense,
+  // such as a column slice of a wider matrix: a source in other storage
+  // cannot overlap the destination)
+  if (src.storage().is_alias_of(dst.storage()) &&
+      at::get_overlap_status(dst, src) != at::MemOverlapStatus::No)
+    return false;
   c10::DeviceGuard guard(dst.device());
   SPYRE_SPH_CHECK(sph_transpose_copy(static_cast<int>(dst.element_size()), src.data_ptr(),
                                      dst.data_ptr(), dst.size(u), dst.size(v), src.stride(u),

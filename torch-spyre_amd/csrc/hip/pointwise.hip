@@ -562,6 +562,55 @@ __global__ void __launch_bounds__(256) transpose_tile_kernel(TransposeArgs a) {
   }
 }
 
+// 2-byte elements with whole 64 x 64 tiles and 16-byte aligned rows: each
+// thread loads two 16-byte chunks of src rows (8 consecutive v) and stores
+// two 16-byte chunks of dst rows (8 consecutive u).  The tile sits in LDS as
+// [u][v] with a 66-element row pitch: the store phase's column reads (8 rows
+// of one v per thread, 8 threads per v) then fall on distinct banks.
+__global__ void __launch_bounds__(256) transpose_tile16_kernel(TransposeArgs a) {
+  constexpr int P = kTT + 2;  // row pitch (elements)
+  __shared__ __attribute__((aligned(16))) uint16_t tile[kTT * P];
+  const int64_t tu = blockIdx.x % a.tiles_u, tv = blockIdx.x / a.tiles_u;
+  const int64_t u0 = tu * kTT, v0 = tv * kTT;
+  const int t = threadIdx.x;
+  for (int64_t b = blockIdx.y; b < a.nbatch; b += gridDim.y) {
+    int64_t rem = b, so = 0, doff = 0;
+    for (int d = a.nb - 1; d >= 0; --d) {
+      const int64_t i = rem % a.bsize[d];
+      rem /= a.bsize[d];
+      so += i * a.bsrc[d];
+      doff += i * a.bdst[d];
+    }
+    const uint16_t* src = static_cast<const uint16_t*>(a.src) + so;
+    uint16_t* dst = static_cast<uint16_t*>(a.dst) + doff;
+    u32x4 ld[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int c = t + 256 * k, u = c >> 3, j = c & 7;
+      ld[k] = *reinterpret_cast<const u32x4*>(src + (u0 + u) * a.su + v0 + 8 * j);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int c = t + 256 * k, u = c >> 3, j = c & 7;
+      uint32_t* row = reinterpret_cast<uint32_t*>(tile + u * P + 8 * j);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) row[e] = ld[k][e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int c = t + 256 * k, v = c >> 3, i = c & 7;
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        w[e] = static_cast<uint32_t>(tile[(8 * i + 2 * e) * P + v]) |
+               (static_cast<uint32_t>(tile[(8 * i + 2 * e + 1) * P + v]) << 16);
+      *reinterpret_cast<u32x4*>(dst + (v0 + v) * a.dv + u0 + 8 * i) = u32x4{w[0], w[1], w[2], w[3]};
+    }
+    __syncthreads();
+  }
+}
+
 }  // namespace
 }  // namespace sph
 
@@ -597,6 +646,14 @@ extern "C" int sph_transpose_copy(int elem_bytes, const void* src, void* dst, in
   dim3 grid(static_cast<unsigned>(a.tiles_u * a.tiles_v),
             static_cast<unsigned>(a.nbatch < 65535 ? a.nbatch : 65535));
   hipStream_t st = as_stream(stream);
+  // whole tiles, rows and batch offsets of both sides 16-byte aligned
+  bool wide = elem_bytes == 2 && U % kTT == 0 && V % kTT == 0 && su % 8 == 0 && dv % 8 == 0 &&
+              (reinterpret_cast<uintptr_t>(src) & 15) == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0;
+  for (int d = 0; d < nb && wide; ++d) wide = (a.bsize[d] == 1) || (a.bsrc[d] % 8 == 0 && a.bdst[d] % 8 == 0);
+  if (wide) {
+    transpose_tile16_kernel<<<grid, 256, 0, st>>>(a);
+    return check_launch("sph_transpose_copy");
+  }
   switch (elem_bytes) {
     case 1: transpose_tile_kernel<uint8_t><<<grid, 256, 0, st>>>(a); break;
     case 2: transpose_tile_kernel<uint16_t><<<grid, 256, 0, st>>>(a); break;
