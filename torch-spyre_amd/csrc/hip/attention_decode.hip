@@ -614,52 +614,54 @@ __global__ void __launch_bounds__(kStepThreads) attn_decode_step_kernel(const St
   }
 }
 
-// Merge of one unit (blockIdx.x): the partials of the chunks holding keys
-// 0..P, O = sum_c 2^(m_c - M) o_c / sum_c 2^(m_c - M) l_c, M = max m_c.
+// Merge of one query head of one unit (blockIdx.x = unit * g + head), one
+// thread per output column: the partials of the chunks holding keys 0..P,
+// O = sum_c 2^(m_c - M) o_c / sum_c 2^(m_c - M) l_c, M = max m_c.  Up to 32
+// chunks' partials are loaded in one round (a 1152-slot cache has 18), so
+// the kernel waits for memory once.
+constexpr int kMergeThreads = DD;
 template <typename T>
-__global__ void __launch_bounds__(kStepThreads) attn_decode_step_merge(const StepArgs p) {
-  const int t = threadIdx.x, unit = blockIdx.x;
-  const int b = unit / p.n_kv, h = unit % p.n_kv, G = p.g;
+__global__ void __launch_bounds__(kMergeThreads) attn_decode_step_merge(const StepArgs p) {
+  const int d = threadIdx.x, G = p.g;
+  const int unit = blockIdx.x / G, i = blockIdx.x % G;
+  const int b = unit / p.n_kv, h = unit % p.n_kv;
   // every chunk has a partial (those past P with m = -inf); P is read
   // alongside them, only to write nothing when the step kernel refused it
   const int nvis = p.nchunks;
   const int64_t P = *p.pos;
-  const float* up = p.part + static_cast<int64_t>(unit) * p.nchunks * G * kStepPart;
-  T* O = static_cast<T*>(p.out) + b * p.ld_out + static_cast<int64_t>(h * G) * DD;
-  constexpr int NB = 16;  // partials loaded together (all loads in flight)
-  for (int x = t; x < G * DD; x += kStepThreads) {
-    const int i = x / DD, d = x % DD;
-    float M = -INFINITY, l = 0.f, acc = 0.f;
-    for (int c0 = 0; c0 < nvis; c0 += NB) {
-      float mm[NB], ll[NB], oo[NB];
+  const float* up = p.part + (static_cast<int64_t>(unit) * p.nchunks * G + i) * kStepPart;
+  const int64_t cs = static_cast<int64_t>(G) * kStepPart;  // between chunks
+  T* O = static_cast<T*>(p.out) + b * p.ld_out + static_cast<int64_t>(h * G + i) * DD;
+  constexpr int NB = 32;  // partials loaded together (all loads in flight)
+  float M = -INFINITY, l = 0.f, acc = 0.f;
+  for (int c0 = 0; c0 < nvis; c0 += NB) {
+    float mm[NB], ll[NB], oo[NB];
 #pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        const int c = c0 + j < nvis ? c0 + j : nvis - 1;  // a valid partial
-        const float* pc = up + (c * G + i) * kStepPart;
-        const bool in = c0 + j < nvis;
-        mm[j] = in ? pc[0] : -INFINITY;
-        ll[j] = in ? pc[1] : 0.f;
-        oo[j] = in ? pc[2 + d] : 0.f;
-      }
-      float bm = M;
-#pragma unroll
-      for (int j = 0; j < NB; ++j) bm = fmaxf(bm, mm[j]);
-      // chunk 0 holds key 0, so bm is finite from the first batch on
-      const float sc = __builtin_amdgcn_exp2f(M - bm);
-      l *= sc;
-      acc *= sc;
-#pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        // a neutral partial (m = -inf) carries no output sums
-        const bool live = mm[j] != -INFINITY;
-        const float w = __builtin_amdgcn_exp2f(mm[j] - bm);
-        l = live ? fmaf(ll[j], w, l) : l;
-        acc = live ? fmaf(oo[j], w, acc) : acc;
-      }
-      M = bm;
+    for (int j = 0; j < NB; ++j) {
+      const bool in = c0 + j < nvis;
+      const float* pc = up + (in ? c0 + j : nvis - 1) * cs;  // a valid partial
+      mm[j] = in ? pc[0] : -INFINITY;
+      ll[j] = in ? pc[1] : 0.f;
+      oo[j] = in ? pc[2 + d] : 0.f;
     }
-    if (P >= 0 && P < p.max_len) O[static_cast<int64_t>(i) * DD + d] = Num<T>::from_f(acc / l);
+    float bm = M;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) bm = fmaxf(bm, mm[j]);
+    // chunk 0 holds key 0, so bm is finite from the first batch on
+    const float sc = __builtin_amdgcn_exp2f(M - bm);
+    l *= sc;
+    acc *= sc;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      // a neutral partial (m = -inf) carries no output sums
+      const bool live = mm[j] != -INFINITY;
+      const float w = __builtin_amdgcn_exp2f(mm[j] - bm);
+      l = live ? fmaf(ll[j], w, l) : l;
+      acc = live ? fmaf(oo[j], w, acc) : acc;
+    }
+    M = bm;
   }
+  if (P >= 0 && P < p.max_len) O[d] = Num<T>::from_f(acc / l);
 }
 
 }  // namespace
@@ -747,15 +749,15 @@ extern "C" int sph_decode_attention_step(
   p.part = static_cast<float*>(workspace);
   hipStream_t st = as_stream(stream);
   dim3 grid(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(batch * n_kv_heads));
-  const dim3 mgrid(static_cast<unsigned>(batch * n_kv_heads));
+  const dim3 mgrid(static_cast<unsigned>(batch * n_kv_heads * p.g));
   if (dtype == SPH_F16) {
     if (vt) attn_decode_step_kernel<half_t, true><<<grid, kStepThreads, 0, st>>>(p);
     else attn_decode_step_kernel<half_t, false><<<grid, kStepThreads, 0, st>>>(p);
-    attn_decode_step_merge<half_t><<<mgrid, kStepThreads, 0, st>>>(p);
+    attn_decode_step_merge<half_t><<<mgrid, kMergeThreads, 0, st>>>(p);
   } else {
     if (vt) attn_decode_step_kernel<bf16_t, true><<<grid, kStepThreads, 0, st>>>(p);
     else attn_decode_step_kernel<bf16_t, false><<<grid, kStepThreads, 0, st>>>(p);
-    attn_decode_step_merge<bf16_t><<<mgrid, kStepThreads, 0, st>>>(p);
+    attn_decode_step_merge<bf16_t><<<mgrid, kMergeThreads, 0, st>>>(p);
   }
   return check_launch("sph_decode_attention_step");
 }
