@@ -128,7 +128,51 @@ def test_pointwise_chain_fuses_into_one_kernel(fake_device):
     code = _compile(lambda x, y: torch.sigmoid(x * 2 + y).relu() - 1,
                     [((1000, 3), torch.float32), ((1000, 3), torch.float32)])
     assert len(_kernels(code)) == 1
-    assert "if (xindex >= 3000LL) return;" in code
+    # 3000 elements: whole groups of 8 consecutive elements per thread
+    assert "if (spy_xb >= 3000LL) return;" in code
+
+
+def test_pointwise_group_form(fake_device):
+    # contiguous loads and stores of 8 consecutive elements become one wide
+    # access each (runtime alignment test, element fallback)
+    code = _compile(lambda x, y: torch.sigmoid(x * 2 + y), [((64, 256), torch.float16)] * 2)
+    assert "spy::load8f(in_ptr0" in code and "spy::load8f(in_ptr1" in code
+    assert "spy::store8v<_Float16, false>(out_ptr0" in code and "spy_al" in code
+    # a permute that keeps the innermost dimension: the permuted store is
+    # contiguous too
+    code = _compile(lambda x: x.permute(1, 0, 2).contiguous() + 1, [((16, 32, 128), torch.float16)])
+    assert "spy::load8f(" in code and "spy::store8v<" in code
+    # a row broadcast ([N] over [M, N]) is contiguous along the row
+    code = _compile(lambda x, b: x * b, [((64, 256), torch.float16), ((256,), torch.float16)])
+    assert code.count("spy::load8f(") == 2
+    # a column broadcast ([M, 1]) is the same value for the whole group: one
+    # element load, no wide one
+    code = _compile(lambda x, b: x * b, [((64, 256), torch.float16), ((64, 1), torch.float16)])
+    assert code.count("spy::load8f(") == 1 and "spy::store8v<" in code
+
+
+def test_pointwise_group_form_not_used(fake_device):
+    # element count not a multiple of 8
+    code = _compile(lambda x: x * 2 + 1, [((7, 5), torch.float16)])
+    assert "spy::load8f" not in code and "spy_xb" not in code
+    # a row broadcast over an innermost dimension of 6: a group of 8 would
+    # wrap the row
+    code = _compile(lambda x, b: x * b, [((8, 6), torch.float16), ((6,), torch.float16)])
+    assert "spy::load8f" not in code and "spy_xb" not in code
+    # a gathered row (embedding) keeps the element form, and so the whole
+    # kernel keeps the block-strided layout
+    code = _compile(lambda t, e: F.embedding(t, e) * 2,
+                    [((4, 16), torch.int64), ((100, 64), torch.float16)])
+    assert "spy::load8f" not in code and "spy_xb" not in code
+
+
+def test_pointwise_group_form_in_place(fake_device):
+    # an in-place update reads and writes the same buffer as whole groups
+    def fn(x, y):
+        x.mul_(2).add_(y)
+        return x
+    code = _compile(fn, [((32, 64), torch.float16), ((32, 64), torch.float16)])
+    assert "spy::store8v<" in code
 
 
 def test_transposing_copy_uses_flat_index(fake_device):

@@ -143,6 +143,50 @@ def test_pointwise_chain_and_broadcast_compiled():
                                rtol=1e-5, atol=1e-5)
 
 
+def _rotate_half(x):
+    h = x.shape[-1] // 2
+    return torch.cat([-x[..., h:], x[..., :h]], dim=-1)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_pointwise_group_form_compiled(dtype):
+    # 8 consecutive elements per thread with 16-byte accesses: rotate-half
+    # (masked loads whose shifted index leaves the buffer at its first and
+    # last rows), a permuted store, row broadcasts; results bit-exact
+    # against torch on the CPU (pure data movement, negation and one
+    # rounding per output)
+    _log(f"compiled group-form pointwise {dtype}")
+    x = randn((3, 16, 4, 64), k=30, dtype=dtype)
+    c = randn((16, 64), k=31, dtype=dtype)
+    f = torch.compile(lambda a, cs: (a * cs[:, None, :] + _rotate_half(a) * cs[:, None, :]).transpose(1, 2)
+                      .contiguous())
+    got = f(x.to(DEV), c.to(DEV)).cpu()
+    ref = ((x.float() * c.float()[:, None, :] + _rotate_half(x.float()) * c.float()[:, None, :])
+           .to(dtype).transpose(1, 2).contiguous())
+    # each output is one fp32 multiply-add of the same two products, rounded once
+    torch.testing.assert_close(got.float(), ref.float(), rtol=1e-2, atol=1e-2)
+    g = torch.compile(lambda a: _rotate_half(a))
+    torch.testing.assert_close(g(x.to(DEV)).cpu(), _rotate_half(x), rtol=0, atol=0)
+    # a buffer whose last group ends exactly at the end of the allocation,
+    # and a row of 40 elements (groups never straddle rows: 40 % 8 == 0)
+    y = randn((5, 40), k=32, dtype=dtype)
+    h = torch.compile(lambda a: torch.cat([a[:, 20:] * 2, -a[:, :20]], dim=-1))
+    torch.testing.assert_close(h(y.to(DEV)).cpu(), torch.cat([y[:, 20:] * 2, -y[:, :20]], dim=-1),
+                               rtol=0, atol=0)
+
+
+def test_pointwise_group_form_unaligned_views():
+    # buffers that are not 16-byte aligned (views at an odd element offset)
+    # take the element path of the group form
+    _log("compiled group-form pointwise, unaligned views")
+    base = randn((1, 8 * 64 + 3), k=33, dtype=torch.float16)
+    dev = base.to(DEV)
+    f = torch.compile(lambda a, b: a * 2 + b)
+    a, b = dev[0, 1:1 + 8 * 64], dev[0, 3:3 + 8 * 64]
+    torch.testing.assert_close(f(a, b).cpu(), base[0, 1:1 + 512] * 2 + base[0, 3:3 + 512],
+                               rtol=0, atol=0)
+
+
 @pytest.mark.parametrize("sk", [77, 130])
 def test_fused_masked_attention_any_key_count(sk):
     # a mask whose rows are not a multiple of 8 keys long goes through the

@@ -86,6 +86,69 @@ __device__ inline void store_nt<bfloat16>(bfloat16* p, bfloat16 v) {
   __builtin_nontemporal_store(v.bits, &p->bits);
 }
 
+// ---- 8-element groups of the pointwise template ------------------------------
+// A pointwise kernel whose direct accesses walk their buffers contiguously
+// gives each thread 8 consecutive elements.  Such a load is one 16-byte load
+// of the group (two for 4-byte elements) and such a store collects the 8
+// values and writes them once; `al` (every such buffer 16-byte aligned, one
+// uniform test per kernel) selects the wide form, element accesses otherwise.
+typedef uint32_t spy_u32x4 __attribute__((ext_vector_type(4)));
+template <typename T>
+__device__ inline void load8f(const T* __restrict__ p, bool al, float (&v)[8]) {
+  if (al && (sizeof(T) == 2 || sizeof(T) == 4)) {
+    constexpr int W = 16 / sizeof(T);  // elements per 16-byte load
+#pragma unroll
+    for (int h = 0; h < 8 / W; ++h) {
+      const spy_u32x4 w = *reinterpret_cast<const spy_u32x4*>(p + h * W);
+      const T* e = reinterpret_cast<const T*>(&w);
+#pragma unroll
+      for (int i = 0; i < W; ++i) v[h * W + i] = to_f(e[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = to_f(p[i]);
+  }
+}
+// The group at p[i0 .. i0 + 7] of a buffer of n elements, for a masked load:
+// whole where it lies inside the buffer, else element by element with the
+// elements outside it read as 0 (the mask never selects them).
+template <typename T>
+__device__ inline void load8f_in(const T* __restrict__ p, int64_t i0, int64_t n, bool al,
+                                 float (&v)[8]) {
+  if (i0 >= 0 && i0 + 8 <= n) {
+    load8f(p + i0, al, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t j = i0 + i;
+      v[i] = (j >= 0 && j < n) ? to_f(p[j]) : 0.f;
+    }
+  }
+}
+template <typename T, bool NT>
+__device__ inline void store8v(T* __restrict__ p, bool al, const T (&v)[8]) {
+  if (al && (sizeof(T) == 2 || sizeof(T) == 4)) {
+    constexpr int W = 16 / sizeof(T);
+#pragma unroll
+    for (int h = 0; h < 8 / W; ++h) {
+      spy_u32x4 w;
+      T* e = reinterpret_cast<T*>(&w);
+#pragma unroll
+      for (int i = 0; i < W; ++i) e[i] = v[h * W + i];
+      if constexpr (NT)
+        __builtin_nontemporal_store(w, reinterpret_cast<spy_u32x4*>(p + h * W));
+      else
+        *reinterpret_cast<spy_u32x4*>(p + h * W) = w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (NT) store_nt(p + i, v[i]);
+      else p[i] = v[i];
+    }
+  }
+}
+
 // Rounds an fp32 value to the precision of a narrower dtype (to_dtype).
 __device__ inline float round_half(float v) { return static_cast<float>(static_cast<_Float16>(v)); }
 __device__ inline float round_bf16(float v) { return to_f(Cvt<bfloat16>::from(v)); }
