@@ -448,8 +448,9 @@ def test_gemm_stream_decode_shapes(m, n, k, dtype):
     # the persistent weight-stream kernel (batch 1, M <= 8, K >= 1024):
     # K not a multiple of the 512-element lane sweep, N off the 16 waves of
     # a workgroup, several rows per wave; leftover rows split along K over
-    # 2 to 16 waves (N % 4096 of 2048, 1024, 16, 3, 2 rows), every row split
-    # (N below one round), no leftover (N = 4096); K at the LDS staging
+    # 2 to 16 waves (N % 4096 of 1024, 16, 3, 2 rows), every row split
+    # (N below one round), no leftover (N = 4096), whole rounds of 12 or 10
+    # waves per workgroup (N = 6144, 25600); K at the LDS staging
     # limits (16384 for M <= 4, 8192 for M <= 8) and past them (M = 8,
     # K = 8200: the small-M kernel)
     _log(f"gemm stream {m}x{n}x{k} {dtype}")
