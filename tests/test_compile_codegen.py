@@ -159,11 +159,24 @@ def test_pointwise_group_form_not_used(fake_device):
     # wrap the row
     code = _compile(lambda x, b: x * b, [((8, 6), torch.float16), ((6,), torch.float16)])
     assert "spy::load8f" not in code and "spy_xb" not in code
-    # a gathered row (embedding) keeps the element form, and so the whole
+    # a gather whose index changes along the innermost dimension (columns
+    # picked by an index tensor) keeps the element form, and so the whole
     # kernel keeps the block-strided layout
-    code = _compile(lambda t, e: F.embedding(t, e) * 2,
-                    [((4, 16), torch.int64), ((100, 64), torch.float16)])
+    code = _compile(lambda x, i: x[:, i] * 2,
+                    [((16, 64), torch.float16), ((64,), torch.int64)])
     assert "spy::load8f" not in code and "spy_xb" not in code
+
+
+def test_pointwise_group_form_gathered_rows(fake_device):
+    # an embedding row: the token index is the same for the 8 elements of a
+    # group (its load is indexed by the row only), so the gathered row is
+    # read as whole groups, by the group's first element, after the index
+    # (and its bounds check) is computed
+    code = _compile(lambda t, e, r: F.embedding(t, e) + r,
+                    [((4, 16), torch.int64), ((100, 64), torch.float16),
+                     ((4, 16, 64), torch.float16)])
+    assert "#define SPY_GLD0 if (spy_v == 0) spy::load8f(in_ptr1" in code
+    assert "spy_bad |=" in code and "spy::store8v<" in code
 
 
 def test_pointwise_group_form_in_place(fake_device):

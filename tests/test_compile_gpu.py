@@ -175,6 +175,18 @@ def test_pointwise_group_form_compiled(dtype):
                                rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_pointwise_group_form_gathered_rows(dtype):
+    # rows gathered by an index tensor (negative indices wrap, as in torch)
+    # read as whole 8-element groups; bit-exact against torch on the CPU
+    _log(f"compiled group-form gathered rows {dtype}")
+    t = randn((50, 40), k=34, dtype=dtype)
+    r = randn((7, 40), k=35, dtype=dtype)
+    i = torch.tensor([0, 49, -1, -50, 17, 3, 3])
+    f = torch.compile(lambda tt, ii, rr: tt[ii] + rr)
+    torch.testing.assert_close(f(t.to(DEV), i.to(DEV), r.to(DEV)).cpu(), t[i] + r, rtol=0, atol=0)
+
+
 def test_pointwise_group_form_unaligned_views():
     # buffers that are not 16-byte aligned (views at an odd element offset)
     # take the element path of the group form

@@ -95,6 +95,8 @@ NT_STORE_BYTES = 64 << 20
 
 _GROUP_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 _XINDEX = re.compile(r"\bxindex\b")
+_IDENT = re.compile(r"\b[A-Za-z_]\w*\b")
+_TMP = re.compile(r"tmp\d+")
 
 
 def _next_pow2(n: int) -> int:
@@ -500,6 +502,7 @@ class SpyreKernel(SIMDKernel):
         self._grp_load_info: list[tuple[str, sympy.Expr, torch.dtype, Optional[int]]] = []
         self._grp_stores: list[tuple[str, str, sympy.Expr, torch.dtype, bool]] = []
         self._grp_bad = False
+        self._grp_gathered: set[int] = set()  # group loads with a gathered index
         self._x_entries: list[tuple[str, str, int, int]] = []
 
     # -- sizes ----------------------------------------------------------------
@@ -615,6 +618,38 @@ class SpyreKernel(SIMDKernel):
             self._x_entries.append((entry.name, expr, div, length))
 
     # -- memory -------------------------------------------------------------------
+    def _group_uniform(self, name: str, depth: int = 0) -> bool:
+        """A value of the kernel body (a CSE variable) that is the same for
+        GROUP consecutive elements whose first flat index is a multiple of
+        GROUP: every name in its defining expression is such a value, an
+        index variable with a divisor that is a multiple of GROUP, or a
+        pointer, type or function name."""
+        if depth > 32:
+            return False
+        expr = None
+        for key, var in self.cse._cache.items():
+            if isinstance(key, str) and str(var) == name:
+                expr = key
+                break
+        if expr is None:
+            return False
+        entries = {str(s): e for s, e in self.range_tree_nodes.items()}
+        for ident in _IDENT.findall(expr):
+            if _TMP.fullmatch(ident):
+                if not self._group_uniform(ident, depth + 1):
+                    return False
+            elif ident in entries:
+                e = entries[ident]
+                try:
+                    div = int(e.divisor)
+                except (TypeError, ValueError):
+                    return False
+                if e.is_reduction or div == 1 or div % GROUP:
+                    return False
+            elif ident == "xindex" or ident.startswith(("r0_", "spy_", "SPY_")):
+                return False
+        return True
+
     def _group_class(self, index: sympy.Expr) -> str:
         """How a pointwise access moves over GROUP consecutive elements whose
         first flat index is a multiple of GROUP: "vec" (the index advances
@@ -626,6 +661,9 @@ class SpyreKernel(SIMDKernel):
         entries = {}
         for sym in index.free_symbols:
             e = self.range_tree_nodes.get(sym)
+            if e is None and self._group_uniform(str(sym)):
+                entries[sym] = (GROUP, 0)  # a gathered index, the same for the group
+                continue
             if e is None or e.is_reduction:
                 return "other"  # gathered (indirect) index
             try:
@@ -681,9 +719,9 @@ class SpyreKernel(SIMDKernel):
         self.dtype_to_str(dtype)
         masked = bool(self._load_mask)
         grouped = False
+        gathered = self.is_indirect_indexing(index)
         if not (self.features.is_reduction() or self.inside_reduction):
-            cls = ("other" if self.is_indirect_indexing(index)
-                   else self._group_class(index))
+            cls = self._group_class(index)
             span = None
             if cls == "vec" and dtype in _GROUP_DTYPES:
                 # A masked load reads its whole group where the group lies
@@ -691,7 +729,7 @@ class SpyreKernel(SIMDKernel):
                 # outside it read 0), and the mask selects per element.
                 if masked:
                     span = self._buffer_span(name)
-                grouped = not masked or span is not None
+                grouped = (not masked or span is not None) and not (masked and gathered)
             elif cls == "other":
                 self._grp_bad = True
         if grouped and masked:
@@ -708,6 +746,13 @@ class SpyreKernel(SIMDKernel):
                 k = len(self._grp_load_info)
                 self._grp_loads[key] = k
                 self._grp_load_info.append((str(var), index, dtype, span))
+                if gathered:
+                    # the gathered index is computed in the body: the group
+                    # is read there, by its first element
+                    self._grp_gathered.add(k)
+                    self.compute.writeline(f"SPY_GLD{k};")
+            if gathered:
+                return self.cse.generate(self.compute, f"SPY_LD{k}", dtype=torch.float32)
             if not masked:
                 return self.cse.generate(self.loads, f"SPY_LD{k}", dtype=torch.float32)
             other = self._load_other
@@ -971,6 +1016,10 @@ class SpyreKernel(SIMDKernel):
         for k, (var, index, dt, _) in enumerate(self._grp_load_info):
             code.writeline(f"#define SPY_LD{k} spy_ld{k}[spy_v]" if group else
                            f"#define SPY_LD{k} spy::to_f({var}[{self.index_to_str(index)}])")
+            if k in self._grp_gathered:
+                code.writeline(f"#define SPY_GLD{k} if (spy_v == 0) spy::load8f({var} + "
+                               f"({self._group_first(index)}), spy_al, spy_ld{k})" if group else
+                               f"#define SPY_GLD{k}")
         for k, (name, var, index, dt, nt) in enumerate(self._grp_stores):
             ct = self.dtype_to_str(dt)
             if group:
@@ -1061,6 +1110,13 @@ class SpyreKernel(SIMDKernel):
         spec.writeline(")")
         return spec.getvalue()
 
+    def _group_first(self, index: sympy.Expr) -> str:
+        """The index of a group's first element (index variables at their
+        group base; a gathered index, the same for the group, as it is)."""
+        return self.kexpr(index.subs({s: sympy.Symbol(f"spy_b_{s.name}", integer=True)
+                                      for s in index.free_symbols
+                                      if s in self.range_tree_nodes}))
+
     def _codegen_group(self, code: IndentedBuffer, block: int, xnumel: int, stores) -> None:
         """Pointwise body over GROUP consecutive elements per thread: the
         contiguous loads are read as whole groups before the element loop
@@ -1075,13 +1131,11 @@ class SpyreKernel(SIMDKernel):
             base = _XINDEX.sub("spy_xb", expr)
             code.writeline(f"const int64_t spy_b_{nm} = {base};")
 
-        def first(index: sympy.Expr) -> str:
-            # the index of the group's first element
-            return self.kexpr(index.subs({s: sympy.Symbol(f"spy_b_{s.name}", integer=True)
-                                          for s in index.free_symbols}))
-
+        first = self._group_first
         for k, (var, index, dt, span) in enumerate(self._grp_load_info):
             code.writeline(f"float spy_ld{k}[{GROUP}];")
+            if k in self._grp_gathered:
+                continue  # read in the body (SPY_GLD)
             if span is None:
                 code.writeline(f"spy::load8f({var} + ({first(index)}), spy_al, spy_ld{k});")
             else:
