@@ -11,6 +11,7 @@ calls to the MFMA GEMM, per-argument extents for the launch-time bounds
 check, and the fusions the reference forbids (choices.py:58-83).
 """
 
+import os
 import re
 
 import pytest
@@ -198,3 +199,23 @@ def test_unsupported_dynamic_shapes_raise(fake_device):
     from torch_spyre._inductor import Unsupported
 
     assert issubclass(Unsupported, RuntimeError)
+
+
+def test_compiled_graph_cache_key_covers_the_backend_sources(monkeypatch):
+    # Inductor reuses a cached compiled graph while the custom pass's uuid is
+    # unchanged: the uuid must hash every source of the backend, so changed
+    # kernel generation, scheduling or device runtime code is never served
+    # from a stale cache
+    from torch_spyre._inductor import passes
+
+    seen = {}
+
+    def fake_hash(files):
+        seen["files"] = [os.path.basename(f) for f in files]
+        return b"h"
+
+    monkeypatch.setattr(passes, "get_hash_for_files", fake_hash)
+    passes.CustomPostPasses().uuid()
+    for name in ("spyre_kernel.py", "spyre_inductor_rt.h", "scheduling.py", "lowering.py",
+                 "fuse_attention.py", "fuse_transpose.py", "__init__.py"):
+        assert name in seen["files"], name

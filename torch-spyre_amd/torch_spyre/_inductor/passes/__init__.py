@@ -17,6 +17,7 @@ them (fuse_decode_norm.py), and transposing copies as one tiled transpose
 
 from __future__ import annotations
 
+import os
 from typing import Any, Callable, List, Optional
 
 import torch
@@ -37,7 +38,16 @@ class CustomPostPasses(CustomGraphModulePass):
             p(gm)
 
     def uuid(self) -> Optional[Any]:
+        # Inductor keys its compiled-graph cache on this value: it covers
+        # every source of the backend (passes, scheduling, the kernel
+        # generator, lowerings, the device runtime header), so a cached
+        # graph is never reused after any of them changes.
+        inductor_dir = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
         files = {__file__}
+        for root, _, names in os.walk(inductor_dir):
+            for n in names:
+                if n.endswith((".py", ".h")):
+                    files.add(os.path.join(root, n))
         for p in custom_post_passes:
             f = getattr(p, "file", None)
             if callable(f):
