@@ -169,12 +169,18 @@ def _mlp(x, w: dict, cfg: DecoderConfig):
     return F.linear(F.silu(g) * u, w["wd"])
 
 
-def layer_forward(h, w: dict, cos, sin, mask, cfg: DecoderConfig, cache_kv=None):
+def layer_forward(h, w: dict, cos, sin, mask, cfg: DecoderConfig, cache_kv=None, x=None,
+                  next_norm=None):
     """One decoder layer on h [B, S, hidden] (prefill).  If `cache_kv` is
     given (the layer's (K, V) cache buffers [B, 8, max_len, D]), K/V of
-    positions [0, S) are written into it."""
+    positions [0, S) are written into it.  `x`, if given, is h normalised
+    with this layer's attention norm (computed by the layer before); with
+    `next_norm` the layer returns (output, output normalised with that
+    weight), so its last residual add and the next layer's first RMSNorm
+    are one kernel of this layer's compiled graph."""
     B, S, _ = h.shape
-    x = F.rms_norm(h, (cfg.hidden,), w["attn_norm"], cfg.eps)
+    if x is None:
+        x = F.rms_norm(h, (cfg.hidden,), w["attn_norm"], cfg.eps)
     q, k, v = _qkv(x, w, cfg)
     q = q.reshape(B, S, cfg.n_heads, cfg.head_dim)
     k = k.reshape(B, S, cfg.n_kv_heads, cfg.head_dim)
@@ -187,7 +193,10 @@ def layer_forward(h, w: dict, cos, sin, mask, cfg: DecoderConfig, cache_kv=None)
         cache_kv[1][:, :, :, :S].copy_(v.transpose(2, 3))
     h = h + F.linear(_attention(q, k, v, cfg, mask), w["wo"]).view(B, S, cfg.hidden)
     x = F.rms_norm(h, (cfg.hidden,), w["mlp_norm"], cfg.eps)
-    return h + _mlp(x, w, cfg)
+    h = h + _mlp(x, w, cfg)
+    if next_norm is None:
+        return h
+    return h, F.rms_norm(h, (cfg.hidden,), next_norm, cfg.eps)
 
 
 def block_forward(tokens, params: dict, cos, sin, mask, cfg: DecoderConfig):
@@ -218,9 +227,15 @@ def prefill(tokens, params: dict, cos, sin, mask, cache, cfg: DecoderConfig, lay
     cache, and returns the logits of the last position [B, vocab]."""
     layer_fn = layer_fn or layer_forward
     h = F.embedding(tokens, params["embed"])
-    for i, w in enumerate(params["layers"]):
-        h = layer_fn(h, w, cos, sin, mask, cfg, cache[i])
-    return lm_logits(h[:, -1], params, cfg)
+    layers = params["layers"]
+    # Each layer also normalises its output for the next one (the last for
+    # the LM head), so every call has the same arguments: one compiled
+    # graph serves all layers.
+    x = F.rms_norm(h, (cfg.hidden,), layers[0]["attn_norm"], cfg.eps)
+    for i, w in enumerate(layers):
+        nxt = layers[i + 1]["attn_norm"] if i + 1 < len(layers) else params["final_norm"]
+        h, x = layer_fn(h, w, cos, sin, mask, cfg, cache[i], x, nxt)
+    return F.linear(x[:, -1], params["lm_head"])
 
 
 def decode_step(tokens, pos: int, params: dict, cos, sin, cache, cfg: DecoderConfig):
