@@ -287,3 +287,29 @@ def test_oracle_decode_step_attention_pinned(v_dim_major):
     bad2, _, _ = OD.decode_step_attention(qkv.numpy(), cs.numpy(), sn.numpy(), pos - 1,
                                           kc.numpy(), vc.numpy(), H, Hkv, scale, act=None)
     assert not np.allclose(bad2, out.numpy(), rtol=1e-3, atol=1e-3)
+
+
+def test_prefill_chains_each_layer_norm_into_the_layer_before():
+    # prefill hands each layer its input already normalised and takes the
+    # next layer's normalised input (the LM head's, after the last layer)
+    # from the layer before: the same arithmetic as normalising at the
+    # start of each layer, so the logits are bit-identical on the CPU
+    cfg = dataclasses.replace(TINY, n_layers=3)
+    p = _params(cfg, torch.float32)
+    tok = torch.randint(0, cfg.vocab, (2, 10), generator=torch.Generator().manual_seed(5))
+    cos, sin = D.rope_tables(cfg, 10, "cpu", torch.float32)
+    mask = D.causal_mask(cfg, 10, "cpu", torch.float32)
+    cache = D.new_cache(cfg, 2, 10, "cpu", torch.float32)
+    got = D.prefill(tok, p, cos, sin, mask, cache, cfg)
+    h = F.embedding(tok, p["embed"])
+    for w in p["layers"]:
+        h = D.layer_forward(h, w, cos, sin, mask, cfg)  # normalises its own input
+    want = D.lm_logits(h[:, -1], p, cfg)
+    assert torch.equal(got, want)
+    # and the cache holds the same K / V as the layers computed them
+    cache2 = D.new_cache(cfg, 2, 10, "cpu", torch.float32)
+    h = F.embedding(tok, p["embed"])
+    for i, w in enumerate(p["layers"]):
+        h = D.layer_forward(h, w, cos, sin, mask, cfg, cache2[i])
+    for (k1, v1), (k2, v2) in zip(cache, cache2):
+        assert torch.equal(k1, k2) and torch.equal(v1, v2)
