@@ -180,6 +180,23 @@ def test_pointwise_group_form_gathered_rows(fake_device):
     assert "spy_bad |=" in code and "spy::store8v<" in code
 
 
+def test_scatter_keeps_element_stores(fake_device):
+    # a scatter's index is computed in the element loop: the store stays an
+    # element store inside that loop (a grouped store after the loop would
+    # name a variable out of scope, and hiprtc rejects the kernel)
+    cases = [
+        (lambda c, p, k: c.index_copy(1, p, k),
+         [((8, 64, 128), torch.float16), ((1,), torch.int64), ((8, 1, 128), torch.float16)]),
+        (lambda c, p, k: c.index_put((p,), k),
+         [((64, 128), torch.float16), ((4,), torch.int64), ((4, 128), torch.float16)]),
+    ]
+    for fn, specs in cases:
+        code = _compile(fn, specs)
+        assert _kernels(code)
+        assert not re.search(r"store8v<[^>]*>\(out_ptr\d+ \+ \([^)]*tmp\d+", code)
+        assert re.search(r"out_ptr\d+\[[^\]]*tmp\d+[^\]]*\] = spy::cvt", code)
+
+
 def test_pointwise_group_form_in_place(fake_device):
     # an in-place update reads and writes the same buffer as whole groups
     def fn(x, y):

@@ -811,7 +811,11 @@ class SpyreKernel(SIMDKernel):
         else:
             line = f"{var}[{self.index_to_str(index)}] = spy::cvt<{ctype}>({value});"
         if not (self.features.is_reduction() or self.inside_reduction):
-            if self._group_class(index) == "vec" and dtype in _GROUP_DTYPES:
+            # A scatter (an index computed in the body) keeps the element
+            # form: the grouped store is written after the element loop,
+            # where the body's index variables are out of scope.
+            if (self._group_class(index) == "vec" and dtype in _GROUP_DTYPES
+                    and not self.is_indirect_indexing(index)):
                 k = len(self._grp_stores)
                 self._grp_stores.append((name, str(var), index, dtype,
                                          self._streaming_output(name, dtype)))
