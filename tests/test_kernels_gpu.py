@@ -1217,6 +1217,48 @@ def test_decode_attention_step_vs_oracle(dtype, B, H, Hkv, L, v_dim_major):
     assert_close_fp(out, o_want, out_dtype=dtype, what="decode step after errors", **tol)
 
 
+@pytest.mark.parametrize("v_dim_major", [True, False])
+def test_decode_attention_step_ignores_slots_past_pos(v_dim_major):
+    """Cache slots after the step's position may hold anything (an
+    uninitialised or recycled cache): NaN, +Inf and -Inf there leave the
+    output equal to the oracle's over keys 0..pos, and finite."""
+    from oracle import decoder as OD
+
+    _log(f"decode step with NaN / Inf past pos, vdm={v_dim_major}")
+    B, H, Hkv, L, D = 2, 16, 4, 136, 128
+    dtype = torch.float16
+    ang = torch.arange(L, dtype=torch.float32)[:, None] * \
+        (1e4 ** (-torch.arange(0, D, 2, dtype=torch.float32) / D))[None, :]
+    ang = torch.cat([ang, ang], -1)
+    cs, sn = ang.cos().to(dtype), ang.sin().to(dtype)
+    csd, snd = cs.to(DEV), sn.to(DEV)
+    scale = 1.0 / math.sqrt(D)
+    nws = _capi.lib().sph_decode_attention_step_workspace_bytes(B, H, Hkv, L)
+    ws = torch.empty(nws, dtype=torch.uint8, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = torch.empty(B, H * D, dtype=dtype, device=DEV)
+    junk = torch.tensor([float("nan"), float("inf"), float("-inf")], dtype=dtype)
+    for n, pos in enumerate((0, 10, 63, 64, 100, L - 2)):
+        kc = randn((B, Hkv, L, D), k=120 + n).to(dtype)
+        vc = randn((B, Hkv, L, D), k=130 + n).to(dtype)
+        idx = torch.arange(B * Hkv * (L - pos - 1) * D) % 3
+        kc[:, :, pos + 1:] = junk[idx].view(B, Hkv, L - pos - 1, D)
+        vc[:, :, pos + 1:] = junk[(idx + 1) % 3].view(B, Hkv, L - pos - 1, D)
+        kcd = kc.to(DEV)
+        vcd = (vc.transpose(2, 3).contiguous() if v_dim_major else vc).to(DEV)
+        qkv = randn((B, (H + 2 * Hkv) * D), k=140 + n).to(dtype)
+        pos_d = torch.tensor([pos], dtype=torch.int64, device=DEV)
+        _step_call(qkv.to(DEV), csd, snd, pos_d, err, kcd, vcd, H, Hkv, L, scale, v_dim_major,
+                   out, ws)
+        o_want, _, _ = OD.decode_step_attention(
+            qkv.float().numpy(), cs.float().numpy(), sn.float().numpy(), pos,
+            kc.float().numpy(), vc.float().numpy(), H, Hkv, scale, act=np.float16)
+        assert bool(torch.isfinite(out).all()), f"pos={pos}"
+        assert_close_fp(out, o_want, out_dtype=dtype, what=f"junk past pos={pos}",
+                        rtol=1e-2, atol=1e-2)
+        assert int(err.cpu()[0]) == 0
+
+
 def test_attention_decode_causal_and_empty_rows():
     _log("decode attention causal / all-masked rows")
     b, mq, sk = 3, 6, 300

@@ -537,15 +537,28 @@ __global__ void __launch_bounds__(kStepThreads) attn_decode_step_kernel(const St
         qs[i][dq] = rq * p.scale_log2;
       }
     }
+    // Slots past P (the chunk holding P) may hold anything, NaN or Inf
+    // included: their scores are replaced by -inf below, and their values
+    // are staged as zeros so that a zero probability times a stale value
+    // adds nothing to the output sums.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int x = t + kStepThreads * i, key = x >> 4, cc = (x & 15) * 8;
       *reinterpret_cast<u32x4*>(&ks[key][cc]) = kr[i];
       if constexpr (VT) {
         const int dm = x >> 3, kc = (x & 7) * 8;
-        *reinterpret_cast<u32x4*>(&vs[dm][kc]) = vr[i];
+        u32x4 w = vr[i];
+        if (kc + 8 > nkeys) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t keep = (kc + 2 * q < nkeys ? 0x0000FFFFu : 0u) |
+                                  (kc + 2 * q + 1 < nkeys ? 0xFFFF0000u : 0u);
+            w[q] &= keep;
+          }
+        }
+        *reinterpret_cast<u32x4*>(&vs[dm][kc]) = w;
       } else {
-        *reinterpret_cast<u32x4*>(&vs[key][cc]) = vr[i];
+        *reinterpret_cast<u32x4*>(&vs[key][cc]) = key < nkeys ? vr[i] : zero_chunk();
       }
     }
     const int own = static_cast<int>(P - kbase);  // the new key's slot, if here
