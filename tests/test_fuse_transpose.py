@@ -59,6 +59,20 @@ def test_innermost_kept_stays_with_inductor():
     assert torch.equal(out, fn(x))
 
 
+def test_clone_preserving_strides_is_left_alone():
+    # clone() without a memory format keeps the permuted strides: it is not
+    # a transposing copy, and the result's strides stay eager's
+    x = torch.randn(88, 40).half()
+    fn = lambda x: x.t().clone() * 2  # noqa: E731
+    out, n = _run(fn, x)
+    assert n == 0
+    assert torch.equal(out, fn(x)) and out.stride() == fn(x).stride()
+    fn = lambda x: x.t().clone()  # noqa: E731
+    out, n = _run(fn, x)
+    assert n == 0
+    assert torch.equal(out, fn(x)) and out.stride() == fn(x).stride()
+
+
 def test_spyre_wrapper_calls_transpose_copy(fake_device):
     code = _compile(lambda x: x.t().contiguous(), [((1088, 320), torch.float16)])
     assert "torch.ops.spyre.transpose_copy.default(" in code

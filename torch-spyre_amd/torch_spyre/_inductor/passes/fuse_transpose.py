@@ -60,8 +60,14 @@ def fuse_transpose(gm: torch.fx.GraphModule) -> int:
     n = 0
     for node in list(g.nodes):
         if _is(node, aten.clone.default):
+            # A clone without a memory format preserves the permuted strides
+            # (preserve_format): only a clone whose result is contiguous is a
+            # transposing copy.
             mf = node.kwargs.get("memory_format", None)
-            if mf not in (None, torch.contiguous_format) or _val(node) is None:
+            out = _val(node)
+            if mf not in (None, torch.contiguous_format) or out is None:
+                continue
+            if mf is None and not out.is_contiguous():
                 continue
             chain = _permute_chain(node.args[0])
             if chain is None or not _moves_innermost(*chain):
