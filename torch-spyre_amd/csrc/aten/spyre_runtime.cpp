@@ -25,8 +25,11 @@ std::once_flag g_start_once;
 std::atomic<bool> g_started{false};
 int g_device_count = 0;
 
+// Per-device lazily created state is published with a release store after
+// its creation under the mutex and read with an acquire load, so a reader
+// that sees the pointer also sees what it points to.
 std::mutex g_stream_mu;
-std::array<hipStream_t, kMaxDevices> g_streams{};
+std::array<std::atomic<hipStream_t>, kMaxDevices> g_streams{};
 
 std::array<std::atomic<uint64_t>, kMaxDevices> g_seeds{};
 // Philox counter offset of each device's generator (blocks used so far).
@@ -35,8 +38,24 @@ std::array<std::atomic<uint64_t>, kMaxDevices> g_rng_offsets{};
 // Per device: the host address of its error word and the device-side
 // address kernels are given.
 std::mutex g_err_mu;
-std::array<volatile int32_t*, kMaxDevices> g_err_host{};
-std::array<int32_t*, kMaxDevices> g_err_dev{};
+std::array<std::atomic<int32_t*>, kMaxDevices> g_err_host{};
+std::array<std::atomic<int32_t*>, kMaxDevices> g_err_dev{};
+
+// Makes `device` current for a scope and restores the caller's device when
+// the scope ends, also when a HIP check throws inside it.
+class DeviceScope {
+ public:
+  explicit DeviceScope(int device) {
+    SPYRE_HIP_CHECK(hipGetDevice(&prev_));
+    if (prev_ != device) SPYRE_HIP_CHECK(hipSetDevice(device));
+  }
+  ~DeviceScope() { (void)hipSetDevice(prev_); }
+  DeviceScope(const DeviceScope&) = delete;
+  DeviceScope& operator=(const DeviceScope&) = delete;
+
+ private:
+  int prev_ = 0;
+};
 
 void do_start() {
   int n = 0;
@@ -77,29 +96,30 @@ void set_device(int device) {
 hipStream_t stream(int device) {
   if (device < 0) device = current_device();
   TORCH_CHECK(device < device_count(), "spyre: invalid device index ", device);
-  hipStream_t s = g_streams[device];
+  hipStream_t s = g_streams[device].load(std::memory_order_acquire);
   if (s) return s;
   std::lock_guard<std::mutex> lk(g_stream_mu);
-  if (!g_streams[device]) {
-    int cur = current_device();
-    if (cur != device) SPYRE_HIP_CHECK(hipSetDevice(device));
-    hipStream_t ns = nullptr;
-    SPYRE_HIP_CHECK(hipStreamCreateWithFlags(&ns, hipStreamNonBlocking));
-    g_streams[device] = ns;
-    if (cur != device) SPYRE_HIP_CHECK(hipSetDevice(cur));
+  s = g_streams[device].load(std::memory_order_relaxed);
+  if (!s) {
+    DeviceScope scope(device);
+    SPYRE_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    g_streams[device].store(s, std::memory_order_release);
   }
-  return g_streams[device];
+  return s;
 }
 
 void synchronize(int device) {
   if (device >= 0) {
-    if (g_streams[device]) SPYRE_HIP_CHECK(hipStreamSynchronize(g_streams[device]));
+    hipStream_t s = g_streams[device].load(std::memory_order_acquire);
+    if (s) SPYRE_HIP_CHECK(hipStreamSynchronize(s));
     release_copy_keepalive(device);
     check_device_errors(device);
     return;
   }
-  for (int d = 0; d < device_count(); ++d)
-    if (g_streams[d]) SPYRE_HIP_CHECK(hipStreamSynchronize(g_streams[d]));
+  for (int d = 0; d < device_count(); ++d) {
+    hipStream_t s = g_streams[d].load(std::memory_order_acquire);
+    if (s) SPYRE_HIP_CHECK(hipStreamSynchronize(s));
+  }
   release_copy_keepalive(-1);
   check_device_errors(-1);
 }
@@ -107,33 +127,36 @@ void synchronize(int device) {
 int32_t* device_error_word(int device) {
   if (device < 0) device = current_device();
   TORCH_CHECK(device < device_count(), "spyre: invalid device index ", device);
-  if (g_err_dev[device]) return g_err_dev[device];
+  int32_t* dev = g_err_dev[device].load(std::memory_order_acquire);
+  if (dev) return dev;
   std::lock_guard<std::mutex> lk(g_err_mu);
-  if (!g_err_dev[device]) {
-    const int cur = current_device();
-    if (cur != device) SPYRE_HIP_CHECK(hipSetDevice(device));
+  dev = g_err_dev[device].load(std::memory_order_relaxed);
+  if (!dev) {
+    DeviceScope scope(device);
     void* h = nullptr;
     // fine-grained (coherent) so a kernel's store is visible to the host
     // once the kernel has completed
     SPYRE_HIP_CHECK(hipHostMalloc(&h, 64, hipHostMallocMapped | hipHostMallocCoherent));
-    *static_cast<volatile int32_t*>(h) = 0;
+    __atomic_store_n(static_cast<int32_t*>(h), 0, __ATOMIC_RELAXED);
     void* d = nullptr;
     SPYRE_HIP_CHECK(hipHostGetDevicePointer(&d, h, 0));
-    g_err_host[device] = static_cast<volatile int32_t*>(h);
-    g_err_dev[device] = static_cast<int32_t*>(d);
-    if (cur != device) SPYRE_HIP_CHECK(hipSetDevice(cur));
+    dev = static_cast<int32_t*>(d);
+    g_err_host[device].store(static_cast<int32_t*>(h), std::memory_order_release);
+    g_err_dev[device].store(dev, std::memory_order_release);
   }
-  return g_err_dev[device];
+  return dev;
 }
 
 void check_device_errors(int device) {
   const int lo = device < 0 ? 0 : device;
   const int hi = device < 0 ? kMaxDevices : device + 1;
   for (int d = lo; d < hi; ++d) {
-    volatile int32_t* w = g_err_host[d];
-    if (w == nullptr || *w == 0) continue;
-    const int32_t code = *w;
-    *w = 0;
+    int32_t* w = g_err_host[d].load(std::memory_order_acquire);
+    if (w == nullptr || __atomic_load_n(w, __ATOMIC_ACQUIRE) == 0) continue;
+    // read and clear in one step: two host threads never both report (or
+    // both lose) the same error
+    const int32_t code = __atomic_exchange_n(w, 0, __ATOMIC_ACQ_REL);
+    if (code == 0) continue;
     if (code == 2)
       TORCH_CHECK_INDEX(false, "spyre: decode attention position outside the KV cache on "
                         "spyre:", d, " (code 2); the step wrote nothing");
@@ -513,10 +536,8 @@ void free_runtime() {
   empty_cache();
   std::lock_guard<std::mutex> lk(g_stream_mu);
   for (int d = 0; d < kMaxDevices; ++d) {
-    if (g_streams[d]) {
-      (void)hipStreamDestroy(g_streams[d]);
-      g_streams[d] = nullptr;
-    }
+    hipStream_t s = g_streams[d].exchange(nullptr, std::memory_order_acq_rel);
+    if (s) (void)hipStreamDestroy(s);
   }
 }
 
