@@ -912,6 +912,9 @@ def main(argv=None):
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
+    # A function that hits dynamo's recompile limit would run eagerly from
+    # then on: a figure labelled compiled must come from the compiled program.
+    torch._dynamo.config.fail_on_recompile_limit_hit = True
     from torch_spyre import _capi
 
     stream = torch.cuda.current_stream()

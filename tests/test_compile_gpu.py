@@ -55,9 +55,12 @@ def test_building_block_softmax_dims(dim):
     torch.testing.assert_close(y.cpu(), torch.softmax(x.float(), dim=dim).half(), **TOL)
 
 
-def test_c3_norms_and_gelu_chain_compiled_vs_oracle():
-    _log("compiled c3 at [512,4096]")
-    R, C = 512, 4096
+@pytest.mark.parametrize("R", [512, 8192])
+def test_c3_norms_and_gelu_chain_compiled_vs_oracle(R):
+    """The compiled c3 programs the benchmark times, at [512, 4096] and at
+    the config's [8192, 4096]."""
+    _log(f"compiled c3 at [{R},4096]")
+    C = 4096
     x, r = randn((R, C), k=0), randn((R, C), k=1)
     w = randn((C,), k=2, scale=0.02, mean=1.0)
     b = randn((C,), k=3, scale=0.02)
@@ -114,6 +117,17 @@ def test_c2_matmul_and_bmm_compiled():
         Q.to(DEV), K.to(DEV))
     ref = torch.softmax(torch.bmm(Q.float(), K.float()).half().float() * 0.088, -1).half()
     torch.testing.assert_close(S.cpu(), ref, **TOL)
+
+
+def test_c2_compiled_mm_4096_vs_oracle_sample():
+    """The compiled c2 product the benchmark reports, M = N = K = 4096, a
+    sample of rows against the oracle."""
+    _log("compiled mm 4096^3 (row sample vs oracle)")
+    A, B = uniform((4096, 4096), k=0), uniform((4096, 4096), k=1)
+    C = torch.compile(lambda a, b: a @ b)(A.to(DEV), B.to(DEV))
+    rows = torch.arange(0, 4096, 257)
+    assert_close_fp(C.index_select(0, rows.to(DEV)), O.gemm(A[rows].numpy(), B.numpy()),
+                    what="compiled c2 mm sampled rows")
 
 
 def test_building_block_softplus_and_attention():

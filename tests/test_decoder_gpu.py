@@ -7,9 +7,12 @@ float32 form (act=None).
 c4 runs at its full shape (hidden 4096, 32/8 heads, SwiGLU 12800, seq
 2048).  c5 runs at its full size (40 layers, vocab 49155, batch 4, a
 1024-token prompt, 128 greedy decode steps in a 1152-slot KV cache):
-KV-cache consistency (decode logits equal a fresh prefill's), layer 0 of
-the full prompt and its cache entries against the oracle, and every logit
-finite with every token in range.  The decode steps' numerics are checked
+the 40-layer prefill's last-position logits and 8 teacher-forced decode
+steps of one batch row against the oracle (computed layer by layer on the
+host, fp16 rounding points and float32), KV-cache consistency (decode
+logits equal a fresh prefill's), layer 0 of the full prompt and its cache
+entries against the oracle, and every logit finite with every token in
+range.  The decode steps' numerics are also checked
 teacher-forced (the CPU's tokens fed to both) on a 2-layer model of the
 same layer shape with the full 1024-token prompt over all 128 steps, and
 on a short prompt eagerly; greedy tokens must agree with the oracle's
@@ -30,6 +33,7 @@ move a logit two layers later by ~0.01):
 """
 
 import dataclasses
+import functools
 import time
 
 import numpy as np
@@ -51,6 +55,13 @@ SMALL = D.DecoderConfig(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, interm
 
 def _log(msg):
     print(f"[case] {msg}", flush=True)
+
+
+@pytest.fixture(autouse=True)
+def _compiled_means_compiled(monkeypatch):
+    # A function that hits dynamo's recompile limit runs eagerly from then
+    # on; a test of the compiled program must fail instead.
+    monkeypatch.setattr(torch._dynamo.config, "fail_on_recompile_limit_hit", True)
 
 
 def _np(params):
@@ -166,6 +177,32 @@ def test_c5_flow_teacher_forced_vs_oracle(compiled):
     _check_greedy(toks, want)
 
 
+def test_compiled_decode_step_unfused_attention_vs_oracle():
+    """decode_step_static with fused_attention=False under torch.compile:
+    the K / V cache append is a compiled scatter (index_copy_ at the
+    device-side position) and attention is bmm -> masked softmax -> bmm over
+    the whole cache; a 2-layer model with head dim 64, a 4 x 64 prompt and
+    6 teacher-forced steps against the oracle's compiled rounding points,
+    with its eager rounding points as the other noise-floor variant."""
+    _log("compiled decode step, fused_attention=False (head dim 64)")
+    cfg = SMALL
+    params = D.init_params(cfg, "cpu", seed=0xAFFE + 3)
+    prompt = _tokens(4, 64, cfg.vocab, seed=3)
+    teacher = _tokens(4, 6, cfg.vocab, seed=4)
+    torch._dynamo.reset()
+    layer_fn = torch.compile(D.layer_forward)
+    decode_fn = torch.compile(functools.partial(D.decode_step_static, fused_attention=False))
+    toks, logits = D.generate(prompt.to(DEV), _to(params, DEV), cfg, 6, DEV, layer_fn=layer_fn,
+                              teacher=teacher.to(DEV), decode_fn=decode_fn)
+    pn = _np(params)
+    want = OD.generate_teacher_forced(prompt.numpy(), teacher.numpy(), pn, cfg, fused=True)
+    exact = OD.generate_teacher_forced(prompt.numpy(), teacher.numpy(), pn, cfg, act=None)
+    other = OD.generate_teacher_forced(prompt.numpy(), teacher.numpy(), pn, cfg, fused=False)
+    _gate(logits.cpu().float().numpy(), want, exact, "compiled unfused decode step",
+          floor16=other)
+    _check_greedy(toks, want)
+
+
 def _check_greedy(toks, want):
     """Greedy tokens equal the oracle's argmax wherever that argmax is
     decided by more than the tolerance (want [T+1, B, vocab], the logits of
@@ -207,6 +244,127 @@ def test_c5_decode_teacher_forced_full_prompt():
     assert got.shape == (129, 4, cfg.vocab)
     _gate(got, want, exact, "c5 2-layer full prompt, 128 steps")
     _check_greedy(toks, want)
+
+
+def _rel_l2(a, b):
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+def _oracle_rows_layerwise(params, prompt, teacher, cfg, variants):
+    """OD.generate_teacher_forced for the batch rows `prompt` [R, S] /
+    `teacher` [R, T], computed layer by layer so that only one layer's
+    weights are on the host at a time: layer l runs over the prompt and then
+    over the T teacher-forced steps (whose inputs are layer l-1's outputs,
+    known under teacher forcing).  `variants` maps a name to OD's (act,
+    fused); returns name -> logits [T+1, R, vocab] (prefill's last position
+    first).  The variants of one layer run on two threads (numpy releases
+    the GIL in its array work)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    prompt, teacher = np.asarray(prompt), np.asarray(teacher)
+    S, T = prompt.shape[1], teacher.shape[1]
+    table = params["embed"]
+    dev = table.device
+
+    def rows_of(tok):
+        return table.index_select(0, torch.from_numpy(tok.reshape(-1)).to(dev)).cpu()
+
+    emb_p = OD.embed(np.arange(prompt.size), rows_of(prompt).float().numpy())
+    emb_t = OD.embed(np.arange(teacher.size), rows_of(teacher.T.copy()).float().numpy())
+    R = prompt.shape[0]
+    state = {n: (emb_p.reshape(R, S, -1), [emb_t[t * R:(t + 1) * R].reshape(R, 1, -1)
+                                           for t in range(T)]) for n in variants}
+
+    def run_layer(name, w):
+        act, fused = variants[name]
+        h, steps = state[name]
+        h, kv = OD.layer(h, w, cfg, np.arange(S), act, fused=fused)
+        out = []
+        for t in range(T):
+            ht, kv = OD.layer(steps[t], w, cfg, np.array([S + t]), act, kv_prefix=kv,
+                              fused=fused)
+            out.append(ht)
+        state[name] = (h, out)
+
+    t0 = time.time()
+    with ThreadPoolExecutor(len(variants)) as ex:
+        for li, lw in enumerate(params["layers"]):
+            w = {k: lw[k].cpu().float().numpy() for k in D.LAYER_WEIGHTS}
+            list(ex.map(lambda n: run_layer(n, w), list(variants)))
+            if li % 8 == 7 or li + 1 == len(params["layers"]):
+                _log(f"oracle layer {li + 1}/{len(params['layers'])} "
+                     f"({time.time() - t0:.0f} s)")
+    head = {"final_norm": params["final_norm"].cpu().float().numpy(),
+            "lm_head": params["lm_head"].cpu().float().numpy()}
+    res = {}
+    for name, (act, fused) in variants.items():
+        h, steps = state[name]
+        rows = [OD.logits(h[:, -1], head, cfg, act)]
+        rows += [OD.logits(ht[:, -1], head, cfg, act, fused=fused) for ht in steps]
+        res[name] = np.stack(rows, 0)
+    return res
+
+
+def test_c5_full_size_vs_oracle():
+    """c5 at its stated size against the oracle: the 40-layer model with
+    vocab 49155, a compiled 4 x 1024 prefill and 8 teacher-forced steps of
+    the graph-replayed compiled decode step (the benchmark's programs and
+    weights), the last-position prefill logits and every step's logits of
+    one batch row against the oracle at the device's rounding points and in
+    float32, computed layer by layer on the host.
+
+    Over 40 random-init layers a one-ulp fp16 difference in an early
+    activation grows to a few 1e-2 in the logits, so two correct fp16
+    programs (the oracle's fp16 form and the device) each differ from the
+    float32 form at a large fraction of the logits; the gate is the
+    oracle's own fp16-vs-float32 distance: the device may differ from the
+    float32 oracle by at most 1.5x its relative L2 error and largest
+    deviation and 2x its fraction beyond rtol = atol = 1e-2.  A real fault
+    (a wrong layer, a misplaced cache entry, a dropped term) moves the
+    logits by their own scale, ~100x that floor.  Greedy tokens must equal
+    the float32 oracle's argmax wherever its top two logits are further
+    apart than the floor's largest deviation; the token-match rate over
+    all checked positions is reported."""
+    cfg, B, S, T = D.C5, 4, 1024, 8
+    rows = (1,)
+    t0 = time.time()
+    _log("c5 40 layers vs oracle: init weights")
+    params = D.init_params(cfg, DEV, seed=0xAFFE + 5, pool_elems=1 << 26)
+    prompt = _tokens(B, S, cfg.vocab, seed=5)
+    teacher = _tokens(B, T, cfg.vocab, seed=6)
+    torch._dynamo.reset()
+    layer_fn = torch.compile(D.layer_forward, dynamic=False)
+    decode_fn = torch.compile(D.decode_step_static, dynamic=False)
+    _, logits = D.generate(prompt.to(DEV), params, cfg, T, DEV, layer_fn=layer_fn,
+                           teacher=teacher.to(DEV), decode_fn=decode_fn, use_graph=True)
+    got = logits.cpu().float().numpy()[:, list(rows)]
+    assert got.shape == (T + 1, len(rows), cfg.vocab) and np.isfinite(got).all()
+    _log(f"device prefill + {T} teacher-forced graph steps done at {time.time() - t0:.0f} s")
+    res = _oracle_rows_layerwise(params, prompt.numpy()[list(rows)],
+                                 teacher.numpy()[list(rows)], cfg,
+                                 {"fp16": (np.float16, True), "fp32": (None, False)})
+    want16, exact = res["fp16"], res["fp32"]
+    frac16, max16 = _violations(got, want16)
+    frac32, max32 = _violations(got, exact)
+    ffrac, fmax = _violations(want16, exact)
+    rel16, rel32, frel = _rel_l2(got, want16), _rel_l2(got, exact), _rel_l2(want16, exact)
+    top2 = np.sort(exact, axis=-1)[..., -2:]
+    decided = (top2[..., 1] - top2[..., 0]) > fmax
+    match = got.argmax(-1) == exact.argmax(-1)
+    match16 = want16.argmax(-1) == exact.argmax(-1)
+    _log(f"c5 40 layers, row {rows}, prefill + {T} steps: device vs fp16 oracle {frac16:.2e} "
+         f"beyond 1e-2, max {max16:.4f}, rel L2 {rel16:.2e}; device vs fp32 oracle "
+         f"{frac32:.2e}, max {max32:.4f}, rel L2 {rel32:.2e}; floor (oracle fp16 vs fp32) "
+         f"{ffrac:.2e}, max {fmax:.4f}, rel L2 {frel:.2e}; token match vs fp32 argmax "
+         f"{int(match.sum())}/{match.size} (oracle fp16: {int(match16.sum())}/{match.size}), "
+         f"decided {int(decided.sum())}/{decided.size} ({time.time() - t0:.0f} s)")
+    assert frac32 <= max(2 * ffrac, 1e-5) and max32 <= 1.5 * max(fmax, 1e-2)
+    assert rel32 <= 1.5 * frel
+    assert np.array_equal(match[decided], np.ones(int(decided.sum()), bool))
+    # every greedy choice is a near-best token under exact arithmetic: its
+    # float32 logit is within the floor's largest deviation of the best one
+    chosen = np.take_along_axis(exact, got.argmax(-1)[..., None], -1)[..., 0]
+    assert np.all(chosen >= exact.max(-1) - 1.5 * max(fmax, 1e-2))
 
 
 def test_c5_full_size_flow():

@@ -311,6 +311,15 @@ def test_c1_softmax_config_vs_oracle():
     assert_close_fp(y, O.softmax(x.numpy()), what="c1 softmax")
 
 
+def test_c3_rms_norm_eager_config_size():
+    """Eager rms_norm on spyre tensors at the c3 size the benchmark times."""
+    _log("eager rms_norm [8192,4096] vs oracle")
+    x = randn((8192, 4096), k=0)
+    w = randn((4096,), k=2, scale=0.02, mean=1.0)
+    r = torch.nn.functional.rms_norm(x.to(DEV), [4096], w.to(DEV), 1e-5)
+    assert_close_fp(r, O.rmsnorm(x.numpy(), w.numpy(), 1e-5)[0], what="rms_norm [8192,4096]")
+
+
 def test_layer_norm_and_rms_norm():
     _log("layer_norm / rms_norm")
     x = randn((64, 4096), k=0)
