@@ -5,7 +5,7 @@ Produces, next to the Python sources so they travel with the tree:
   torch_spyre/_C.<abi>.so           the PrivateUse1 backend extension (g++,
                                     ATen glue over the C-ABI)
 
-Usage: python torch-spyre_amd/build.py [--only hip|aten] [-j N]
+Usage: python torch-spyre_amd/build.py [--only hip|aten] [-j N] [--incremental]
 Every invocation recompiles everything (no stale objects survive a build).
 """
 
@@ -61,9 +61,21 @@ def _torch_lib_dir() -> str:
     return os.path.join(os.path.dirname(torch.__file__), "lib")
 
 
-def build_hip(jobs: int) -> str:
+def _stale(obj: str, src: str, header_dirs: list[str]) -> bool:
+    """True when obj is missing or older than src or any header under
+    header_dirs."""
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    deps = [src] + [os.path.join(d, f) for d in header_dirs for f in os.listdir(d)
+                    if f.endswith((".h", ".hpp", ".cuh"))]
+    return any(os.path.getmtime(p) > t for p in deps)
+
+
+def build_hip(jobs: int, incremental: bool = False) -> str:
     objdir = os.path.join(BUILD_DIR, "hip")
-    shutil.rmtree(objdir, ignore_errors=True)
+    if not incremental:
+        shutil.rmtree(objdir, ignore_errors=True)
     os.makedirs(objdir, exist_ok=True)
     os.makedirs(LIB_DIR, exist_ok=True)
     srcs = sorted(f for f in os.listdir(HIP_SRC) if f.endswith(".hip"))
@@ -71,6 +83,8 @@ def build_hip(jobs: int) -> str:
 
     def compile_one(pair):
         src, obj = pair
+        if incremental and not _stale(obj, os.path.join(HIP_SRC, src), [HIP_SRC, INCLUDE]):
+            return obj
         _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(HIP_SRC, src), "-o", obj])
         return obj
 
@@ -88,7 +102,7 @@ def build_hip(jobs: int) -> str:
     return out
 
 
-def build_aten(jobs: int) -> str | None:
+def build_aten(jobs: int, incremental: bool = False) -> str | None:
     if not os.path.isdir(ATEN_SRC):
         return None
     srcs = sorted(f for f in os.listdir(ATEN_SRC) if f.endswith(".cpp"))
@@ -97,7 +111,8 @@ def build_aten(jobs: int) -> str | None:
     from torch.utils import cpp_extension
 
     objdir = os.path.join(BUILD_DIR, "aten")
-    shutil.rmtree(objdir, ignore_errors=True)
+    if not incremental:
+        shutil.rmtree(objdir, ignore_errors=True)
     os.makedirs(objdir, exist_ok=True)
     py_inc = sysconfig.get_paths()["include"]
     incs = [f"-I{p}" for p in cpp_extension.include_paths()] + [
@@ -113,6 +128,8 @@ def build_aten(jobs: int) -> str | None:
 
     def compile_one(pair):
         src, obj = pair
+        if incremental and not _stale(obj, os.path.join(ATEN_SRC, src), [ATEN_SRC, INCLUDE]):
+            return obj
         _run(["g++", *cflags, "-c", os.path.join(ATEN_SRC, src), "-o", obj])
         return obj
 
@@ -134,11 +151,13 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--only", choices=["hip", "aten"], default=None)
     ap.add_argument("-j", "--jobs", type=int, default=min(8, os.cpu_count() or 1))
+    ap.add_argument("--incremental", action="store_true",
+                    help="keep object files newer than their source and the headers")
     args = ap.parse_args(argv)
     if args.only in (None, "hip"):
-        print("built", build_hip(args.jobs), flush=True)
+        print("built", build_hip(args.jobs, args.incremental), flush=True)
     if args.only in (None, "aten"):
-        out = build_aten(args.jobs)
+        out = build_aten(args.jobs, args.incremental)
         if out:
             print("built", out, flush=True)
     return 0
