@@ -358,6 +358,87 @@ def bench_attention(steps, warmup, stream, capi):
     return out
 
 
+def bench_decode_step(reps, stream, capi):
+    """c5's fused decode-step attention (sph_decode_attention_step: RoPE,
+    KV-cache append and attention over keys 0..pos, plus the merge of the
+    64-key partials): batch 4, 32 query / 8 KV heads, a 1152-slot cache with
+    dim-major V, position 1087 (the mean of c5's 128 steps).  16 cache
+    copies (302 MB, more than the 256 MB MALL) are used in turn, so K and V
+    come from HBM as in the decode step, where 16 GB of weights pass between
+    two visits of a layer's cache.  Algorithmic bytes: K and V of keys
+    0..pos."""
+    import math
+
+    import torch
+
+    lib = capi.lib()
+    B, H, Hkv, L, D, pos, ncopy = 4, 32, 8, 1152, 128, 1087, 16
+    g = _gen(60)
+    ks = [torch.randn(B, Hkv, L, D, generator=g).half().cuda() for _ in range(ncopy)]
+    vs = [torch.randn(B, Hkv, D, L, generator=g).half().cuda() for _ in range(ncopy)]
+    ang = torch.arange(L, dtype=torch.float32)[:, None] * \
+        (1e4 ** (-torch.arange(0, D, 2, dtype=torch.float32) / D))[None, :]
+    ang = torch.cat([ang, ang], -1)
+    cs, sn = ang.cos().half().cuda(), ang.sin().half().cuda()
+    qkv = torch.randn(B, (H + 2 * Hkv) * D, generator=g).half().cuda()
+    nws = lib.sph_decode_attention_step_workspace_bytes(B, H, Hkv, L)
+    ws = torch.empty(nws, dtype=torch.uint8, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = torch.empty(B, H * D, dtype=torch.float16, device="cuda")
+    pd = torch.tensor([pos], dtype=torch.int64, device="cuda")
+    turn = [0]
+
+    def launch(st):
+        kc, vc = ks[turn[0] % ncopy], vs[turn[0] % ncopy]
+        turn[0] += 1
+        capi.check(lib.sph_decode_attention_step(
+            capi.F16, B, H, Hkv, D, qkv.data_ptr(), qkv.stride(0), cs.data_ptr(), sn.data_ptr(),
+            cs.stride(0), pd.data_ptr(), err.data_ptr(), kc.data_ptr(), kc.stride(0),
+            kc.stride(1), kc.stride(2), vc.data_ptr(), vc.stride(0), vc.stride(1), 1,
+            vc.stride(2), L, 1.0 / math.sqrt(D), out.data_ptr(), out.stride(0), ws.data_ptr(),
+            nws, st), "sph_decode_attention_step")
+
+    us = graph_us(launch, reps, per_graph=ncopy)
+    torch.cuda.synchronize()
+    assert int(err.cpu()[0]) == 0
+    nbytes = 2 * B * Hkv * (pos + 1) * D * 2
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"c5_decode_attention_step": {
+        "us_per_call": round(us, 2), "algorithmic_bytes": nbytes, "GB/s": round(gbs, 1),
+        "roofline_frac": round(gbs / PEAK_HBM_GBS, 4), "bound": "hbm",
+        "note": "step kernel + merge kernel back to back in a HIP graph, K/V from HBM"}}
+
+
+def bench_launch_floor(reps, capi):
+    """What a small kernel costs back to back in one HIP graph (GPU time per
+    launch): torch's fill of one element (the dispatch floor), torch's copy
+    of 4 MiB into 4 MiB (the 8 MiB that c1's softmax reads and writes, at
+    the same launch count) and the c1 softmax itself through the C-ABI.  A
+    softmax near the copy's time is at the floor that launch latency and
+    first-byte latency set for this many bytes, whatever its arithmetic."""
+    import torch
+
+    lib = capi.lib()
+    R, C = 512, 4096
+    one = torch.empty(1, dtype=torch.float16, device="cuda")
+    src = torch.randn(R, C, generator=_gen(0)).half().cuda()
+    dst = torch.empty_like(src)
+    x = (torch.randn(R, C, generator=_gen(0)) * 4).half().cuda()
+    y = torch.empty_like(x)
+    out = {}
+    for name, fn in (
+            ("fill_1_element_torch", lambda st: one.fill_(1.0)),
+            ("copy_4MiB_torch", lambda st: dst.copy_(src)),
+            ("c1_softmax_512x4096", lambda st: capi.check(
+                lib.sph_softmax_rows_f16(x.data_ptr(), y.data_ptr(), R, C, st),
+                "sph_softmax_rows_f16"))):
+        out[name] = {"us_per_launch": round(graph_us(fn, reps, per_graph=50), 2)}
+    nbytes = 2 * R * C * 2
+    for k in ("copy_4MiB_torch", "c1_softmax_512x4096"):
+        out[k]["GB/s"] = round(nbytes / (out[k]["us_per_launch"] * 1e-6) / 1e9, 1)
+    return {"launch_floor": out}
+
+
 def bench_bmm(steps, warmup, stream, capi):
     """c2 bmm 32 x [2048,128] x [128,2048]: HBM-bound (AI 113.8 < ridge 314.6)."""
     import torch
@@ -890,9 +971,10 @@ def main(argv=None):
     ap.add_argument("--c5-layers", type=int, default=40)
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--kernel", choices=["all", "gemm", "copy", "decoder", "bmm", "h2d",
-                                         "attention", "spyre", "rows"],
+                                         "attention", "spyre", "rows", "decode_step", "floor"],
                     default="all",
-                    help="gemm / copy / decoder / bmm / h2d / attention / rows (c1 softmax and "
+                    help="gemm / copy / decoder / bmm / h2d / attention / decode_step / floor / "
+                         "rows (c1 softmax and "
                          "the c3 row kernels) / spyre (the eager and compiled paths on spyre "
                          "tensors): run only that part (for rocprofv3 passes)")
     ap.add_argument("--traffic-from", metavar="DIR",
@@ -931,6 +1013,13 @@ def main(argv=None):
         print(json.dumps({"kernel": "attention",
                           **bench_attention(args.steps, args.warmup, stream, _capi)}))
         return 0
+    if args.kernel == "floor":
+        print(json.dumps({"kernel": "floor", **bench_launch_floor(max(20, args.steps), _capi)}))
+        return 0
+    if args.kernel == "decode_step":
+        print(json.dumps({"kernel": "decode_step",
+                          **bench_decode_step(max(20, args.steps), stream, _capi)}))
+        return 0
     if args.kernel == "h2d":
         print(json.dumps({"kernel": "h2d", **bench_host_copies()}))
         return 0
@@ -955,6 +1044,8 @@ def main(argv=None):
         extra = bench_extra(max(10, args.steps), sub_w, stream, _capi)
         _log("fused attention (c4 shape)")
         extra.update(bench_attention(max(10, args.steps), sub_w, stream, _capi))
+        _log("decode-step attention (c5 shape)")
+        extra.update(bench_decode_step(max(20, args.steps), stream, _capi))
     _log("gemm 4096^3")
     g = bench_gemm(args.steps, args.warmup, stream, _capi)
     if not args.no_extra:

@@ -21,6 +21,8 @@
 // Rows whose keys are all masked yield NaN, as softmax over all -inf does.
 #include "sph_common.h"
 
+#include <type_traits>
+
 namespace sph {
 namespace {
 
@@ -391,19 +393,24 @@ extern "C" int sph_attention_decode(sph_dtype dtype, int64_t batch, int64_t mq, 
 //
 // Layout: K cache [.., max_len, 128] key-major (dim stride 1); V cache
 // key-major or dim-major ([.., 128, max_len], key stride 1, the layout the
-// decoder's caches keep).  Each workgroup takes one unit and one 64-key
-// chunk (grid = chunks of max_len x units; P is only known on the device,
-// so chunks past P do nothing but report), stages the chunk's K and V in
-// LDS while the queries are rotated, computes the G x 64 scores (one key
-// per lane, one query head per wave), their softmax state (max, sum) and
-// the unnormalised G x 128 output and writes that partial to the
-// workspace (a chunk past P writes a neutral one); a second kernel merges
-// each unit's partials and writes O.  (Merging in the last workgroup of a unit to arrive,
-// behind an atomic count, needs a device-scope release per workgroup: on
-// this 8-XCD part each one writes back the XCD's L2, and 576 of them took
-// 87 us against a few for the two launches.)  The chunk holding P takes the
-// new key and value from the rotated registers, not from the cache it
-// writes in the same launch.
+// decoders' caches keep).  Each workgroup (256 threads) takes one unit and
+// one 64-key chunk (grid = chunks of max_len x units; P is only known on
+// the device, so chunks past P do nothing but report), stages the chunk's
+// K and V in LDS while the queries are rotated, computes the G x 64 scores
+// (one key per lane, one query head per wave, v_dot2_f32_f16 on the
+// rounded query), their softmax state (max, sum) and the unnormalised
+// G x 128 output, and writes that partial to the workspace (a chunk past P
+// writes a neutral one); a second kernel merges each unit's partials and
+// writes O.  Measured alternatives (c5: 4 x 8 KV heads, 1152 slots,
+// 18.9 MB of K / V): larger chunks on more threads (128 to 256 keys on 256
+// to 1024 threads) run 8.0-11.3 us against 7.4, since fewer workgroups per
+// CU overlap one's loads with another's arithmetic; one workgroup per
+// unit with no merge reads the bytes alone in 11.5 us (one CU pulls ~50
+// GB/s); merging in the last workgroup of a unit to arrive, behind an
+// atomic count, needs a device-scope release per workgroup, which on this
+// 8-XCD part writes back the XCD's L2 (576 of them took 87 us).  The chunk
+// holding P takes the new key and value from the rotated registers, not
+// from the cache it writes in the same launch.
 //
 // Rounding: rotated q and k round once to the element type (k as it is
 // stored); scores, softmax and the output sums are fp32; O rounds once.
@@ -412,11 +419,11 @@ namespace sph {
 namespace {
 
 constexpr int SG = 8;              // max query heads per KV head
-constexpr int SKC = 64;            // keys per chunk
-constexpr int kStepThreads = 256;  // 4 waves
+constexpr int SKB = 64;            // keys per score block (one key per lane)
 constexpr int kMaxUnits = 4096;    // batch x KV heads per launch
 constexpr int kStepPart = 2 + DD;  // m, l, o[128] per query head
 constexpr int32_t kStepBadPos = 2;  // error code: position outside [0, max_len)
+constexpr int kMinChunk = 64;      // the smallest chunk any launch shape uses
 
 struct StepArgs {
   const void* qkv;
@@ -444,14 +451,52 @@ __device__ inline u32x4 zero_chunk() {
   return z;
 }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-template <typename T, bool VT>
-__global__ void __launch_bounds__(kStepThreads) attn_decode_step_kernel(const StepArgs p) {
+// acc + the dot product of 8 two-byte values a and b (16 bytes each):
+// fp16 as four v_dot2_f32_f16 (exact products, fp32 sums), bf16 widened by
+// shifts into fp32 FMAs.
+template <typename T>
+__device__ inline float dot8(u32x4 a, u32x4 b, float acc) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t ai = a[i], bi = b[i];
+    if constexpr (__is_same(T, half_t)) {
+      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, ai), __builtin_bit_cast(f16x2, bi),
+                                   acc, false);
+    } else {
+      acc = fmaf(__uint_as_float(ai << 16), __uint_as_float(bi << 16), acc);
+      acc = fmaf(__uint_as_float(ai & 0xffff0000u), __uint_as_float(bi & 0xffff0000u), acc);
+    }
+  }
+  return acc;
+}
+
+// One workgroup of NT threads: one unit (blockIdx.y) and one chunk of SKC
+// keys (blockIdx.x).  The chunk's K and V (SKC * 16 / NT 16-byte loads of
+// each per thread, all in flight at once) are loaded before P is known.
+// Scores: work item (query head i, 64-key block kb) on a wave, one key per
+// lane; each block keeps its own max and sum, so no barrier joins the
+// blocks before P V.  P V: item (query head i, key split r) on a slot of
+// 128 threads, one head-dim column per thread; the R splits of a head meet
+// in LDS, each block's sum scaled by 2^(m_block - m_chunk).
+template <typename T, bool VT, int SKC, int NT>
+__global__ void __launch_bounds__(NT) attn_decode_step_kernel(const StepArgs p) {
+  constexpr int NB = SKC / SKB;       // score blocks per chunk
+  constexpr int NW = NT / 64;         // waves
+  constexpr int SLOTS = NT / DD;      // P V thread slots
+  constexpr int LOADS = SKC * DD / 8 / NT;  // 16-byte K (and V) loads per thread
+  constexpr int SVPITCH = SKC + 8;    // dim-major V rows in LDS
+  constexpr int VCH = SKC / 8;        // 16-byte chunks per dim-major V row
+  static_assert(LOADS * NT * 8 == SKC * DD && NB * SKB == SKC && SLOTS >= 1, "launch shape");
+  // ps holds the probabilities, then (after the P V sums) the split sums
+  constexpr int PS = SKC > DD ? SG * SKC : SG * DD;
+  constexpr int MAXW = (SG + SLOTS - 1) / SLOTS;  // P V items per slot, at most
   __shared__ __attribute__((aligned(16))) T ks[SKC][KPITCH];
-  __shared__ __attribute__((aligned(16))) T vs[VT ? DD : SKC][VT ? VPITCH_T : KPITCH];
-  __shared__ __attribute__((aligned(16))) float qs[SG][DD];
-  __shared__ __attribute__((aligned(16))) float ps[SG][SKC];
-  __shared__ float mrow[SG], lrow[SG];
+  __shared__ __attribute__((aligned(16))) T vs[VT ? DD : SKC][VT ? SVPITCH : KPITCH];
+  __shared__ __attribute__((aligned(16))) T qs[SG][DD];
+  __shared__ __attribute__((aligned(16))) float ps[PS];
+  __shared__ float mblk[SG][NB], lblk[SG][NB];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int unit = blockIdx.y, chunk = blockIdx.x;
   const int b = unit / p.n_kv, h = unit % p.n_kv, G = p.g;
@@ -463,14 +508,14 @@ __global__ void __launch_bounds__(kStepThreads) attn_decode_step_kernel(const St
   // every address is inside the cache) and P itself are loaded together.
   const int64_t P = *p.pos;
   const int kmax = static_cast<int>(min<int64_t>(SKC, p.max_len - kbase));
-  u32x4 kr[4], vr[4];
+  u32x4 kr[LOADS], vr[LOADS];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int x = t + kStepThreads * i, key = x >> 4, cc = (x & 15) * 8;
+  for (int i = 0; i < LOADS; ++i) {
+    const int x = t + NT * i, key = x >> 4, cc = (x & 15) * 8;
     kr[i] = key < kmax ? *reinterpret_cast<const u32x4*>(Kc + (kbase + key) * p.k_ss + cc)
                        : zero_chunk();
     if constexpr (VT) {
-      const int dm = x >> 3, kc = (x & 7) * 8;
+      const int dm = x / VCH, kc = (x % VCH) * 8;
       const T* src = Vc + dm * p.v_ds + kbase + kc;
       if (p.v_al && kc + 8 <= kmax) {
         vr[i] = *reinterpret_cast<const u32x4*>(src);
@@ -491,19 +536,20 @@ __global__ void __launch_bounds__(kStepThreads) attn_decode_step_kernel(const St
   }
   // The step's queries (element d and its rotate-half partner) and the new
   // key / value do not depend on P either.
-  constexpr int QR = SG * DD / kStepThreads;  // query elements per thread
+  constexpr int QR = SG * DD / NT;  // query elements per thread
+  static_assert(QR >= 1 && QR * NT == SG * DD, "whole query rows per thread");
   const int dq = t & (DD - 1), dpart = dq < DD / 2 ? dq + DD / 2 : dq - DD / 2;
   float qa[QR], qb[QR];
 #pragma unroll
   for (int r = 0; r < QR; ++r) {
-    const int i = (t + kStepThreads * r) / DD;
+    const int i = (t + NT * r) / DD;
     const T* q = row + static_cast<int64_t>(h * G + (i < G ? i : 0)) * DD;
     qa[r] = Num<T>::to_f(q[dq]);
     qb[r] = Num<T>::to_f(q[dpart]);
   }
   const T* knew = row + static_cast<int64_t>(p.n_heads + h) * DD;
   const T* vnew = row + static_cast<int64_t>(p.n_heads + p.n_kv + h) * DD;
-  const float ka = Num<T>::to_f(knew[dq]), kb = Num<T>::to_f(knew[dpart]);
+  const float ka = Num<T>::to_f(knew[dq]), kb_ = Num<T>::to_f(knew[dpart]);
   const T vv = vnew[dq];
   if (P < 0 || P >= p.max_len) {
     // nothing is written (every workgroup sees the same P); the caller's
@@ -521,90 +567,104 @@ __global__ void __launch_bounds__(kStepThreads) attn_decode_step_kernel(const St
     }
     return;
   }
-  {
-    const int nkeys = static_cast<int>(min<int64_t>(SKC, P + 1 - kbase));
-    const T* cs = static_cast<const T*>(p.cos) + P * p.ld_rope;
-    const T* sn = static_cast<const T*>(p.sin) + P * p.ld_rope;
-    const float cd = Num<T>::to_f(cs[dq]), sd = Num<T>::to_f(sn[dq]);
-    const float sgn = dq < DD / 2 ? -1.f : 1.f;  // rot(x)[d] = -x[d + 64] | x[d - 64]
-    // rotated queries (rounded as a stored tensor would be), scaled into
-    // log2 units
+  const int nkeys = static_cast<int>(min<int64_t>(SKC, P + 1 - kbase));
+  const T* cs = static_cast<const T*>(p.cos) + P * p.ld_rope;
+  const T* sn = static_cast<const T*>(p.sin) + P * p.ld_rope;
+  const float cd = Num<T>::to_f(cs[dq]), sd = Num<T>::to_f(sn[dq]);
+  const float sgn = dq < DD / 2 ? -1.f : 1.f;  // rot(x)[d] = -x[d + 64] | x[d - 64]
+  // rotated queries, rounded as a stored tensor would be (the scores are
+  // scaled into log2 units after the dot products)
 #pragma unroll
-    for (int r = 0; r < QR; ++r) {
-      const int i = (t + kStepThreads * r) / DD;
-      if (i < G) {
-        const float rq = Num<T>::to_f(Num<T>::from_f(qa[r] * cd + sgn * qb[r] * sd));
-        qs[i][dq] = rq * p.scale_log2;
-      }
-    }
-    // Slots past P (the chunk holding P) may hold anything, NaN or Inf
-    // included: their scores are replaced by -inf below, and their values
-    // are staged as zeros so that a zero probability times a stale value
-    // adds nothing to the output sums.
+  for (int r = 0; r < QR; ++r) {
+    const int i = (t + NT * r) / DD;
+    if (i < G) qs[i][dq] = Num<T>::from_f(qa[r] * cd + sgn * qb[r] * sd);
+  }
+  // Slots past P (the chunk holding P) may hold anything, NaN or Inf
+  // included: their scores are replaced by -inf below, and their values
+  // are staged as zeros so that a zero probability times a stale value
+  // adds nothing to the output sums.
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int x = t + kStepThreads * i, key = x >> 4, cc = (x & 15) * 8;
-      *reinterpret_cast<u32x4*>(&ks[key][cc]) = kr[i];
-      if constexpr (VT) {
-        const int dm = x >> 3, kc = (x & 7) * 8;
-        u32x4 w = vr[i];
-        if (kc + 8 > nkeys) {
+  for (int i = 0; i < LOADS; ++i) {
+    const int x = t + NT * i, key = x >> 4, cc = (x & 15) * 8;
+    *reinterpret_cast<u32x4*>(&ks[key][cc]) = kr[i];
+    if constexpr (VT) {
+      const int dm = x / VCH, kc = (x % VCH) * 8;
+      u32x4 w = vr[i];
+      if (kc + 8 > nkeys) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const uint32_t keep = (kc + 2 * q < nkeys ? 0x0000FFFFu : 0u) |
-                                  (kc + 2 * q + 1 < nkeys ? 0xFFFF0000u : 0u);
-            w[q] &= keep;
-          }
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t keep = (kc + 2 * q < nkeys ? 0x0000FFFFu : 0u) |
+                                (kc + 2 * q + 1 < nkeys ? 0xFFFF0000u : 0u);
+          w[q] &= keep;
         }
-        *reinterpret_cast<u32x4*>(&vs[dm][kc]) = w;
-      } else {
-        *reinterpret_cast<u32x4*>(&vs[key][cc]) = key < nkeys ? vr[i] : zero_chunk();
       }
+      *reinterpret_cast<u32x4*>(&vs[dm][kc]) = w;
+    } else {
+      *reinterpret_cast<u32x4*>(&vs[key][cc]) = key < nkeys ? vr[i] : zero_chunk();
     }
-    const int own = static_cast<int>(P - kbase);  // the new key's slot, if here
-    __syncthreads();  // chunk staged: the new key / value replace slot `own`
-    if (own < SKC && t < DD) {
-      const T kr_ = Num<T>::from_f(ka * cd + sgn * kb * sd);
-      const T vr_ = vv;
-      ks[own][t] = kr_;
-      if constexpr (VT) vs[t][own] = vr_;
-      else vs[own][t] = vr_;
-      Kc[P * p.k_ss + t] = kr_;
-      if constexpr (VT) Vc[t * p.v_ds + P] = vr_;
-      else Vc[P * p.v_ks + t] = vr_;
+  }
+  const int own = static_cast<int>(P - kbase);  // the new key's slot, if here
+  __syncthreads();  // chunk staged: the new key / value replace slot `own`
+  if (own < SKC && t < DD) {
+    const T kr_ = Num<T>::from_f(ka * cd + sgn * kb_ * sd);
+    const T vr_ = vv;
+    ks[own][t] = kr_;
+    if constexpr (VT) vs[t][own] = vr_;
+    else vs[own][t] = vr_;
+    Kc[P * p.k_ss + t] = kr_;
+    if constexpr (VT) Vc[t * p.v_ds + P] = vr_;
+    else Vc[P * p.v_ks + t] = vr_;
+  }
+  __syncthreads();
+  // scores: item (head i, block kb), key kb * 64 + lane; each block's
+  // probabilities relative to its own max (a block with no visible key has
+  // max -inf and contributes nothing)
+  for (int it = wave; it < G * NB; it += NW) {
+    const int i = it / NB, kb = it % NB, key = kb * SKB + lane;
+    float s = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < DD; cc += 8)
+      s = dot8<T>(*reinterpret_cast<const u32x4*>(&qs[i][cc]),
+                  *reinterpret_cast<const u32x4*>(&ks[key][cc]), s);
+    s = key < nkeys ? s * p.scale_log2 : -INFINITY;
+    float mx = s;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    const float pj = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s - mx);
+    float sum = pj;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    ps[i * SKC + key] = pj;
+    if (lane == 0) {
+      mblk[i][kb] = mx;
+      lblk[i][kb] = sum;
     }
-    __syncthreads();
-    // scores: key `lane`, query head i = wave, wave + 4
-    for (int i = wave; i < G; i += kStepThreads / 64) {
-      float s = 0.f;
+  }
+  __syncthreads();
+  // unnormalised P V: R key splits per head, the largest power of two
+  // dividing NB with G * R <= SLOTS (at least 1: a slot then takes several
+  // heads)
+  int R = 1;
+  while (2 * R <= NB && G * 2 * R <= SLOTS) R *= 2;
+  const int slot = t >> 7, d = t & (DD - 1);
+  const int bps = NB / R;  // blocks per split
+  float acc_w[MAXW];
 #pragma unroll
-      for (int cc = 0; cc < DD; cc += 8) {
-        const u32x4 kw = *reinterpret_cast<const u32x4*>(&ks[lane][cc]);
-        const T* ke = reinterpret_cast<const T*>(&kw);
+  for (int n = 0; n < MAXW; ++n) {
+    const int w = slot + n * SLOTS;
+    acc_w[n] = 0.f;
+    if (w >= G * R) continue;
+    const int i = w / R, split = w % R;
+    float mi = -INFINITY;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s = fmaf(qs[i][cc + e], Num<T>::to_f(ke[e]), s);
-      }
-      s = lane < nkeys ? s : -INFINITY;
-      float mx = s;
+    for (int kb = 0; kb < NB; ++kb) mi = fmaxf(mi, mblk[i][kb]);
+    float acc = 0.f;
+    for (int kb = split * bps; kb < (split + 1) * bps; ++kb) {
+      const float m = mblk[i][kb];
+      if (m == -INFINITY) continue;
+      float a = 0.f;
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-      const float pj = __builtin_amdgcn_exp2f(s - mx);  // key 0 of the chunk is visible
-      float sum = pj;
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-      ps[i][lane] = pj;
-      if (lane == 0) {
-        mrow[i] = mx;
-        lrow[i] = sum;
-      }
-    }
-    __syncthreads();
-    // unnormalised P V: column d, query heads i = t / 128, + 2, ...
-    const int d = t & (DD - 1);
-    for (int i = t >> 7; i < G; i += kStepThreads / DD) {
-      float acc = 0.f;
-#pragma unroll
-      for (int j = 0; j < SKC; j += 8) {
+      for (int j = kb * SKB; j < (kb + 1) * SKB; j += 8) {
         float vf[8];
         if constexpr (VT) {
           const u32x4 vw = *reinterpret_cast<const u32x4*>(&vs[d][j]);
@@ -615,14 +675,39 @@ __global__ void __launch_bounds__(kStepThreads) attn_decode_step_kernel(const St
 #pragma unroll
           for (int e = 0; e < 8; ++e) vf[e] = Num<T>::to_f(vs[j + e][d]);
         }
+        const float4 p0 = *reinterpret_cast<const float4*>(&ps[i * SKC + j]);
+        const float4 p1 = *reinterpret_cast<const float4*>(&ps[i * SKC + j + 4]);
+        const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc = fmaf(ps[i][j + e], vf[e], acc);
+        for (int e = 0; e < 8; ++e) a = fmaf(pv[e], vf[e], a);
       }
-      part[i * kStepPart + 2 + d] = acc;
-      if (d == 0) {
-        part[i * kStepPart] = mrow[i];
-        part[i * kStepPart + 1] = lrow[i];
+      acc = fmaf(a, __builtin_amdgcn_exp2f(m - mi), acc);
+    }
+    acc_w[n] = acc;
+  }
+  __syncthreads();  // every P V read of ps is done: it now takes the split sums
+#pragma unroll
+  for (int n = 0; n < MAXW; ++n) {
+    const int w = slot + n * SLOTS;
+    if (w < G * R) ps[w * DD + d] = acc_w[n];
+  }
+  __syncthreads();
+  for (int i = slot; i < G; i += SLOTS) {
+    float acc = 0.f;
+    for (int r = 0; r < R; ++r) acc += ps[(i * R + r) * DD + d];
+    part[i * kStepPart + 2 + d] = acc;
+    if (d == 0) {
+      float mi = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < NB; ++kb) mi = fmaxf(mi, mblk[i][kb]);
+      float l = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < NB; ++kb) {
+        const float m = mblk[i][kb];
+        l += m == -INFINITY ? 0.f : lblk[i][kb] * __builtin_amdgcn_exp2f(m - mi);
       }
+      part[i * kStepPart] = mi;
+      part[i * kStepPart + 1] = l;
     }
   }
 }
@@ -685,7 +770,7 @@ extern "C" int64_t sph_decode_attention_step_workspace_bytes(int64_t batch, int6
                                                               int64_t max_len) {
   if (batch <= 0 || n_kv_heads <= 0 || n_heads <= 0 || max_len <= 0) return 0;
   const int64_t g = n_heads / n_kv_heads;
-  return batch * n_kv_heads * ((max_len + SKC - 1) / SKC) * g * kStepPart * 4;
+  return batch * n_kv_heads * ((max_len + kMinChunk - 1) / kMinChunk) * g * kStepPart * 4;
 }
 
 extern "C" int sph_decode_attention_step(
@@ -755,7 +840,15 @@ extern "C" int sph_decode_attention_step(
   p.n_heads = static_cast<int>(n_heads);
   p.n_kv = static_cast<int>(n_kv_heads);
   p.g = static_cast<int>(n_heads / n_kv_heads);
-  p.nchunks = static_cast<int>((max_len + SKC - 1) / SKC);
+  // Launch shape: 64-key chunks on 256 threads (44 KB of LDS, three
+  // workgroups per CU).  Measured on the c5 decode step (4 x 8 KV heads,
+  // 1152 slots, position 1087): 7.4 us against 8.0 us for 128 keys x 512
+  // threads; before the score dot products became v_dot2, 8.0 us against
+  // 10.1 / 8.6 / 11.3 / 9.5 us for 128 x 256 / 128 x 512 / 256 x 512 /
+  // 256 x 1024 (larger chunks leave fewer workgroups per CU to overlap one's
+  // loads with another's arithmetic).
+  constexpr int kChunk = 64, kThreads = 256;
+  p.nchunks = static_cast<int>((max_len + kChunk - 1) / kChunk);
   p.scale_log2 = scale * kLog2eD;
   p.out = out;
   p.ld_out = ld_out;
@@ -763,14 +856,18 @@ extern "C" int sph_decode_attention_step(
   hipStream_t st = as_stream(stream);
   dim3 grid(static_cast<unsigned>(p.nchunks), static_cast<unsigned>(batch * n_kv_heads));
   const dim3 mgrid(static_cast<unsigned>(batch * n_kv_heads * p.g));
+  auto go = [&](auto tag, auto vt_tag) {
+    using T = decltype(tag);
+    constexpr bool VT = decltype(vt_tag)::value;
+    attn_decode_step_kernel<T, VT, kChunk, kThreads><<<grid, kThreads, 0, st>>>(p);
+    attn_decode_step_merge<T><<<mgrid, kMergeThreads, 0, st>>>(p);
+  };
   if (dtype == SPH_F16) {
-    if (vt) attn_decode_step_kernel<half_t, true><<<grid, kStepThreads, 0, st>>>(p);
-    else attn_decode_step_kernel<half_t, false><<<grid, kStepThreads, 0, st>>>(p);
-    attn_decode_step_merge<half_t><<<mgrid, kMergeThreads, 0, st>>>(p);
+    if (vt) go(half_t{}, std::true_type{});
+    else go(half_t{}, std::false_type{});
   } else {
-    if (vt) attn_decode_step_kernel<bf16_t, true><<<grid, kStepThreads, 0, st>>>(p);
-    else attn_decode_step_kernel<bf16_t, false><<<grid, kStepThreads, 0, st>>>(p);
-    attn_decode_step_merge<bf16_t><<<mgrid, kMergeThreads, 0, st>>>(p);
+    if (vt) go(bf16_t{}, std::true_type{});
+    else go(bf16_t{}, std::false_type{});
   }
   return check_launch("sph_decode_attention_step");
 }
