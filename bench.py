@@ -439,6 +439,74 @@ def bench_launch_floor(reps, capi):
     return {"launch_floor": out}
 
 
+# (name, M, N, K, B layout): "nn" = B [K, N] row-major (A @ B), "nt" = B given
+# as a weight [N, K] (A @ W^T, nn.Linear)
+YARDSTICK_SHAPES = [
+    ("c2 4096^3 A@B", 4096, 4096, 4096, "nn"),
+    ("4096^3 A@W^T", 4096, 4096, 4096, "nt"),
+    ("8192^3 A@B", 8192, 8192, 8192, "nn"),
+    ("c4 QKV 2048x6144x4096", 2048, 6144, 4096, "nt"),
+    ("c4 O 2048x4096x4096", 2048, 4096, 4096, "nt"),
+    ("c4 gate/up 2048x25600x4096", 2048, 25600, 4096, "nt"),
+    ("c4 down 2048x4096x12800", 2048, 4096, 12800, "nt"),
+    ("c5 prefill gate/up 4096x25600x4096", 4096, 25600, 4096, "nt"),
+    ("c5 prefill down 4096x4096x12800", 4096, 4096, 12800, "nt"),
+]
+
+
+def bench_gemm_yardstick(stream, capi, settle_ms=60.0, time_ms=40.0):
+    """This build's GEMM (sph_gemm_ex with its split-K workspace, as the
+    ATen mm / linear ops call it) next to torch's ROCm BLAS with hipBLASLt
+    selected, on the same fp16 operands (U(-1, 1)), at the c2 / c4 / c5
+    shapes and 8192^3.  Each side runs ~settle_ms of untimed launches (the
+    part's steady clock) and then ~time_ms of timed ones (HIP events on one
+    stream); a sample of rows of both results must agree within 1e-2, so
+    both do the same work."""
+    import torch
+
+    torch.backends.cuda.preferred_blas_library("cublaslt")  # hipBLASLt on ROCm
+    lib = capi.lib()
+    s = stream.cuda_stream
+    timer = Timer(stream)
+    out = {}
+    for name, M, N, K, lay in YARDSTICK_SHAPES:
+        A = (torch.rand(M, K, generator=_gen(70)) * 2 - 1).half().cuda()
+        Bm = (torch.rand(*((N, K) if lay == "nt" else (K, N)), generator=_gen(71)) * 2 - 1)
+        Bm = Bm.half().cuda()
+        D = torch.empty(M, N, dtype=torch.float16, device="cuda")
+        nws = lib.sph_gemm_workspace_bytes(1, M, N, K)
+        ws = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
+        tb = 1 if lay == "nt" else 0
+        ldb = K if lay == "nt" else N
+
+        def ours():
+            capi.check(lib.sph_gemm_ex(capi.F16, 0, tb, 1, M, N, K, 1.0, A.data_ptr(), K, 0,
+                                       Bm.data_ptr(), ldb, 0, 0.0, None, 0, 0, 0, D.data_ptr(),
+                                       N, 0, 0, ws.data_ptr(), nws, s), "sph_gemm_ex")
+
+        def theirs():
+            return torch.mm(A, Bm.t() if lay == "nt" else Bm)
+
+        flop = 2.0 * M * N * K
+        est_ms = flop / 1.2e15 * 1e3
+        warm = max(5, int(settle_ms / est_ms))
+        reps = max(5, int(time_ms / est_ms))
+        ms_o, _ = timer.run(ours, reps, warm)
+        with torch.cuda.stream(stream):
+            ms_t, _ = timer.run(theirs, reps, warm)
+            ref = theirs()
+        torch.cuda.synchronize()
+        rows = torch.arange(0, M, max(1, M // 16), device="cuda")
+        torch.testing.assert_close(D.index_select(0, rows).float(),
+                                   ref.index_select(0, rows).float(), rtol=1e-2, atol=1e-2)
+        out[name] = {"M": M, "N": N, "K": K, "B": lay,
+                     "spyre_TFLOP/s": round(flop / ms_o / 1e9, 1),
+                     "hipblaslt_TFLOP/s": round(flop / ms_t / 1e9, 1),
+                     "spyre_frac": round(flop / ms_o / 1e9 / PEAK_FP16_TFLOPS, 4)}
+        del A, Bm, D, ws, ref
+    return {"gemm_yardstick": out}
+
+
 def bench_bmm(steps, warmup, stream, capi):
     """c2 bmm 32 x [2048,128] x [128,2048]: HBM-bound (AI 113.8 < ridge 314.6)."""
     import torch
@@ -971,9 +1039,11 @@ def main(argv=None):
     ap.add_argument("--c5-layers", type=int, default=40)
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--kernel", choices=["all", "gemm", "copy", "decoder", "bmm", "h2d",
-                                         "attention", "spyre", "rows", "decode_step", "floor"],
+                                         "attention", "spyre", "rows", "decode_step", "floor",
+                                         "yardstick"],
                     default="all",
                     help="gemm / copy / decoder / bmm / h2d / attention / decode_step / floor / "
+                         "yardstick (the GEMM next to hipBLASLt) / "
                          "rows (c1 softmax and "
                          "the c3 row kernels) / spyre (the eager and compiled paths on spyre "
                          "tensors): run only that part (for rocprofv3 passes)")
@@ -1012,6 +1082,9 @@ def main(argv=None):
     if args.kernel == "attention":
         print(json.dumps({"kernel": "attention",
                           **bench_attention(args.steps, args.warmup, stream, _capi)}))
+        return 0
+    if args.kernel == "yardstick":
+        print(json.dumps({"kernel": "yardstick", **bench_gemm_yardstick(stream, _capi)}))
         return 0
     if args.kernel == "floor":
         print(json.dumps({"kernel": "floor", **bench_launch_floor(max(20, args.steps), _capi)}))

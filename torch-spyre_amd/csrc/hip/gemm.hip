@@ -612,9 +612,15 @@ constexpr int EPITCH = WTN + 8;
 // K-contiguous row r, chunk c -> 16-byte slot (c ^ ((r >> 1) & 7)).
 __device__ inline int kslot(int r, int c) { return r * CPR + (c ^ ((r >> 1) & 7)); }
 
-// BN = 256 (8 waves, 2 x 4) or 128 (4 waves, 2 x 2).
-template <int BN_>
+// BN = 256 (8 waves, 2 x 4) or 128 (4 waves, 2 x 2) with 128 x 64 wave
+// tiles.  (WTN_ = 128, 128 x 128 wave tiles with 256 accumulator registers
+// in AGPRs, one wave per SIMD on a 256-wide tile, reads a third less from
+// LDS per MFMA but measured 2-3 % slower at 4096^3, 8192^3 and the decoder
+// shapes: one wave per SIMD hides less of the K-tile barrier and the LDS
+// latency.)
+template <int BN_, int WTN_ = WTN>
 struct Cfg {
+  static constexpr int WTN = WTN_, TN = WTN / 32, NMF = TM * TN, EPITCH = WTN + 8;
   static constexpr int BN = BN_, WN = BN / WTN, NW = WM * WN, NT = NW * 64;
   static constexpr int B_BYTES = BN * BKD * 2, STAGE = A_BYTES + B_BYTES;
   static constexpr int LPA = A_BYTES / 1024 / NW, LPB = B_BYTES / 1024 / NW;  // DMA lines per wave
@@ -632,10 +638,11 @@ struct Cfg {
 // of the same columns, so each lane's two accumulators hold the gate and up
 // sums of the same output element and the epilogue combines them in
 // registers.
-template <typename T, bool B_KCONT, int BN_, bool SWIGLU = false>
-__global__ void __launch_bounds__(dl::Cfg<BN_>::NT) gemm_dl_kernel(const GemmArgs p) {
+template <typename T, bool B_KCONT, int BN_, bool SWIGLU = false, int WTN_ = dl::WTN>
+__global__ void __launch_bounds__((dl::Cfg<BN_, WTN_>::NT)) gemm_dl_kernel(const GemmArgs p) {
   using namespace dl;
-  using DC = Cfg<BN_>;
+  using DC = Cfg<BN_, WTN_>;
+  constexpr int WTN = DC::WTN, TN = DC::TN, NMF = DC::NMF, EPITCH = DC::EPITCH;
   static_assert(!SWIGLU || (B_KCONT && BN_ == 256), "SwiGLU tiles: K-contiguous B, 256 wide");
   constexpr int BN = DC::BN, WN = DC::WN, STAGE = DC::STAGE, LPA = DC::LPA, LPB = DC::LPB;
   constexpr int NBR = B_KCONT ? 1 : 2;           // LDS reads per B fragment
@@ -1700,7 +1707,7 @@ inline SplitPlan splitk_plan(int64_t tiles, int64_t ksteps, int bn) {
 }
 
 // Launches the direct-load kernel (and, with a split plan, the reduce).
-template <typename T, int BN, bool SWIGLU = false>
+template <typename T, int BN, bool SWIGLU = false, int WTN_ = dl::WTN>
 int launch_dl(GemmArgs& p, int64_t batch, bool b_kcont, hipStream_t st,
               const SplitPlan* plan = nullptr) {
   p.tiles_m = static_cast<int>(p.m / dl::BM);
@@ -1712,10 +1719,11 @@ int launch_dl(GemmArgs& p, int64_t batch, bool b_kcont, hipStream_t st,
   p.kslice = split ? plan->kslice : 0;
   const int64_t wgs = split ? plan->tail_start + (tiles - plan->tail_start) * plan->splits : tiles;
   dim3 grid(static_cast<unsigned>(wgs), static_cast<unsigned>(batch));
+  constexpr int NTH = dl::Cfg<BN, WTN_>::NT;
   if (b_kcont)
-    gemm_dl_kernel<T, true, BN, SWIGLU><<<grid, dim3(dl::Cfg<BN>::NT), 0, st>>>(p);
+    gemm_dl_kernel<T, true, BN, SWIGLU, WTN_><<<grid, dim3(NTH), 0, st>>>(p);
   else if constexpr (!SWIGLU)
-    gemm_dl_kernel<T, false, BN><<<grid, dim3(dl::Cfg<BN>::NT), 0, st>>>(p);
+    gemm_dl_kernel<T, false, BN, false, WTN_><<<grid, dim3(NTH), 0, st>>>(p);
   if (split) {
     constexpr int OUTN = SWIGLU ? BN / 2 : BN;
     dim3 rg(static_cast<unsigned>(tiles - plan->tail_start), (dl::BM * OUTN) / 1024);
