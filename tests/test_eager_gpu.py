@@ -389,6 +389,54 @@ def test_c2_mm_4096_vs_oracle_sample():
     assert_close_fp(C.index_select(0, rows.to(DEV)), ref, what="c2 mm sampled rows")
 
 
+def test_vector_norm_orders_and_dims():
+    """linalg_vector_norm (reference codegen/inputs/Metadata.yaml:139)
+    against torch's CPU op in float32, over the orders with their own
+    reduction (2, 1, 0, +-inf) and general ones, full and partial dims,
+    keepdim, an explicit result dtype, and torch.norm / F.normalize, which
+    reach it."""
+    _log("linalg.vector_norm")
+    x = randn((6, 33, 70), k=11)
+    x[0, 0, :5] = 0  # zeros for ord 0
+    xd = x.to(DEV)
+    for ord_ in (2, 1, 0, float("inf"), float("-inf"), 3, 0.5):
+        for dim, keepdim in ((None, False), (-1, False), ((0, 2), True), (1, True)):
+            got = torch.linalg.vector_norm(xd, ord_, dim, keepdim)
+            # float32 result rounded to the fp16 result dtype (a full ord-0.5
+            # norm of these 13860 values, ~1.2e8, is inf in fp16 on both sides)
+            want = torch.linalg.vector_norm(x.float(), ord_, dim, keepdim).half().float()
+            assert got.dtype == torch.float16 and got.shape == want.shape, (ord_, dim)
+            torch.testing.assert_close(got.cpu().float(), want, rtol=2e-3, atol=1e-3,
+                                       msg=f"ord={ord_} dim={dim}")
+    got = torch.linalg.vector_norm(xd, 2, -1, dtype=torch.float32)
+    assert got.dtype == torch.float32
+    torch.testing.assert_close(got.cpu(), torch.linalg.vector_norm(x.float(), 2, -1),
+                               rtol=1e-5, atol=1e-5)
+    _cmp(torch.norm(xd, dim=-1), torch.norm(x.float(), dim=-1).half())
+    _cmp(torch.nn.functional.normalize(xd, dim=-1),
+         torch.nn.functional.normalize(x.float(), dim=-1).half())
+
+
+def test_dropout_backward_and_nearest_upsample_exact():
+    """native_dropout_backward (Metadata.yaml:93) and upsample_nearest2d
+    (Metadata.yaml:331) against torch's CPU ops: both are exact (a 0 / 1
+    mask and one rounded scale; gathers), so the bits must match."""
+    _log("native_dropout_backward, upsample_nearest2d")
+    g = randn((4, 37, 50), k=12)
+    mask = torch.rand(4, 37, 50, generator=torch.Generator().manual_seed(13)) > 0.3
+    scale = 1.0 / (1.0 - 0.3)
+    got = torch.ops.aten.native_dropout_backward(g.to(DEV), mask.to(DEV), scale)
+    assert torch.equal(got.cpu(), torch.ops.aten.native_dropout_backward(g, mask, scale))
+    x = randn((2, 3, 7, 5), k=14)
+    xd = x.to(DEV)
+    F = torch.nn.functional
+    for kw in (dict(size=(14, 10)), dict(size=(7, 5)), dict(size=(11, 13)), dict(size=(3, 2)),
+               dict(scale_factor=2.5), dict(scale_factor=(1.5, 0.6))):
+        got = F.interpolate(xd, mode="nearest", **kw)
+        want = F.interpolate(x.float(), mode="nearest", **kw).half()
+        assert got.shape == want.shape and torch.equal(got.cpu(), want), kw
+
+
 def test_embedding_cat_stack():
     _log("embedding/cat/stack")
     table = randn((1000, 64), k=1)

@@ -12,6 +12,7 @@
 #include <ATen/native/Resize.h>
 #include <torch/library.h>
 
+#include <algorithm>
 #include <cmath>
 #include <limits>
 #include <mutex>
@@ -328,6 +329,59 @@ at::Tensor& random_to_(at::Tensor& self, int64_t to, std::optional<at::Generator
   return random_from_(self, 0, to, gen);
 }
 
+// native_dropout_backward (reference: codegen/inputs/Metadata.yaml:93):
+// grad * mask * scale, evaluated left to right in grad's dtype as torch's
+// CPU kernel does.
+at::Tensor native_dropout_backward(const at::Tensor& grad, const at::Tensor& mask,
+                                   double scale) {
+  TORCH_CHECK(grad.sizes() == mask.sizes(), "spyre: dropout backward: grad ", grad.sizes(),
+              " and mask ", mask.sizes(), " differ in shape");
+  return grad.mul(mask.to(grad.scalar_type())).mul_(scale);
+}
+
+// upsample_nearest2d (reference: codegen/inputs/Metadata.yaml:331): two
+// row gathers (index_select over H, then over W) with torch's nearest
+// index: the identity when the size is unchanged, o >> 1 when doubled,
+// else min(floor(o * s), in - 1) with s = 1 / scale (a given scale > 0)
+// or in / out in float.
+std::vector<int64_t> nearest_indices(int64_t in, int64_t out, std::optional<double> scale) {
+  std::vector<int64_t> idx(static_cast<size_t>(out));
+  const float s = (scale.has_value() && *scale > 0.0) ? static_cast<float>(1.0 / *scale)
+                                                      : static_cast<float>(in) / out;
+  for (int64_t o = 0; o < out; ++o) {
+    if (out == in) idx[o] = o;
+    else if (out == 2 * in) idx[o] = o >> 1;
+    else idx[o] = std::min(static_cast<int64_t>(std::floor(o * s)), in - 1);
+  }
+  return idx;
+}
+
+at::Tensor& upsample_nearest2d_out(const at::Tensor& self, c10::SymIntArrayRef output_size,
+                                   std::optional<double> scales_h,
+                                   std::optional<double> scales_w, at::Tensor& out) {
+  const auto os = c10::asIntArrayRefUnchecked(output_size);
+  TORCH_CHECK(os.size() == 2, "spyre: upsample_nearest2d expects two output sizes");
+  TORCH_CHECK(self.dim() == 4, "spyre: upsample_nearest2d expects a 4-D input, got ",
+              self.dim(), " dims");
+  const int64_t ih = self.size(2), iw = self.size(3), oh = os[0], ow = os[1];
+  TORCH_CHECK(ih > 0 && iw > 0 && oh > 0 && ow > 0,
+              "spyre: upsample_nearest2d: input and output sizes must be positive");
+  auto dev = [&](const std::vector<int64_t>& v) {
+    return at::tensor(v, at::TensorOptions().dtype(at::kLong)).to(self.device());
+  };
+  at::Tensor y = self.index_select(2, dev(nearest_indices(ih, oh, scales_h)))
+                     .index_select(3, dev(nearest_indices(iw, ow, scales_w)));
+  at::native::resize_output(out, y.sizes());
+  out.copy_(y);
+  return out;
+}
+
+at::Tensor upsample_nearest2d(const at::Tensor& self, c10::SymIntArrayRef output_size,
+                              std::optional<double> scales_h, std::optional<double> scales_w) {
+  at::Tensor out = empty_spyre({0}, self.scalar_type(), self.device());
+  return upsample_nearest2d_out(self, output_size, scales_h, scales_w, out);
+}
+
 }  // namespace
 
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
@@ -337,6 +391,9 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("index_select", TORCH_FN(index_select));
   m.impl("index_select.out", TORCH_FN(index_select_out));
   m.impl("native_dropout", TORCH_FN(native_dropout));
+  m.impl("native_dropout_backward", TORCH_FN(native_dropout_backward));
+  m.impl("upsample_nearest2d", TORCH_FN(upsample_nearest2d));
+  m.impl("upsample_nearest2d.out", TORCH_FN(upsample_nearest2d_out));
   m.impl("arange.start_out", TORCH_FN(arange_out));
   m.impl("cumsum.out", TORCH_FN(cumsum_out));
   m.impl("cumsum", TORCH_FN(cumsum));

@@ -294,9 +294,62 @@ at::Tensor rms_norm(const at::Tensor& input, c10::SymIntArrayRef normalized_shap
       fused_rms_norm(input, c10::asIntArrayRefUnchecked(normalized_shape), weight, eps));
 }
 
+// ---------------------------------------------------------------------------
+// Vector norm (reference: linalg_vector_norm, a base-template op of
+// codegen/inputs/Metadata.yaml:139): |x| reduced in fp32 by the device
+// reductions - ord 2 as the square root of one sum-of-squares reduction,
+// ord 1 a sum of |x|, +-inf a max / min of |x|, 0 the count of non-zeros,
+// any other ord (sum |x|^ord)^(1/ord) - then cast to the result dtype.
+// ---------------------------------------------------------------------------
+at::Tensor& linalg_vector_norm_out(const at::Tensor& self, const at::Scalar& ord,
+                                   at::OptionalIntArrayRef dim, bool keepdim,
+                                   std::optional<at::ScalarType> dtype, at::Tensor& out) {
+  TORCH_CHECK(at::isFloatingType(self.scalar_type()),
+              "spyre: linalg.vector_norm expects a floating-point input, got ",
+              self.scalar_type());
+  const double p = ord.toDouble();
+  const auto dims = dim.value_or(at::IntArrayRef{});
+  const auto shape = reduced_shape(self, dims, keepdim);
+  at::native::resize_output(out, shape);
+  if (self.numel() == 0) {
+    TORCH_CHECK(p >= 0.0 && !std::isinf(p),
+                "linalg.vector_norm cannot compute the ", ord, " norm on an empty tensor "
+                "because the operation does not have an identity");
+  }
+  at::Tensor acc = empty_spyre(shape, at::kFloat, self.device());
+  c10::DeviceGuard guard(self.device());
+  if (p == 2.0) {
+    reduce_into(SPH_RED_SUMSQ, self, dims, keepdim, acc);
+    acc.sqrt_();
+  } else if (p == 0.0) {
+    reduce_into(SPH_RED_SUM, self.ne(0).to(at::kFloat), dims, keepdim, acc);
+  } else if (std::isinf(p)) {
+    reduce_into(p > 0 ? SPH_RED_MAX : SPH_RED_MIN, self.abs().to(at::kFloat), dims, keepdim,
+                acc);
+  } else if (p == 1.0) {
+    reduce_into(SPH_RED_SUM, self.abs().to(at::kFloat), dims, keepdim, acc);
+  } else {
+    reduce_into(SPH_RED_SUM, self.abs().to(at::kFloat).pow(p), dims, keepdim, acc);
+    acc.pow_(1.0 / p);
+  }
+  out.copy_(acc);
+  return out;
+}
+
+at::Tensor linalg_vector_norm(const at::Tensor& self, const at::Scalar& ord,
+                              at::OptionalIntArrayRef dim, bool keepdim,
+                              std::optional<at::ScalarType> dtype) {
+  const at::ScalarType odt = dtype.value_or(self.scalar_type());
+  at::Tensor out = empty_spyre({0}, odt, self.device());
+  linalg_vector_norm_out(self, ord, dim, keepdim, dtype, out);
+  return out;
+}
+
 }  // namespace
 
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
+  m.impl("linalg_vector_norm", TORCH_FN(linalg_vector_norm));
+  m.impl("linalg_vector_norm.out", TORCH_FN(linalg_vector_norm_out));
   m.impl("sum.IntList_out", TORCH_FN(sum_out));
   m.impl("mean.out", TORCH_FN(mean_out));
   m.impl("amax.out", TORCH_FN(minmax_out<SPH_RED_MAX>));
