@@ -78,6 +78,9 @@ def test_softmax_is_one_three_phase_kernel(fake_device):
     assert code.count("block_reduce<spy::MaxF") == 1 and code.count("block_reduce<spy::SumF") == 1
     assert code.count("for (int64_t r0_cnt") == 3
     assert "extent=2097152" in code  # 512*4096 elements bound both arguments
+    # each generated kernel carries a name of its own (kind + source hash)
+    sym = re.search(r"symbol='(spyre_red_[0-9a-f]{10})'", code).group(1)
+    assert f") {sym}(" in code
 
 
 def test_layernorm_gelu_rmsnorm_fuse(fake_device):

@@ -41,11 +41,15 @@ class KernelSpec:
     args: list[TensorArg]        # kernel parameter order
     grid: int
     block: int
-    source: str                  # HIP C++ of the kernel `spyre_kernel`
+    source: str                  # HIP C++ of the kernel `symbol`
     op_info: dict = dataclasses.field(default_factory=dict)
     # the kernel takes the device error word as a last parameter (indirect
     # indexing: out-of-range indices are reported there, see launch_kernel)
     error_word: bool = False
+    # the kernel's extern "C" name; generated kernels are named for their
+    # kind and a hash of their source (spyre_pw_<hash> / spyre_red_<hash>),
+    # so each shows up under its own name in a profiler's kernel trace
+    symbol: str = "spyre_kernel"
 
 
 @dataclasses.dataclass

@@ -13,7 +13,7 @@ from typing import Optional
 
 from . import KernelSpec
 
-# the generated kernel's symbol (spyre_kernel.py emits `spyre_kernel`)
+# the symbol of a kernel whose KernelSpec names none
 KERNEL_SYMBOL = "spyre_kernel"
 
 
@@ -25,7 +25,7 @@ def launch_description(spec: KernelSpec) -> str:
     """The `.launch` line torch_spyre._C.launch_kernel(path, args) reads:
     "<kernel name> <grid> <block> <n> <extent>*n <error word>"."""
     ext = launch_extents(spec)
-    return " ".join([KERNEL_SYMBOL, str(spec.grid), str(spec.block), str(len(ext)),
+    return " ".join([spec.symbol or KERNEL_SYMBOL, str(spec.grid), str(spec.block), str(len(ext)),
                      *map(str, ext), str(int(spec.error_word))]) + "\n"
 
 
@@ -53,7 +53,7 @@ class SpyreHipKernelRunner:
         self.path = path
         # extents[i] bounds argument i (-1 = not checked)
         self.extents = launch_extents(spec)
-        self.handle = _C.load_kernel(code_object, KERNEL_SYMBOL, spec.grid, spec.block,
+        self.handle = _C.load_kernel(code_object, spec.symbol or KERNEL_SYMBOL, spec.grid, spec.block,
                                      self.extents, spec.error_word)
 
     def run(self, *args, **kwargs):

@@ -20,6 +20,7 @@ sizes raise Unsupported.
 
 from __future__ import annotations
 
+import hashlib
 import itertools
 import math
 import re
@@ -1096,6 +1097,11 @@ class SpyreKernel(SIMDKernel):
         src = code.getvalue()
         if grid <= 0 or grid >= 2**31:
             raise Unsupported(f"grid {grid}")
+        # a name of its own per kernel (kind + source hash), so profiles tell
+        # generated kernels apart
+        symbol = (f"spyre_{'red' if is_red else 'pw'}_"
+                  f"{hashlib.sha1(src.encode()).hexdigest()[:10]}")
+        src = src.replace(") spyre_kernel(\n", f") {symbol}(\n", 1)
         spec = IndentedBuffer()
         spec.writeline("KernelSpec(")
         with spec.indent():
@@ -1111,6 +1117,7 @@ class SpyreKernel(SIMDKernel):
                     spec.writeline(a + ",")
             spec.writeline("],")
             spec.writeline(f"source={src!r},")
+            spec.writeline(f"symbol={symbol!r},")
         spec.writeline(")")
         return spec.getvalue()
 
