@@ -437,6 +437,36 @@ def test_dropout_backward_and_nearest_upsample_exact():
         assert got.shape == want.shape and torch.equal(got.cpu(), want), kw
 
 
+def test_advanced_indexing_vs_cpu():
+    """aten::index.Tensor (reference codegen/inputs/Metadata.yaml:158, the
+    `index` Gather) against torch CPU: one index tensor, negative indices,
+    several broadcast index tensors on adjacent and non-adjacent dims, a
+    boolean mask, an empty index; out-of-range indices raise IndexError.
+    Gathers are exact."""
+    _log("advanced indexing")
+    x = randn((6, 7, 5, 4), k=15)
+    xd = x.to(DEV)
+    i0 = torch.tensor([5, 0, -1, 2])
+    i1 = torch.tensor([[1], [6], [-7]])
+    cases = [
+        lambda t, dev: t[i0.to(dev)],
+        lambda t, dev: t[:, i1.to(dev)],
+        lambda t, dev: t[i0.to(dev)[:3, None], i1.to(dev)[:, 0]],
+        lambda t, dev: t[:, i1.to(dev)[:, 0], :, torch.tensor([3, 0, 1]).to(dev)],
+        lambda t, dev: t[i0.to(dev), :, torch.tensor([4, 0, 1, 2]).to(dev)],
+        lambda t, dev: t[(t[:, :, 0, 0] > 0).to(dev)],
+        lambda t, dev: t[torch.tensor([], dtype=torch.long).to(dev)],
+    ]
+    for n, fn in enumerate(cases):
+        want = fn(x, "cpu")
+        got = fn(xd, DEV)
+        assert got.shape == want.shape and torch.equal(got.cpu(), want), n
+    with pytest.raises(IndexError):
+        xd[torch.tensor([0, 6]).to(DEV)]
+    with pytest.raises(IndexError):
+        xd[:, torch.tensor([-8]).to(DEV)]
+
+
 def test_embedding_cat_stack():
     _log("embedding/cat/stack")
     table = randn((1000, 64), k=1)

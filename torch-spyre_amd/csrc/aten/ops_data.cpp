@@ -329,6 +329,103 @@ at::Tensor& random_to_(at::Tensor& self, int64_t to, std::optional<at::Generator
   return random_from_(self, 0, to, gen);
 }
 
+// Advanced indexing, self[indices] (reference: the `index` Gather of
+// codegen/inputs/Metadata.yaml:158).  Boolean masks become the long
+// indices of their true elements; negative indices wrap; an index outside
+// its dimension raises IndexError.  The index tensors broadcast to one shape
+// B; the indexed dimensions (moved to the front when they are not adjacent,
+// as torch orders the result) are flattened into one, whose flat index
+// sum_k idx_k * prod(later indexed sizes) is gathered with one
+// index_select: result = sizes before + B + sizes after.
+at::Tensor index_tensor(const at::Tensor& self,
+                        const c10::List<std::optional<at::Tensor>>& indices) {
+  TORCH_CHECK(static_cast<int64_t>(indices.size()) <= self.dim(),
+              "too many indices for tensor of dimension ", self.dim(), " (got ",
+              indices.size(), ")");
+  std::vector<int64_t> dims;
+  std::vector<at::Tensor> idx;
+  int64_t d = 0;
+  for (size_t i = 0; i < indices.size(); ++i) {
+    const std::optional<at::Tensor> o = indices.get(i);
+    if (!o.has_value() || !o->defined()) {
+      ++d;
+      continue;
+    }
+    const at::Tensor& t = *o;
+    if (t.scalar_type() == at::kBool || t.scalar_type() == at::kByte) {
+      // a mask over the next t.dim() dimensions: the coordinates of its
+      // true elements, found on the host (their count sets the shape)
+      for (int64_t k = 0; k < t.dim(); ++k)
+        TORCH_CHECK_INDEX(d + k < self.dim() && t.size(k) == self.size(d + k),
+                          "The shape of the mask ", t.sizes(), " at index ", k,
+                          " does not match the shape of the indexed tensor ", self.sizes());
+      const at::Tensor nz = t.cpu().to(at::kBool).nonzero();  // [count, t.dim()]
+      for (int64_t k = 0; k < t.dim(); ++k) {
+        dims.push_back(d + k);
+        idx.push_back(nz.select(1, k).contiguous().to(self.device()));
+      }
+      d += t.dim();
+    } else {
+      TORCH_CHECK_INDEX(at::isIntegralType(t.scalar_type(), false),
+                        "tensors used as indices must be long, int, byte or bool tensors");
+      dims.push_back(d);
+      idx.push_back(t.to(self.device(), at::kLong));
+      ++d;
+    }
+  }
+  TORCH_CHECK(!dims.empty(), "spyre: index with no index tensor");
+  TORCH_CHECK(d <= self.dim(), "too many indices for tensor of dimension ", self.dim());
+  // broadcast shape of the index tensors
+  std::vector<at::Tensor> bt = at::broadcast_tensors(idx);
+  const auto bshape = bt[0].sizes().vec();
+  bool adjacent = true;
+  for (size_t k = 1; k < dims.size(); ++k) adjacent = adjacent && dims[k] == dims[k - 1] + 1;
+  // self with the indexed dims together (in order) starting at `first`
+  at::Tensor x = self;
+  int64_t first = dims[0];
+  if (!adjacent) {
+    std::vector<int64_t> perm(dims.begin(), dims.end());
+    for (int64_t k = 0; k < self.dim(); ++k)
+      if (std::find(dims.begin(), dims.end(), k) == dims.end()) perm.push_back(k);
+    x = self.permute(perm);
+    first = 0;
+  }
+  const int64_t nk = static_cast<int64_t>(dims.size());
+  // flat index over the indexed block, each index wrapped and checked
+  at::Tensor flat;
+  int64_t span = 1;
+  for (int64_t k = nk - 1; k >= 0; --k) {
+    const int64_t size = x.size(first + k);
+    at::Tensor ik = bt[k];
+    if (ik.numel() > 0) {
+      const int64_t lo = ik.amin().item<int64_t>(), hi = ik.amax().item<int64_t>();
+      TORCH_CHECK_INDEX(lo >= -size && hi < size, "index ", lo < -size ? lo : hi,
+                        " is out of bounds for dimension ", dims[k], " with size ", size);
+      if (lo < 0) ik = at::where(ik.lt(0), ik.add(size), ik);
+    }
+    at::Tensor term = span == 1 ? ik : ik.mul(span);
+    flat = flat.defined() ? flat.add(term) : term;
+    span *= size;
+  }
+  std::vector<int64_t> xs(x.sizes().begin(), x.sizes().begin() + first);
+  xs.push_back(span);
+  xs.insert(xs.end(), x.sizes().begin() + first + nk, x.sizes().end());
+  at::Tensor g = x.reshape(xs).index_select(first, flat.reshape({-1}));
+  std::vector<int64_t> rs(x.sizes().begin(), x.sizes().begin() + first);
+  rs.insert(rs.end(), bshape.begin(), bshape.end());
+  rs.insert(rs.end(), x.sizes().begin() + first + nk, x.sizes().end());
+  return g.reshape(rs);
+}
+
+at::Tensor& index_tensor_out(const at::Tensor& self,
+                             const c10::List<std::optional<at::Tensor>>& indices,
+                             at::Tensor& out) {
+  at::Tensor r = index_tensor(self, indices);
+  at::native::resize_output(out, r.sizes());
+  out.copy_(r);
+  return out;
+}
+
 // native_dropout_backward (reference: codegen/inputs/Metadata.yaml:93):
 // grad * mask * scale, evaluated left to right in grad's dtype as torch's
 // CPU kernel does.
@@ -388,6 +485,8 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("cat.out", TORCH_FN(cat_out));
   m.impl("tril.out", TORCH_FN(tri_out<0>));
   m.impl("triu.out", TORCH_FN(tri_out<1>));
+  m.impl("index.Tensor", TORCH_FN(index_tensor));
+  m.impl("index.Tensor_out", TORCH_FN(index_tensor_out));
   m.impl("index_select", TORCH_FN(index_select));
   m.impl("index_select.out", TORCH_FN(index_select_out));
   m.impl("native_dropout", TORCH_FN(native_dropout));
