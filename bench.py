@@ -107,7 +107,7 @@ def graph_us(launch, reps, per_graph=20):
 # traffic until it is measured again.
 TIMED_SYMBOLS = {
     "gemm": "_ZN3sph12_GLOBAL__N_114gemm_dl_kernelIDF16_Lb0ELi256ELb0ELi64EEEvNS0_8GemmArgsE",
-    "bmm": "_ZN3sph12_GLOBAL__N_118gemm_shortk_kernelIDF16_Lb0ELi2EEEvNS0_8GemmArgsE",
+    "bmm": "_ZN3sph12_GLOBAL__N_123gemm_shortk_ring_kernelIDF16_Lb0ELi2ELi2ELi2EEEvNS0_8GemmArgsE",
     "softmax": "_ZN3sph12_GLOBAL__N_112softmax_fullIDF16_DF16_Li128ELi4EEEvPKT_lPT0_llfill",
     "rmsnorm": "_ZN3sph12_GLOBAL__N_19norm_regsIDF16_DF16_Li256ELi2ELb1ELb0EEEvPKT_S4_PKT0_S7_PS2_"
                "S8_PfS9_llf",

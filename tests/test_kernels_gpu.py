@@ -354,11 +354,18 @@ def test_gemm_whole_tile_direct_load(m, n, k, tb, pad, dtype):
 
 @pytest.mark.parametrize("batch,m,n,k,tb,pad", [(1, 128, 128, 64, False, 0), (2, 256, 384, 64, True, 8),
                                                 (3, 384, 128, 128, False, 64), (4, 128, 256, 128, True, 0),
-                                                (32, 2048, 2048, 128, True, 0)])
+                                                (32, 2048, 2048, 128, True, 0),
+                                                (9, 768, 1280, 128, False, 64),
+                                                (40, 1664, 256, 64, True, 8),
+                                                (24, 512, 768, 64, True, 8),
+                                                (12, 1024, 2048, 64, False, 0)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_gemm_short_k(batch, m, n, k, tb, pad, dtype):
     # K = 64 / 128 on whole 128x128 tiles: the short-K kernel (attention
-    # scores), batched, both B layouts, padded leading dimensions
+    # scores), batched, both B layouts, padded leading dimensions.  From 512
+    # tiles up the persistent ring kernel runs: runs of 2-6 tiles that start
+    # and end inside tile rows (540 / 576 / 1536 tiles), 2-tile rows that
+    # switch A panels every other tile (1040 tiles).
     _log(f"gemm short-K b={batch} {m}x{n}x{k} tb={tb} pad={pad} {dtype}")
     A = uniform((batch, m, k), k=31, dtype=dtype)
     B = uniform((batch, k, n), k=32, dtype=dtype)

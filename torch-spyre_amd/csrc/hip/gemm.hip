@@ -73,6 +73,8 @@ struct GemmArgs {
   // them from the same loads.
   const void* norm_w;
   float norm_eps;
+  // Batch entries (persistent kernels, whose grid does not carry them).
+  int64_t batches;
 };
 
 template <typename T>
@@ -1097,6 +1099,254 @@ __global__ void __launch_bounds__(sk::NT) gemm_shortk_kernel(const GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Short-K products over many tiles (the attention scores of a whole batch):
+// a persistent form of the kernel above, one workgroup of 4 waves (64x64
+// each) per CU, walking a contiguous run of the (batch entry, tile row,
+// tile column) sequence of 128x128 tiles.
+//   * The A row panel of the current (batch entry, tile row) stays in LDS
+//     while the workgroup walks that row's tile columns, so a tile streams
+//     only its B block: half the operand bytes of the one-shot kernel.
+//   * B blocks go through a three-stage LDS ring: while tile i computes,
+//     tiles i+1 and i+2 are in flight (issued one and two tiles earlier).
+//   * Results leave through a per-wave 32 x 64 slab (two halves per tile)
+//     as streaming 16-byte stores of whole 128-byte rows that the loop never
+//     waits for: vector memory counts return in issue order, so waiting for
+//     an older block's DMA leaves the stores issued after it in flight.
+//   * Consecutive workgroups of one XCD (dispatch is round-robin over the 8
+//     XCDs) take consecutive runs, so one batch entry's B panel is fetched
+//     into one XCD's L2 and re-read from there by its tile rows.
+//   * The tile position advances by a cursor (no 64-bit divisions in the
+//     loop) and each tile's first MFMAs take a zero accumulator operand.
+// A new A panel (a run crossing into the next tile row) is loaded after
+// every wave has finished the previous tile: one exposed load per switch,
+// at most a few per workgroup.
+// Measured on MI355X (attention-score shape 32 x 2048 x 2048 from K = 128,
+// alternating on one box): 67.5-70 us against 79-81 for the one-shot
+// kernel.  Not kept: 8 waves of 64x32 (64-byte row stores) 93-95 us; 8
+// waves of 32x64, 69.6; 256-row tiles on 8 waves with a two-stage ring,
+// 76.5 against 74.3 on a slower box; the same kernel with 64-bit tile
+// divisions and zeroed accumulators, 75.
+// ---------------------------------------------------------------------------
+namespace skr {
+constexpr int NSTG = 3;                               // B stages
+// Wave layout WM x WN over the 128x128 tile.
+template <int WM_, int WN_>
+struct L {
+  static constexpr int WM = WM_, WN = WN_, NW = WM * WN, NT = NW * 64;
+  static constexpr int WTM = sk::BM / WM, WTN = sk::BN / WN, TM = WTM / 32, TN = WTN / 32;
+  static constexpr int CPR = WTN * 2 / 16;            // 16-byte chunks per slab row
+  static constexpr int RPS = 1024 / (WTN * 2);        // slab rows per 16-byte store instruction
+  static constexpr int SLAB = 32 * WTN * 2;           // per-wave slab: 32 rows of the wave tile
+  static constexpr int STORES = TM * 32 / RPS;        // stores per wave per tile
+  static constexpr int LPW = sk::A_BLK / 1024 / NW;   // DMA lines per wave per 64-deep block
+  static_assert(LPW * NW * 1024 == sk::A_BLK && (CPR & (CPR - 1)) == 0, "wave layout");
+  // slab row m, chunk c -> 16-byte slot
+  __device__ static int sslot(int m, int c) { return m * CPR + (c ^ ((m >> 1) & (CPR - 1))); }
+};
+// Position (batch entry, tile row, tile column) in the tile sequence.
+struct Cursor {
+  int b, tm, tn;
+  __device__ void next(int tiles_m, int tiles_n) {
+    if (++tn == tiles_n) {
+      tn = 0;
+      if (++tm == tiles_m) tm = 0, ++b;
+    }
+  }
+};
+}  // namespace skr
+
+template <typename T, bool B_KCONT, int KT, int WM_, int WN_>
+__global__ void __launch_bounds__((skr::L<WM_, WN_>::NT)) gemm_shortk_ring_kernel(const GemmArgs p) {
+  using sk::A_BLK;
+  using sk::B_BLK;
+  using sk::BM;
+  using sk::BN;
+  using sk::KB;
+  using sk::aslot;
+  using skr::Cursor;
+  using skr::NSTG;
+  using W = skr::L<WM_, WN_>;
+  constexpr int WN = W::WN, WTM = W::WTM, WTN = W::WTN, TM = W::TM, TN = W::TN;
+  constexpr int NW = W::NW, LPW = W::LPW, STORES = W::STORES, CPR = W::CPR, RPS = W::RPS;
+  constexpr int A_PANEL = KT * A_BLK, B_TILE = KT * B_BLK;
+  constexpr int LB = KT * LPW;                     // DMA lines per wave per B block (= per A panel)
+  constexpr int SLAB_OFF = A_PANEL + NSTG * B_TILE;
+  __shared__ __attribute__((aligned(1024))) char lds[SLAB_OFF + NW * W::SLAB];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int lda = static_cast<int>(p.lda), ldb = static_cast<int>(p.ldb);
+  const int tiles_m = p.tiles_m, tiles_n = p.tiles_n;
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((SPH_LDS char*)(lds)));
+
+  // This workgroup's run [t0, t0 + n) of the tile sequence.
+  const int64_t total = p.batches * tiles_m * tiles_n;
+  const int G = static_cast<int>(gridDim.x);
+  int slot = static_cast<int>(blockIdx.x);
+  if ((G & 7) == 0) slot = (slot & 7) * (G >> 3) + (slot >> 3);
+  const int64_t t0 = total * slot / G;
+  const int n = static_cast<int>(total * (slot + 1) / G - t0);
+  if (n <= 0) return;
+  Cursor cur;  // tile i
+  {
+    const int64_t u = t0 / tiles_n;
+    cur.tn = static_cast<int>(t0 - u * tiles_n);
+    cur.b = static_cast<int>(u / tiles_m);
+    cur.tm = static_cast<int>(u - static_cast<int64_t>(cur.b) * tiles_m);
+  }
+
+  // Per-lane byte offsets of this wave's DMA lines within a 64-deep K block.
+  uint32_t va[LPW], vb[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int s = (wave * LPW + i) * 64 + lane;
+    const int r = s >> 3, c = (s & 7) ^ ((r >> 1) & 7);
+    va[i] = static_cast<uint32_t>(r * lda * 2 + c * 16);
+    if constexpr (B_KCONT) {
+      vb[i] = static_cast<uint32_t>(r * ldb * 2 + c * 16);
+    } else {
+      const int k = s >> 4, cb = (s & 15) ^ (4 * (k & 3));
+      vb[i] = static_cast<uint32_t>(k * ldb * 2 + cb * 16);
+    }
+  }
+  const uint16_t* const A0 = static_cast<const uint16_t*>(p.a);
+  const uint16_t* const B0 = static_cast<const uint16_t*>(p.b);
+  // A row panel of the cursor's (batch entry, tile row) into the panel slot.
+  auto dma_a = [&](const Cursor& c) {
+    const i32x4 ra = buffer_rsrc(A0 + c.b * p.stride_a + static_cast<int64_t>(c.tm) * BM * p.lda,
+                                 static_cast<uint32_t>(((BM - 1) * static_cast<int64_t>(lda) + p.k) * 2));
+#pragma unroll
+    for (int kb = 0; kb < KT; ++kb)
+#pragma unroll
+      for (int i = 0; i < LPW; ++i)
+        dma16(ra, __builtin_amdgcn_readfirstlane(lds_base + kb * A_BLK + (wave * LPW + i) * 1024), va[i],
+              __builtin_amdgcn_readfirstlane(kb * KB * 2));
+  };
+  // B block of the cursor's tile into ring stage st.
+  auto dma_b = [&](const Cursor& c, int st) {
+    const uint16_t* B = B0 + c.b * p.stride_b;
+    const i32x4 rb = B_KCONT
+        ? buffer_rsrc(B + static_cast<int64_t>(c.tn) * BN * p.ldb,
+                      static_cast<uint32_t>(((BN - 1) * static_cast<int64_t>(ldb) + p.k) * 2))
+        : buffer_rsrc(B + static_cast<int64_t>(c.tn) * BN, static_cast<uint32_t>(((p.k - 1) * ldb + BN) * 2));
+#pragma unroll
+    for (int kb = 0; kb < KT; ++kb)
+#pragma unroll
+      for (int i = 0; i < LPW; ++i)
+        dma16(rb,
+              __builtin_amdgcn_readfirstlane(lds_base + A_PANEL + st * B_TILE + kb * B_BLK +
+                                             (wave * LPW + i) * 1024),
+              vb[i], __builtin_amdgcn_readfirstlane(B_KCONT ? kb * KB * 2 : kb * KB * ldb * 2));
+  };
+
+  Cursor ahead = cur;  // tile i + 2 once the loop runs
+  dma_a(cur);
+  dma_b(ahead, 0);
+  ahead.next(tiles_m, tiles_n);
+  if (n > 1) dma_b(ahead, 1);
+  ahead.next(tiles_m, tiles_n);
+
+  const int row_in = lane & 31, khalf = lane >> 5;
+  const int g = lane >> 4, jj = lane & 15, e = jj >> 2, q = jj & 3;
+  char* const slab = lds + SLAB_OFF + wave * W::SLAB;
+  T* const D0 = static_cast<T*>(p.d);
+  bool reloaded = false;  // the previous tile loaded a new A panel
+  for (int i = 0; i < n; ++i) {
+    const bool sw = i > 0 && cur.tn == 0;  // tile i starts a new tile row
+    // B block i (and everything issued before it) has landed.  Issued
+    // after it: the stores of tiles i-2 and i-1, B block i+1 unless i is
+    // the last tile, and an A panel if tile i-1 switched rows; waiting for
+    // fewer than that many waits longer, never shorter.
+    if (i == 0) {
+      wait_vmcnt<0>();
+    } else if (i == 1) {
+      wait_vmcnt<STORES>();
+    } else if (!reloaded && i + 1 < n) {
+      wait_vmcnt<2 * STORES + LB>();
+    } else {
+      wait_vmcnt<2 * STORES>();
+    }
+    // Past this barrier every wave is done with tile i-1: its ring stage
+    // and, on a row switch, the A panel may be refilled.
+    __syncthreads();
+    if (sw) dma_a(cur);
+    if (i + 2 < n) {
+      dma_b(ahead, (i + 2) % NSTG);
+      ahead.next(tiles_m, tiles_n);
+    }
+    if (sw) {
+      if (i + 2 < n) wait_vmcnt<LB>();
+      else wait_vmcnt<0>();
+      __syncthreads();
+    }
+    reloaded = sw;
+
+    const char* sb = lds + A_PANEL + (i % NSTG) * B_TILE;
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int kb = 0; kb < KT; ++kb) {
+      const char* sa = lds + kb * A_BLK;
+      const char* sbk = sb + kb * B_BLK;
+#pragma unroll
+      for (int kk = 0; kk < KB / 16; ++kk) {
+        u32x4 af[TM], bf[TN];
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+          af[a] = *reinterpret_cast<const u32x4*>(sa + aslot(wm * WTM + a * 32 + row_in, kk * 2 + khalf) * 16);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          if constexpr (B_KCONT) {
+            bf[j] = *reinterpret_cast<const u32x4*>(sbk + aslot(wn * WTN + j * 32 + row_in, kk * 2 + khalf) * 16);
+          } else {
+            const int nn = wn * WTN + j * 32 + 16 * (g & 1) + 4 * q;
+            const int k = kk * 16 + 8 * (g >> 1) + e;
+            const SPH_LDS char* p0 =
+                (const SPH_LDS char*)(sbk) + k * (BN * 2) + (((nn >> 3) ^ (4 * e)) << 4) + 8 * (q & 1);
+            const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((SPH_LDS s16x4*)(p0)));
+            const u32x2 hi = __builtin_bit_cast(
+                u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((SPH_LDS s16x4*)(p0 + 4 * BN * 2)));
+            bf[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3);
+          }
+        }
+        // (the first sub-step starts from a zero accumulator operand)
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[a][j] = mfma32<T>(bf[j], af[a], kb == 0 && kk == 0 ? f32x16{} : acc[a][j]);
+      }
+    }
+    // acc[a][j][r]: row a*32 + lane%32, column j*32 + 8*(r/4) + 4*(lane/32) + r%4.
+    // Each 32-row block goes through the wave's own slab: 8-byte writes,
+    // 16-byte reads of whole slab rows, streaming stores.
+    T* D = D0 + cur.b * p.stride_d + (static_cast<int64_t>(cur.tm) * BM + wm * WTM) * p.ldd +
+           static_cast<int64_t>(cur.tn) * BN + wn * WTN;
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          uint32_t w[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint16_t lo = __builtin_bit_cast(uint16_t, Num<T>::from_f(acc[a][j][4 * rg + 2 * h]));
+            const uint16_t hi = __builtin_bit_cast(uint16_t, Num<T>::from_f(acc[a][j][4 * rg + 2 * h + 1]));
+            w[h] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+          }
+          *reinterpret_cast<u32x2*>(slab + W::sslot(row_in, j * 4 + rg) * 16 + khalf * 8) = u32x2{w[0], w[1]};
+        }
+#pragma unroll
+      for (int it = 0; it < 32 / RPS; ++it) {
+        const int m = it * RPS + lane / CPR, c = lane % CPR;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(slab + W::sslot(m, c) * 16);
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(D + (a * 32 + m) * p.ldd + c * 8));
+      }
+    }
+    cur.next(tiles_m, tiles_n);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Small-M products: D[m, n] = epi(alpha * sum_k A[m, k] * B[n, k] + beta*C)
 // for M <= MT rows, A and B K-contiguous and 16-byte aligned, K % 8 == 0.
 // A group of TPR threads computes R output columns n for all M rows: thread t
@@ -1735,6 +1985,10 @@ int launch_dl(GemmArgs& p, int64_t batch, bool b_kcont, hipStream_t st,
   return check_launch("sph_gemm");
 }
 
+// Short-K problems of at least this many 128x128 tiles run the persistent
+// ring kernel (two or more tiles per workgroup on 256 CUs).
+constexpr int64_t kShortkRingTiles = 2 * kStreamCUs;
+
 // Short-K kernel: K of 64 or 128, whole 128x128 tiles, K-contiguous A,
 // 16-byte aligned rows everywhere, plain product, 32-bit buffer offsets.
 inline bool shortk_fits(const GemmArgs& p, bool a_kcont, bool b_kcont) {
@@ -1785,6 +2039,21 @@ int gemm_dispatch(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
   if (shortk_fits(p, a_kcont, b_kcont)) {
     p.tiles_m = static_cast<int>(p.m / sk::BM);
     p.tiles_n = static_cast<int>(p.n / sk::BN);
+    const int64_t tiles = static_cast<int64_t>(p.tiles_m) * p.tiles_n * batch;
+    if (tiles >= kShortkRingTiles && p.tiles_n >= 2) {
+      // persistent: one workgroup per CU over runs of at least two tiles
+      p.batches = batch;
+      const dim3 grid(static_cast<unsigned>(kStreamCUs));
+      constexpr int RWM = 2, RWN = 2, RNT = skr::L<RWM, RWN>::NT;
+      if (p.k == 64) {
+        if (b_kcont) gemm_shortk_ring_kernel<T, true, 1, RWM, RWN><<<grid, dim3(RNT), 0, st>>>(p);
+        else gemm_shortk_ring_kernel<T, false, 1, RWM, RWN><<<grid, dim3(RNT), 0, st>>>(p);
+      } else {
+        if (b_kcont) gemm_shortk_ring_kernel<T, true, 2, RWM, RWN><<<grid, dim3(RNT), 0, st>>>(p);
+        else gemm_shortk_ring_kernel<T, false, 2, RWM, RWN><<<grid, dim3(RNT), 0, st>>>(p);
+      }
+      return check_launch("sph_gemm (short K)");
+    }
     dim3 grid(static_cast<unsigned>(p.tiles_m) * p.tiles_n, static_cast<unsigned>(batch));
     if (p.k == 64) {
       if (b_kcont) gemm_shortk_kernel<T, true, 1><<<grid, dim3(sk::NT), 0, st>>>(p);
