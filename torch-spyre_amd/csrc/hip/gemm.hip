@@ -1125,7 +1125,8 @@ __global__ void __launch_bounds__(sk::NT) gemm_shortk_kernel(const GemmArgs p) {
 // kernel.  Not kept: 8 waves of 64x32 (64-byte row stores) 93-95 us; 8
 // waves of 32x64, 69.6; 256-row tiles on 8 waves with a two-stage ring,
 // 76.5 against 74.3 on a slower box; the same kernel with 64-bit tile
-// divisions and zeroed accumulators, 75.
+// divisions and zeroed accumulators, 75; tile i-1's slab epilogue and
+// stores spread between tile i's MFMA sub-steps, 73-74 against 69-71.
 // ---------------------------------------------------------------------------
 namespace skr {
 constexpr int NSTG = 3;                               // B stages
