@@ -41,8 +41,12 @@
 //   * A workgroup is 8 waves in two groups of 4 on the same 128 query rows:
 //     group g takes the key blocks kb with kb % 2 == g, each group with its
 //     own two-stage LDS ring, and the two partial softmax states merge
-//     through LDS at the end.  One workgroup fills a CU (two waves per
-//     SIMD), so the grid is longer than the CU count and its order matters:
+//     through LDS at the end.  (Without a mask or causal positions, where
+//     every job is equally long, one group per workgroup: the two groups of
+//     one workgroup meet at every block's barrier, so their MFMA and
+//     softmax phases coincide, while two workgroups on a CU drift apart.)
+//     One 8-wave workgroup fills a CU (two waves per SIMD), so the grid is
+//     longer than the CU count and its order matters:
 //     jobs run longest first (causal positions: by position block; masks:
 //     by the number of key blocks the mask leaves, counted and sorted on the
 //     device from the block classes), so short jobs fill in behind long
@@ -249,13 +253,14 @@ __global__ void __launch_bounds__(1024) attn_order_kernel(const uint8_t* __restr
   for (int jb = threadIdx.x; jb < jobs; jb += 1024) order[atomicAdd(&cnt[work(jb)], 1)] = jb;
 }
 
-template <typename T, bool MASK, bool CAUSAL>
-__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
+template <typename T, bool MASK, bool CAUSAL, int GR>
+__global__ void __launch_bounds__(GR * 256) __attribute__((amdgpu_waves_per_eu(2)))
 attn_fwd_kernel(const AttnArgs p) {
-  __shared__ __attribute__((aligned(1024))) char lds[4 * STAGE];
+  static_assert(GR == 1 || GR == 2, "key-block groups");
+  __shared__ __attribute__((aligned(1024))) char lds[2 * GR * STAGE];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = wave >> 2, wq = wave & 3;  // key-block group, wave within it (its rows)
+  const int grp = GR == 2 ? wave >> 2 : 0, wq = wave & 3;  // key-block group, wave within it (its rows)
   // The job: batch element b, row block rb.
   int64_t b, rb;
   const int64_t wg = blockIdx.x;
@@ -385,9 +390,9 @@ attn_fwd_kernel(const AttnArgs p) {
   // Group g takes key blocks base + 2 it + g, it = 0 .. nit-1 (those in
   // [kb0, kb1)); base is kb0 rounded down to even, so which group a block
   // goes to does not depend on kb0.
-  const int base = kb0 & ~1;
-  const int nit = kb1 > base ? (kb1 - base + 1) / 2 : 0;
-  auto blk_of = [&](int it) { return base + 2 * it + grp; };
+  const int base = GR == 2 ? kb0 & ~1 : kb0;
+  const int nit = kb1 > base ? (kb1 - base + GR - 1) / GR : 0;
+  auto blk_of = [&](int it) { return base + GR * it + grp; };
   auto valid = [&](int kb) { return kb >= kb0 && kb < kb1; };
   auto cls_of = [&](int kb) -> uint8_t {  // (all mixed without the pre-pass)
     return !valid(kb) ? MB_NEGINF : MASK ? (mcls != nullptr ? mcls[kb] : MB_MIXED) : MB_ZERO;
@@ -527,6 +532,7 @@ attn_fwd_kernel(const AttnArgs p) {
     __syncthreads();
     if (it + 2 < nit && valid(blk_of(it + 2))) issue(blk_of(it + 2), slot);
   }
+  if constexpr (GR == 2) {
   // Merge: group 1 hands (m_ref, l, O) to the group-0 lane of the same row
   // through LDS (all DMA has landed: the loop ends with a wait + barrier).
   float* mg = reinterpret_cast<float*>(lds) + wq * (66 * 64) + lane;
@@ -550,6 +556,7 @@ attn_fwd_kernel(const AttnArgs p) {
     for (int dt = 0; dt < AD / 32; ++dt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[dt][r] = o[dt][r] * a0 + mg[(2 + dt * 16 + r) * 64] * a1;
+  }
   }
   // O[qrow][d], d = 32 dt + 8 rg + 4 h + i, normalised by the row sum.
   const float inv = 1.0f / l_run;
@@ -682,12 +689,16 @@ extern "C" int sph_attention_fwd(sph_dtype dtype, int64_t batch, int64_t mq, int
   }
   dim3 grid(static_cast<unsigned>(batch * (mq / AQ)));
   const bool m = mask != nullptr, c = causal_q > 0;
+  // Without a mask or causal positions every job has the same length and
+  // needs no key split: one group of 4 waves per workgroup, two workgroups
+  // per CU (c4's dense shape 79-81 us against 86.5-87 with two groups).
+  constexpr int kDenseGroups = 1;
 #define SPH_ATTN(T_)                                                                     \
   do {                                                                                   \
-    if (m && c) attn_fwd_kernel<T_, true, true><<<grid, 512, 0, st>>>(p);                \
-    else if (m) attn_fwd_kernel<T_, true, false><<<grid, 512, 0, st>>>(p);               \
-    else if (c) attn_fwd_kernel<T_, false, true><<<grid, 512, 0, st>>>(p);               \
-    else attn_fwd_kernel<T_, false, false><<<grid, 512, 0, st>>>(p);                     \
+    if (m && c) attn_fwd_kernel<T_, true, true, 2><<<grid, 512, 0, st>>>(p);             \
+    else if (m) attn_fwd_kernel<T_, true, false, 2><<<grid, 512, 0, st>>>(p);            \
+    else if (c) attn_fwd_kernel<T_, false, true, 2><<<grid, 512, 0, st>>>(p);            \
+    else attn_fwd_kernel<T_, false, false, kDenseGroups><<<grid, kDenseGroups * 256, 0, st>>>(p); \
   } while (0)
   if (dtype == SPH_F16)
     SPH_ATTN(half_t);
