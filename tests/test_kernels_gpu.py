@@ -324,14 +324,16 @@ def test_gemm_bias_alpha_beta_epilogue(epi, name):
                                           (256, 256, 64, True, 8), (512, 768, 128, False, 64),
                                           (2048, 4096, 12800, True, 0), (768, 1024, 4096, False, 0),
                                           (512, 384, 192, False, 0), (256, 128, 64, True, 8),
-                                          (2048, 4096, 512, False, 0), (1024, 640, 256, True, 0)])
+                                          (2048, 4096, 512, False, 0), (1024, 640, 256, True, 0),
+                                          (2048, 8192, 1216, False, 8), (4096, 4096, 64, True, 0),
+                                          (4096, 4096, 4096, False, 0)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_gemm_whole_tile_direct_load(m, n, k, tb, pad, dtype):
     # whole 256-row tiles with K-contiguous A run the direct-to-LDS kernel,
     # 256 or 128 columns wide (n = 384, 128, 640 only fit 128; 2048 x 4096
     # picks 128 for a full round of tiles): odd and even K-tile counts (k/64 =
-    # 1, 2, 3, 5, 8, 64, 200), row-major and K-contiguous B, leading
-    # dimensions wider than the matrix (pad)
+    # 1, 2, 3, 5, 8, 19, 64, 200), row-major and K-contiguous B, leading
+    # dimensions wider than the matrix (pad); c2's 4096^3 through the C-ABI
     _log(f"gemm direct-load {m}x{n}x{k} tb={tb} pad={pad} {dtype}")
     A = uniform((m, k), k=21, dtype=dtype)
     B = uniform((k, n), k=22, dtype=dtype)
