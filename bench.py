@@ -586,6 +586,23 @@ def bench_spyre_paths(steps, warmup):
     sm = torch.compile(lambda a: torch.softmax(a, dim=-1))
     entry("c1_softmax_eager_spyre", 2 * R * C * 2, lambda: torch.softmax(x, -1))
     entry("c1_softmax_compiled_spyre", 2 * R * C * 2, lambda: sm(x))
+    # The same compiled function with its host path taken away: 20 calls
+    # captured in one HIP graph of the spyre stream, replayed (GPU time per
+    # call).  The gap to the entry above is torch.compile's per-call host
+    # path, not the generated kernel.
+    per_graph = 20
+    g = torch.spyre.SpyreGraph()
+    with torch.spyre.graph(g):
+        for _ in range(per_graph):
+            sm(x)
+    ms, _ = timer.run(g.replay, max(steps // 4, 5), 3)
+    us = ms * 1e3 / per_graph
+    gbs = 2 * R * C * 2 / (us * 1e-6) / 1e9
+    out["c1_softmax_compiled_spyre_graph"] = {
+        "us_per_call": round(us, 2), "GB/s": round(gbs, 1),
+        "roofline_frac": round(gbs / PEAK_HBM_GBS, 4),
+        "note": f"{per_graph} compiled calls per HIP graph replay"}
+    g.reset()
     R, C = 8192, 4096
     x = torch.randn(R, C, generator=_gen(0)).half().to("spyre")
     r = torch.randn(R, C, generator=_gen(1)).half().to("spyre")
