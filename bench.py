@@ -226,6 +226,45 @@ def bench_gemm(steps, warmup, stream, capi):
             "precondition_launches": n_pre}
 
 
+def bench_gemm_cold(steps, warmup, stream, capi, sets=8):
+    """GEMMs whose operands come from HBM: `sets` operand sets used in turn
+    (c2 4096^3 A @ B: 8 x 64 MiB of A and B, more than the 256 MiB MALL;
+    c4's QKV projection x W^T, 2048 x 6144 x 4096: 8 x 64 MiB), so a launch
+    finds none of its operands in the caches, as a projection inside a
+    decoder layer does.  HIP events over launches that rotate the sets."""
+    import torch
+
+    lib = capi.lib()
+    s = stream.cuda_stream
+    timer = Timer(stream)
+    out = {}
+    for name, M, N, K, tb in (("c2_mm_4096_cold", 4096, 4096, 4096, 0),
+                              ("c4_qkv_2048x6144x4096_cold", 2048, 6144, 4096, 1)):
+        A = [(torch.rand(M, K, generator=_gen(20 + i)) * 2 - 1).half().cuda() for i in range(sets)]
+        B = [(torch.rand((N, K) if tb else (K, N), generator=_gen(40 + i)) * 2 - 1).half().cuda()
+             for i in range(sets)]
+        D = [torch.empty(M, N, dtype=torch.float16, device="cuda") for _ in range(sets)]
+        ldb = K if tb else N
+        it = [0]
+
+        def step():
+            i = it[0] % sets
+            it[0] += 1
+            rc = lib.sph_gemm(capi.F16, 0, tb, M, N, K, 1.0, A[i].data_ptr(), K, B[i].data_ptr(),
+                              ldb, 0.0, None, 0, 0, D[i].data_ptr(), N, 0, s)
+            if rc:
+                capi.check(rc, "sph_gemm")
+
+        ms, _ = timer.run(step, max(steps, 2 * sets), max(warmup, 4 * sets))
+        flop = 2.0 * M * N * K
+        out[name] = {"us_per_launch": round(ms * 1e3, 2),
+                     "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1),
+                     "roofline_frac": round(flop / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+                     "bound": "mfma", "operand_sets": sets}
+        del A, B, D
+    return out
+
+
 def bench_extra(steps, warmup, stream, capi):
     """Secondary kernels: bytes / FLOPs per launch and roofline fractions."""
     out = bench_rows(steps, warmup, stream, capi)
@@ -1057,10 +1096,11 @@ def main(argv=None):
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--kernel", choices=["all", "gemm", "copy", "decoder", "bmm", "h2d",
                                          "attention", "spyre", "rows", "decode_step", "floor",
-                                         "yardstick"],
+                                         "yardstick", "gemm_cold"],
                     default="all",
                     help="gemm / copy / decoder / bmm / h2d / attention / decode_step / floor / "
-                         "yardstick (the GEMM next to hipBLASLt) / "
+                         "yardstick (the GEMM next to hipBLASLt) / gemm_cold (operands from "
+                         "HBM) / "
                          "rows (c1 softmax and "
                          "the c3 row kernels) / spyre (the eager and compiled paths on spyre "
                          "tensors): run only that part (for rocprofv3 passes)")
@@ -1103,6 +1143,10 @@ def main(argv=None):
     if args.kernel == "yardstick":
         print(json.dumps({"kernel": "yardstick", **bench_gemm_yardstick(stream, _capi)}))
         return 0
+    if args.kernel == "gemm_cold":
+        print(json.dumps({"kernel": "gemm_cold",
+                          **bench_gemm_cold(args.steps, args.warmup, stream, _capi)}))
+        return 0
     if args.kernel == "floor":
         print(json.dumps({"kernel": "floor", **bench_launch_floor(max(20, args.steps), _capi)}))
         return 0
@@ -1136,6 +1180,8 @@ def main(argv=None):
         extra.update(bench_attention(max(10, args.steps), sub_w, stream, _capi))
         _log("decode-step attention (c5 shape)")
         extra.update(bench_decode_step(max(20, args.steps), stream, _capi))
+        _log("GEMMs with operands from HBM")
+        extra.update(bench_gemm_cold(max(10, args.steps), sub_w, stream, _capi))
     _log("gemm 4096^3")
     g = bench_gemm(args.steps, args.warmup, stream, _capi)
     if not args.no_extra:
