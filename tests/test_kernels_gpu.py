@@ -519,33 +519,44 @@ def test_gemm_swiglu(m, n, k, pad, dtype):
         assert bool((d[:, n:] == 7.0).all()), "padding columns written"
 
 
-@pytest.mark.parametrize("m,n,k,tb,epi", [(2048, 4096, 4096, True, 0), (768, 512, 2048, False, 2),
-                                           (512, 1024, 12800, True, 0), (256, 256, 2048, True, 3)])
-def test_gemm_splitk_tail(m, n, k, tb, epi):
+@pytest.mark.parametrize("m,n,k,tb,epi,dtype", [
+    (2048, 4096, 4096, True, 0, torch.float16),    # 128 tiles, 2 K slices (O / down shape)
+    (2048, 4096, 4096, False, 3, torch.bfloat16),  # row-major B, bf16
+    (768, 512, 2048, False, 2, torch.float16),     # 6 tiles, 8 K slices
+    (512, 1024, 12800, True, 0, torch.float16),    # 8 tiles, 200 K tiles in 8 slices
+    (256, 256, 2048, True, 3, torch.float16),      # one tile
+    (2048, 10240, 2048, True, 0, torch.float16),   # 320 tiles: a full round, then 64 in 4 slices
+    (2048, 10240, 2048, False, 2, torch.bfloat16)])
+def test_gemm_splitk_tail(m, n, k, tb, epi, dtype):
     # sph_gemm_ex with a workspace: the partial last round of 256 x 256
     # tiles runs as K slices plus a reduce (alpha, beta*C with a bias row,
-    # activation applied there); against the oracle and the unsplit call
-    _log(f"gemm split-K tail {m}x{n}x{k} tb={tb} epi={epi}")
+    # activation applied there); against the oracle and the call without a
+    # workspace
+    _log(f"gemm split-K tail {m}x{n}x{k} tb={tb} epi={epi} {dtype}")
     lib = _capi.lib()
     nws = lib.sph_gemm_workspace_bytes(1, m, n, k)
     assert nws > 0, "shape should take a split"
-    X = uniform((m, k), k=61)
-    W = uniform((n, k) if tb else (k, n), k=62) * 0.05
-    bias = uniform((n,), k=63)
+    X = uniform((m, k), k=61).to(dtype)
+    W = (uniform((n, k) if tb else (k, n), k=62) * 0.05).to(dtype)
+    bias = uniform((n,), k=63).to(dtype)
     xd, wd, bd = X.to(DEV), W.to(DEV), bias.to(DEV)
     ws = torch.empty(nws, dtype=torch.uint8, device=DEV)
     outs = []
-    for w_ptr, w_n in ((_p(ws), nws), (None, 0)):
-        d = torch.empty(m, n, dtype=torch.float16, device=DEV)
-        _capi.call("sph_gemm_ex", _capi.F16, 0, int(tb), 1, m, n, k, 0.75, _p(xd), k, 0, _p(wd),
+    for rep, (w_ptr, w_n) in enumerate(((_p(ws), nws), (None, 0), (_p(ws), nws))):
+        d = torch.empty(m, n, dtype=dtype, device=DEV)
+        _capi.call("sph_gemm_ex", DT[dtype], 0, int(tb), 1, m, n, k, 0.75, _p(xd), k, 0, _p(wd),
                    k if tb else n, 0, 0.5, _p(bd), 0, 1, 0, _p(d), n, 0, epi, w_ptr, w_n, _stream())
         _sync()
         outs.append(d)
-    b_ = W.numpy().T if tb else W.numpy()
-    want = O.gemm(X.numpy(), b_, alpha=0.75, beta=0.5, c=bias.numpy()[None, :],
+    b_ = W.float().numpy().T if tb else W.float().numpy()
+    want = O.gemm(X.float().numpy(), b_, alpha=0.75, beta=0.5, c=bias.float().numpy()[None, :],
                   epilogue={0: "none", 2: "gelu", 3: "silu"}[epi])
-    assert_close_fp(outs[0], want, what="split-K tail")
-    torch.testing.assert_close(outs[0].float(), outs[1].float(), rtol=2e-3, atol=2e-3)
+    tol = dict(rtol=1e-2, atol=1e-2) if dtype == torch.float16 else dict(rtol=2e-2, atol=2e-2)
+    assert_close_fp(outs[0], want, out_dtype=dtype, what="split-K tail", **tol)
+    close = dict(rtol=2e-3, atol=2e-3) if dtype == torch.float16 else dict(rtol=1.6e-2, atol=1e-2)
+    torch.testing.assert_close(outs[0].float(), outs[1].float(), **close)
+    # the same call again: the reduce sums the slices in a fixed order
+    assert torch.equal(outs[0], outs[2]), "second call with the workspace differs"
 
 
 @pytest.mark.parametrize("m,n,k,swiglu,pad,dtype", [
