@@ -408,7 +408,12 @@ extern "C" int sph_attention_decode(sph_dtype dtype, int64_t batch, int64_t mq, 
 // unit with no merge reads the bytes alone in 11.5 us (one CU pulls ~50
 // GB/s); merging in the last workgroup of a unit to arrive, behind an
 // atomic count, needs a device-scope release per workgroup, which on this
-// 8-XCD part writes back the XCD's L2 (576 of them took 87 us).  The chunk
+// 8-XCD part writes back the XCD's L2 (576 of them took 87 us); with the
+// partials stored and loaded with sc1 (written through to the coherence
+// point, so no release) it ran 19.7 us per call against 14.6 for the pair
+// and the c5 decode step 4.46 ms against 4.28: the wait for the stores to
+// complete, the atomic and the coherent loads on the last workgroup's path
+// cost more than the second launch.  The chunk
 // holding P takes the new key and value from the rotated registers, not
 // from the cache it writes in the same launch.
 //
