@@ -1,5 +1,6 @@
-// fp16 / bf16 GEMM on gfx950 MFMA (v_mfma_f32_32x32x16_{f16,bf16}), fp32
-// accumulate, with an alpha/beta/bias/activation epilogue.
+// fp16 / bf16 GEMM on gfx950 MFMA (v_mfma_f32_16x16x32 in the direct-load
+// kernel, v_mfma_f32_32x32x16 elsewhere; {f16,bf16}), fp32 accumulate, with
+// an alpha/beta/bias/activation epilogue.
 //
 // Structure
 //   * Workgroup tile BM x BN, K step 64, WM x WN waves; each wave owns a
@@ -41,6 +42,7 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BK = 64;  // K per LDS stage (eight 16-byte chunks of fp16)
 
@@ -555,20 +557,27 @@ gemm_kernel(const GemmArgs p) {
 //     lane i the column n0 + i at k0 .. k0 + 3, half of a B fragment.  Row
 //     k's 16-byte chunk c is stored at slot c ^ 4 (k & 3): the 4 rows x 4
 //     chunks a half-wave reads then cover all 64 banks.
+//   * 16x16x32 MFMAs (v_mfma_f32_16x16x32_{f16,bf16}), not 32x32x16: the
+//     same FLOPs per LDS byte for a given wave tile, but a quarter of the
+//     accumulator registers per instruction.  This part runs the GEMM at
+//     its power limit, and a loop of nothing but MFMAs sustains 2006
+//     TFLOP/s with 16x16x32 against 1705 with 32x32x16 (8 waves per CU,
+//     random operands); the kernel gained 5-10 % on every measured shape.
 //   * Two LDS stages.  The K step is ordered by hand (sched_barrier): each of
-//     the four 16-deep MFMA sub-steps issues its MFMAs one-for-one with the
-//     LDS reads of the next sub-step's fragments.  Before sub-step 3 a wave
-//     waits for its own DMA of the next tile and its own LDS reads, then
-//     joins the barrier; sub-step 3 then also issues the DMA of the tile
-//     after next into the stage just vacated and reads the next tile's
-//     first fragments.  (Reading two sub-steps ahead measured no faster.)  Past the last tile the DMA re-loads the last tile
-//     and the fragment reads fetch values nobody uses, so the loop has no
-//     branches.
+//     the two 32-deep MFMA sub-steps issues its 32 MFMAs interleaved with
+//     the LDS reads of the next sub-step's fragments (B first, each A tile
+//     right after this sub-step's last use of the same A index).  Early in
+//     sub-step 1 a wave waits for its own DMA of the next tile and its own
+//     LDS reads, then joins the barrier; the rest of sub-step 1 issues the
+//     DMA of the tile after next into the stage just vacated and reads the
+//     next tile's first fragments.  Past the last tile the DMA re-loads the
+//     last tile and the fragment reads fetch values nobody uses, so the
+//     loop has no branches.
 //   * The DMA is issued from inline asm: as an intrinsic, the compiler waits
 //     for every outstanding LDS DMA before any later LDS read (it cannot tell
 //     the stages apart), which would serialise load and compute.  Completion
 //     is awaited explicitly (vmcnt) before the barrier.
-//   * 8 waves (2 x 4, two per SIMD), each owning a 128 x 64 block of 32x32
+//   * 8 waves (2 x 4, two per SIMD), each owning a 128 x 64 block of 16x16
 //     MFMA tiles; epilogue as in the register-staged kernel.
 // ---------------------------------------------------------------------------
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
@@ -602,44 +611,51 @@ __device__ inline void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" :::
 
 namespace dl {
 // Shared by both tile widths: 256-row tiles, 64-deep K tiles, two waves
-// along M, each wave owning a 128 x 64 block of 32x32 MFMA tiles.
-constexpr int BM = 256, BKD = 64, WM = 2, WTM = 128, WTN = 64, TM = WTM / 32, TN = WTN / 32;
+// along M, each wave owning a 128 x 64 block of 16x16 MFMA tiles
+// (v_mfma_f32_16x16x32: two 32-deep sub-steps per K tile).
+constexpr int BM = 256, BKD = 64, WM = 2, WTM = 128, WTN = 64, TM = WTM / 16;
 constexpr int CPR = BKD / 8;                    // 16-byte chunks per K row
 constexpr int A_BYTES = BM * BKD * 2;
-constexpr int KK = BKD / 16;                     // MFMA sub-steps per K tile
-constexpr int P = 1;                             // fragment prefetch distance (sub-steps)
-constexpr int NB = 2;                            // fragment buffers (kk % NB)
-constexpr int NMF = TM * TN;                     // MFMAs per sub-step
-constexpr int EPITCH = WTN + 8;
+constexpr int KK = BKD / 32;                     // MFMA sub-steps per K tile
 // K-contiguous row r, chunk c -> 16-byte slot (c ^ ((r >> 1) & 7)).
 __device__ inline int kslot(int r, int c) { return r * CPR + (c ^ ((r >> 1) & 7)); }
 
 // BN = 256 (8 waves, 2 x 4) or 128 (4 waves, 2 x 2) with 128 x 64 wave
-// tiles.  (WTN_ = 128, 128 x 128 wave tiles with 256 accumulator registers
-// in AGPRs, one wave per SIMD on a 256-wide tile, reads a third less from
-// LDS per MFMA but measured 2-3 % slower at 4096^3, 8192^3 and the decoder
-// shapes: one wave per SIMD hides less of the K-tile barrier and the LDS
-// latency.)
+// tiles.  (WTN_ = 128, 128 x 128 wave tiles with 256 accumulator registers,
+// one wave per SIMD on a 256-wide tile, reads a third less from LDS per
+// MFMA but measured 2-3 % slower with 32x32x16 MFMAs: one wave per SIMD
+// hides less of the K-tile barrier and the LDS latency.)
 template <int BN_, int WTN_ = WTN>
 struct Cfg {
-  static constexpr int WTN = WTN_, TN = WTN / 32, NMF = TM * TN, EPITCH = WTN + 8;
+  static constexpr int WTN = WTN_, TN = WTN / 16, NMF = TM * TN, EPITCH = WTN + 8;
   static constexpr int BN = BN_, WN = BN / WTN, NW = WM * WN, NT = NW * 64;
   static constexpr int B_BYTES = BN * BKD * 2, STAGE = A_BYTES + B_BYTES;
   static constexpr int LPA = A_BYTES / 1024 / NW, LPB = B_BYTES / 1024 / NW;  // DMA lines per wave
   static constexpr int BCH = BN / 8;             // 16-byte chunks per row-major B row
   static_assert(LPA * NW * 1024 == A_BYTES && LPB * NW * 1024 == B_BYTES, "DMA lines");
-  static_assert(P * NMF * 2 >= LPA + LPB, "DMA fits in the post-barrier sub-steps");
+  static_assert(NMF >= TN - 1 + LPA + LPB, "DMA fits in the post-barrier sub-step");
   static_assert(NW * 32 * EPITCH * 4 <= 2 * STAGE, "epilogue staging exceeds LDS");
 };
 }  // namespace dl
 
+template <typename T>
+__device__ inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (__is_same(T, half_t)) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(
+        __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+        __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+}
+
 // SWIGLU: B holds the gate rows [0, n) and the up rows [n, 2n) of one
 // weight matrix (K-contiguous) and D[m, j] = silu(A B_gate[j]) * (A B_up[j]).
 // A 256-wide tile then covers 128 output columns: in the 64 columns of wave
-// wn, MFMA tile 0 takes gate rows j0 + 32 wn .. + 31 and tile 1 the up rows
-// of the same columns, so each lane's two accumulators hold the gate and up
-// sums of the same output element and the epilogue combines them in
-// registers.
+// wn, MFMA tiles 0 and 1 take gate rows j0 + 32 wn .. + 31 and tiles 2 and 3
+// the up rows of the same columns, so a lane's accumulators j and j + 2
+// hold the gate and up sums of the same output element and the epilogue
+// combines them in registers.
 template <typename T, bool B_KCONT, int BN_, bool SWIGLU = false, int WTN_ = dl::WTN>
 __global__ void __launch_bounds__((dl::Cfg<BN_, WTN_>::NT)) gemm_dl_kernel(const GemmArgs p) {
   using namespace dl;
@@ -648,8 +664,7 @@ __global__ void __launch_bounds__((dl::Cfg<BN_, WTN_>::NT)) gemm_dl_kernel(const
   static_assert(!SWIGLU || (B_KCONT && BN_ == 256), "SwiGLU tiles: K-contiguous B, 256 wide");
   constexpr int BN = DC::BN, WN = DC::WN, STAGE = DC::STAGE, LPA = DC::LPA, LPB = DC::LPB;
   constexpr int NBR = B_KCONT ? 1 : 2;           // LDS reads per B fragment
-  constexpr int NDS = TM + TN * NBR;             // LDS reads per sub-step
-  static_assert(NDS <= NMF, "one read per MFMA");
+  constexpr int XB = TN - 1;                     // barrier before this MFMA of the last sub-step
   __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
 
   // Tile rank and K slice: workgroups past tail_start are split-K slices of
@@ -709,61 +724,61 @@ __global__ void __launch_bounds__((dl::Cfg<BN_, WTN_>::NT)) gemm_dl_kernel(const
     }
   }
   const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((SPH_LDS char*)(lds)));
-  const int row_in = lane & 31, khalf = lane >> 5;
-  int boff[TN];  // row-major B: byte offset of this lane's transpose-read pointer
+  // Fragment reads.  16x16x32 operands: lane l holds row (column) l % 16 and
+  // the 8 K values 8 (l / 16) .. + 7 of the sub-step, one 16-byte chunk of a
+  // K-contiguous row: chunk 4 kk + l / 16, whose slot is swizzled by
+  // (r >> 1) & 7 = (l % 16 >> 1) & 7 for every tile (tiles start at rows that
+  // are multiples of 16), so offset(kk, tile t) = off[kk] + 2048 t.
+  const int m16 = lane & 15, g4 = lane >> 4, sw = g4 ^ ((m16 >> 1) & 7);
+  int aoff[KK], bkoff[KK];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) {
+    aoff[kk] = (wm * WTM + m16) * (CPR * 16) + ((sw ^ (4 * kk)) << 4);
+    bkoff[kk] = A_BYTES + (wn * WTN + m16) * (CPR * 16) + ((sw ^ (4 * kk)) << 4);
+  }
+  // Row-major B: two transposing reads per fragment.  ds_read_b64_tr_b16
+  // has each 16-lane group read a 4 x 16 block (lane e * 4 + q: row e,
+  // columns 4q .. 4q + 3) and hands lane m column m of it; group g4 reads K
+  // rows 32 kk + 8 g4 + 4 h + e of the fragment's 16 columns.
+  int boff[TN];
   {
-    const int g = lane >> 4, jj = lane & 15, e = jj >> 2, q = jj & 3;
+    const int e = m16 >> 2, q = m16 & 3;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int n = wn * WTN + j * 32 + 16 * (g & 1) + 4 * q;
-      const int k = 8 * (g >> 1) + e;
-      boff[j] = A_BYTES + k * (BN * 2) + (((n >> 3) ^ (4 * e)) << 4) + 8 * (q & 1);
+      const int n = wn * WTN + j * 16 + 4 * q;
+      boff[j] = A_BYTES + (8 * g4 + e) * (BN * 2) + (((n >> 3) ^ (4 * e)) << 4) + 8 * (q & 1);
     }
   }
 
-  f32x16 acc[TM][TN];
+  f32x4 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-  u32x4 af[NB][TM];
-  u32x2 bl[NB][TN], bh[NB][TN];
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4 af[2][TM];
+  u32x2 bl[2][TN], bh[2][TN];
 
-// LDS read number X (0 .. NDS-1) of sub-step KK_'s fragments from the stage at
-// byte offset STB_, into buffer BUF_.  Order: A0, the B fragments, A1 ..: the
-// first MFMAs of a sub-step need A0 and all of B.
-#define SPH_DL_READ(BUF_, X_, STB_, KK_)                                                    \
+// Fragment reads of sub-step KK_ from the stage at byte offset STB_ into
+// buffer BUF_: A tile I_; B fragment read X_ (K-contiguous: fragment X_;
+// row-major: fragment X_ / 2, half X_ % 2).
+#define SPH_DL_READ_A(BUF_, I_, STB_, KK_)                                                  \
+  af[BUF_][I_] = *reinterpret_cast<const u32x4*>(lds + (STB_) + aoff[KK_] + (I_) * 2048)
+#define SPH_DL_READ_B(BUF_, X_, STB_, KK_)                                                  \
   do {                                                                                      \
-    const int x_ = (X_);                                                                    \
-    const char* st_ = lds + (STB_);                                                         \
-    if (x_ == 0 || x_ > TN * NBR) {                                                         \
-      const int i_ = x_ == 0 ? 0 : x_ - TN * NBR;                                           \
-      const int r_ = wm * WTM + i_ * 32 + row_in;                                          \
-      af[BUF_][i_] = *reinterpret_cast<const u32x4*>(st_ + kslot(r_, (KK_) * 2 + khalf) * 16); \
-    } else if constexpr (B_KCONT) {                                                         \
-      const int j_ = x_ - 1;                                                                \
-      const int r_ = wn * WTN + j_ * 32 + row_in;                                          \
+    if constexpr (B_KCONT) {                                                                \
       const u32x4 v_ =                                                                      \
-          *reinterpret_cast<const u32x4*>(st_ + A_BYTES + kslot(r_, (KK_) * 2 + khalf) * 16); \
-      bl[BUF_][j_] = u32x2{v_[0], v_[1]};                                                   \
-      bh[BUF_][j_] = u32x2{v_[2], v_[3]};                                                   \
+          *reinterpret_cast<const u32x4*>(lds + (STB_) + bkoff[KK_] + (X_) * 2048);         \
+      bl[BUF_][X_] = u32x2{v_[0], v_[1]};                                                   \
+      bh[BUF_][X_] = u32x2{v_[2], v_[3]};                                                   \
     } else {                                                                                \
-      const int j_ = (x_ - 1) >> 1, h_ = (x_ - 1) & 1;                                      \
-      const SPH_LDS char* p_ =                                                              \
-          (const SPH_LDS char*)(st_) + boff[j_] + ((KK_) * 16 + 4 * h_) * (BN * 2);         \
+      const int j_ = (X_) >> 1, h_ = (X_) & 1;                                              \
+      const SPH_LDS char* p_ = (const SPH_LDS char*)(lds + (STB_)) + boff[j_] +             \
+                               ((KK_) * 32 + 4 * h_) * (BN * 2);                            \
       const u32x2 v_ = __builtin_bit_cast(                                                  \
           u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((SPH_LDS s16x4*)(p_)));            \
       if (h_) bh[BUF_][j_] = v_;                                                            \
       else bl[BUF_][j_] = v_;                                                               \
     }                                                                                       \
-  } while (0)
-#define SPH_DL_MFMA(BUF_, X_)                                                               \
-  do {                                                                                      \
-    const int i_ = (X_) / TN, j_ = (X_) % TN;                                               \
-    const u32x4 b_ = __builtin_shufflevector(bl[BUF_][j_], bh[BUF_][j_], 0, 1, 2, 3);       \
-    acc[i_][j_] = mfma32<T>(af[BUF_][i_], b_, acc[i_][j_]);                                 \
   } while (0)
 // DMA line LINE_ (A lines first, then B) of K tile T_ into stage SL_ & 1.
 #define SPH_DL_DMA(T_, SL_, LINE_)                                                          \
@@ -780,8 +795,8 @@ __global__ void __launch_bounds__((dl::Cfg<BN_, WTN_>::NT)) gemm_dl_kernel(const
                                                    : (kt0 + t_) * BKD * ldb * 2));          \
   } while (0)
 
-  // Prologue: K tiles 0 and 1 in flight; wait for tile 0; fragments of the
-  // first P sub-steps.
+  // Prologue: K tiles 0 and 1 in flight; wait for tile 0; the fragments of
+  // its first sub-step.
 #pragma unroll
   for (int l = 0; l < LPA + LPB; ++l) SPH_DL_DMA(0, 0, l);
   if (ksteps > 1) {
@@ -793,45 +808,54 @@ __global__ void __launch_bounds__((dl::Cfg<BN_, WTN_>::NT)) gemm_dl_kernel(const
   }
   __syncthreads();
 #pragma unroll
-  for (int kk = 0; kk < P; ++kk)
+  for (int x = 0; x < TN * NBR; ++x) SPH_DL_READ_B(0, x, 0, 0);
 #pragma unroll
-    for (int x = 0; x < NDS; ++x) SPH_DL_READ(kk % NB, x, 0, kk);
+  for (int i = 0; i < TM; ++i) SPH_DL_READ_A(0, i, 0, 0);
 
+  // Sub-step kk: MFMA x = (A tile x / TN, B fragment x % TN).  Its reads of
+  // the next sub-step's fragments: the B reads first (the next sub-step's
+  // first MFMAs need all of B), each A tile right after the last MFMA that
+  // uses this sub-step's A tile of the same index (so the two can share
+  // registers).  Before MFMA XB of the last sub-step a wave waits for its own
+  // DMA of the next K tile and its own LDS reads, then joins the barrier;
+  // after it the sub-step reads the next tile's fragments and issues the DMA
+  // of the tile after next into the stage just vacated.  Past the last tile
+  // the DMA re-loads the last tile and the fragment reads fetch values nobody
+  // uses, so the loop has no branches.
   for (int ks = 0; ks < ksteps; ++ks) {
     const int cs = (ks & 1) * STAGE, ns = ((ks + 1) & 1) * STAGE;
     const int tnext = ks + 2 < ksteps ? ks + 2 : ksteps - 1;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
-      if (kk == KK - P) {
-        // This wave's DMA of tile ks+1 has landed and its reads of tile ks
-        // are complete; past the barrier every wave is.
-        wait_vmcnt<0>();
-        wait_lgkmcnt0();
-        __syncthreads();
-      }
+      const bool lastk = kk == KK - 1;
+      const int nst = lastk ? ns : cs;           // stage of the next sub-step
+      const int nkk = lastk ? 0 : kk + 1;        // and its index
+      const int x0 = lastk ? XB : 0;             // first slot of the B reads
 #pragma unroll
       for (int x = 0; x < NMF; ++x) {
-        SPH_DL_MFMA(kk % NB, x);
-        if (x < NDS) {
-          if (kk + P < KK)
-            SPH_DL_READ((kk + P) % NB, x, cs, kk + P);
-          else
-            SPH_DL_READ((kk + P) % NB, x, ns, kk + P - KK);
+        const int i = x / TN, j = x % TN;
+        if (lastk && x == XB) {
+          wait_vmcnt<0>();
+          wait_lgkmcnt0();
+          __syncthreads();
         }
-        if (kk >= KK - P) {
-#pragma unroll
-          for (int d = (kk - (KK - P)) * NMF + x; d < LPA + LPB; d += P * NMF)
-            SPH_DL_DMA(tnext, ks, d);
+        {
+          const u32x4 b_ = __builtin_shufflevector(bl[kk & 1][j], bh[kk & 1][j], 0, 1, 2, 3);
+          acc[i][j] = mfma16<T>(af[kk & 1][i], b_, acc[i][j]);
         }
+        if (x >= x0 && x - x0 < TN * NBR) SPH_DL_READ_B((kk + 1) & 1, x - x0, nst, nkk);
+        if (j == TN - 1) SPH_DL_READ_A((kk + 1) & 1, i, nst, nkk);
+        if (lastk && x >= XB && x - XB < LPA + LPB) SPH_DL_DMA(tnext, ks, x - XB);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
-#undef SPH_DL_READ
-#undef SPH_DL_MFMA
+#undef SPH_DL_READ_A
+#undef SPH_DL_READ_B
 #undef SPH_DL_DMA
 
-  // Epilogue (LDS reused as fp32 slabs once every DMA has landed).
+  // Epilogue (LDS reused as fp32 slabs once every DMA has landed).  16x16
+  // accumulator r of lane l: row 4 (l / 16) + r, column l % 16 of its tile.
   wait_vmcnt<0>();
   if (partial) {
     // split-K slice: the raw fp32 tile, element (r, c) at r * BN + c
@@ -841,9 +865,9 @@ __global__ void __launch_bounds__((dl::Cfg<BN_, WTN_>::NT)) gemm_dl_kernel(const
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          W[row * BN + wn * WTN + j * 32 + (lane & 31)] = acc[i][j][r];
+        for (int r = 0; r < 4; ++r) {
+          const int row = wm * WTM + i * 16 + 4 * g4 + r;
+          W[row * BN + wn * WTN + j * 16 + m16] = acc[i][j][r];
         }
     return;
   }
@@ -854,31 +878,36 @@ __global__ void __launch_bounds__((dl::Cfg<BN_, WTN_>::NT)) gemm_dl_kernel(const
   const int64_t row0 = m0 + wm * WTM;
   if constexpr (SWIGLU) {
     // silu(gate) * up per element, 32 output columns per wave
-    static_assert(TN == 2, "gate / up tile pair");
+    static_assert(TN == 4, "gate / up tile pairs");
     constexpr int SP = 32 + 8;
     const int64_t colw = n0 + wn * 32;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int i2 = 0; i2 < TM / 2; ++i2) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        slab[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * SP + (lane & 31)] =
-            silu(acc[i][0][r]) * acc[i][1][r];
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            slab[(ii * 16 + 4 * g4 + r) * SP + j * 16 + m16] =
+                silu(acc[2 * i2 + ii][j][r]) * acc[2 * i2 + ii][j + 2][r];
       __syncthreads();
-      store_slab<T, 32, SP>(p, slab, D, C, row0 + i * 32, colw, lane);
+      store_slab<T, 32, SP>(p, slab, D, C, row0 + i2 * 32, colw, lane);
       __syncthreads();
     }
   } else {
     const int64_t colw = n0 + wn * WTN;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int i2 = 0; i2 < TM / 2; ++i2) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+      for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          slab[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * EPITCH + j * 32 + (lane & 31)] =
-              acc[i][j][r];
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            slab[(ii * 16 + 4 * g4 + r) * EPITCH + j * 16 + m16] = acc[2 * i2 + ii][j][r];
       __syncthreads();
-      store_slab<T, WTN, EPITCH>(p, slab, D, C, row0 + i * 32, colw, lane);
+      store_slab<T, WTN, EPITCH>(p, slab, D, C, row0 + i2 * 32, colw, lane);
       __syncthreads();
     }
   }
@@ -889,7 +918,6 @@ __global__ void __launch_bounds__((dl::Cfg<BN_, WTN_>::NT)) gemm_dl_kernel(const
 // consecutive output columns of one row (16-byte reads of every slice).
 // SWIGLU: output column oc of the tile is silu(gate) * up with the gate sum
 // at tile column 64 (oc / 32) + oc % 32 and the up sum 32 columns further.
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T, int BN, bool SWIGLU>
 __global__ void __launch_bounds__(256) gemm_splitk_reduce(const GemmArgs p) {
