@@ -633,7 +633,9 @@ struct Cfg {
   static constexpr int LPA = A_BYTES / 1024 / NW, LPB = B_BYTES / 1024 / NW;  // DMA lines per wave
   static constexpr int BCH = BN / 8;             // 16-byte chunks per row-major B row
   static_assert(LPA * NW * 1024 == A_BYTES && LPB * NW * 1024 == B_BYTES, "DMA lines");
-  static_assert(NMF >= TN - 1 + LPA + LPB, "DMA fits in the post-barrier sub-step");
+  // the K-tile barrier comes before MFMA XB of the last sub-step
+  static constexpr int XB = 8 < NMF - LPA - LPB ? 8 : NMF - LPA - LPB;
+  static_assert(XB >= TN - 1, "barrier after the last reads of the stage");
   static_assert(NW * 32 * EPITCH * 4 <= 2 * STAGE, "epilogue staging exceeds LDS");
 };
 }  // namespace dl
@@ -664,7 +666,7 @@ __global__ void __launch_bounds__((dl::Cfg<BN_, WTN_>::NT)) gemm_dl_kernel(const
   static_assert(!SWIGLU || (B_KCONT && BN_ == 256), "SwiGLU tiles: K-contiguous B, 256 wide");
   constexpr int BN = DC::BN, WN = DC::WN, STAGE = DC::STAGE, LPA = DC::LPA, LPB = DC::LPB;
   constexpr int NBR = B_KCONT ? 1 : 2;           // LDS reads per B fragment
-  constexpr int XB = TN - 1;                     // barrier before this MFMA of the last sub-step
+  constexpr int XB = DC::XB;                     // barrier before this MFMA of the last sub-step
   __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
 
   // Tile rank and K slice: workgroups past tail_start are split-K slices of
@@ -844,7 +846,14 @@ __global__ void __launch_bounds__((dl::Cfg<BN_, WTN_>::NT)) gemm_dl_kernel(const
           acc[i][j] = mfma16<T>(af[kk & 1][i], b_, acc[i][j]);
         }
         if (x >= x0 && x - x0 < TN * NBR) SPH_DL_READ_B((kk + 1) & 1, x - x0, nst, nkk);
-        if (j == TN - 1) SPH_DL_READ_A((kk + 1) & 1, i, nst, nkk);
+#pragma unroll
+        for (int ii = 0; ii < TM; ++ii) {
+          // after this sub-step's last use of A tile ii (the last sub-step
+          // shifts the reads past the barrier)
+          const int last_use = ii * TN + TN - 1;
+          const int at = lastk ? min(NMF - 1, last_use + XB - (TN - 1)) : last_use;
+          if (x == at) SPH_DL_READ_A((kk + 1) & 1, ii, nst, nkk);
+        }
         if (lastk && x >= XB && x - XB < LPA + LPB) SPH_DL_DMA(tnext, ks, x - XB);
         __builtin_amdgcn_sched_barrier(0);
       }
