@@ -555,8 +555,10 @@ gemm_kernel(const GemmArgs p) {
 //     i % 4 of the rows addressed by lanes i / 4, 4 + i / 4, 8 + i / 4,
 //     12 + i / 4.  Pointing lane 4e + q at (k0 + e, n0 + 4q) therefore gives
 //     lane i the column n0 + i at k0 .. k0 + 3, half of a B fragment.  Row
-//     k's 16-byte chunk c is stored at slot c ^ 4 (k & 3): the 4 rows x 4
-//     chunks a half-wave reads then cover all 64 banks.
+//     k's 16-byte chunk c is stored at slot c ^ bswz(k) (4 (k & 3) + 2
+//     (bit 3 of k)): the 8 rows x 2 chunks a half-wave reads then cover all
+//     64 banks.  (With c ^ 4 (k & 3) alone, rows k and k + 8 share banks:
+//     27 % of the LDS-active cycles were bank conflicts.)
 //   * 16x16x32 MFMAs (v_mfma_f32_16x16x32_{f16,bf16}), not 32x32x16: the
 //     same FLOPs per LDS byte for a given wave tile, but a quarter of the
 //     accumulator registers per instruction.  This part runs the GEMM at
@@ -619,6 +621,12 @@ constexpr int A_BYTES = BM * BKD * 2;
 constexpr int KK = BKD / 32;                     // MFMA sub-steps per K tile
 // K-contiguous row r, chunk c -> 16-byte slot (c ^ ((r >> 1) & 7)).
 __device__ inline int kslot(int r, int c) { return r * CPR + (c ^ ((r >> 1) & 7)); }
+// Row-major B: K row k's 16-byte chunk c sits at slot c ^ bswz(k).  A
+// transposing read's 32-lane half covers rows k0 .. k0 + 3 and k0 + 8 ..
+// k0 + 11 (k0 a multiple of 4 with bit 3 clear) at the same two chunks:
+// bits 2-3 of the XOR spread the four rows of a lane group over the 256
+// bytes of banks, bit 1 moves the second group's rows to the other half.
+__device__ inline int bswz(int k) { return 4 * (k & 3) + 2 * ((k >> 3) & 1); }
 
 // BN = 256 (8 waves, 2 x 4) or 128 (4 waves, 2 x 2) with 128 x 64 wave
 // tiles.  (WTN_ = 128, 128 x 128 wave tiles with 256 accumulator registers,
@@ -721,7 +729,7 @@ __global__ void __launch_bounds__((dl::Cfg<BN_, WTN_>::NT)) gemm_dl_kernel(const
       const int r = s / CPR, c = (s % CPR) ^ ((r >> 1) & 7);
       vb[i] = static_cast<uint32_t>(r * ldb * 2 + c * 16);
     } else {
-      const int k = s / DC::BCH, c = (s % DC::BCH) ^ (4 * (k & 3));
+      const int k = s / DC::BCH, c = (s % DC::BCH) ^ bswz(k);
       vb[i] = static_cast<uint32_t>(k * ldb * 2 + c * 16);
     }
   }
@@ -748,7 +756,7 @@ __global__ void __launch_bounds__((dl::Cfg<BN_, WTN_>::NT)) gemm_dl_kernel(const
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int n = wn * WTN + j * 16 + 4 * q;
-      boff[j] = A_BYTES + (8 * g4 + e) * (BN * 2) + (((n >> 3) ^ (4 * e)) << 4) + 8 * (q & 1);
+      boff[j] = A_BYTES + (8 * g4 + e) * (BN * 2) + (((n >> 3) ^ bswz(8 * g4 + e)) << 4) + 8 * (q & 1);
     }
   }
 
