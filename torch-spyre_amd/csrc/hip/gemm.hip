@@ -33,6 +33,7 @@
 //     streaming kernel (gemm_skinny_kernel) with packed fp16 dot products
 //     instead of MFMA tiles, which would leave most CUs idle at M <= 16.
 #include <algorithm>
+#include <type_traits>
 
 #include "sph_common.h"
 
@@ -325,15 +326,20 @@ __device__ inline void store_slab_impl(const GemmArgs& p, const float* slab, T* 
   }
 }
 
-template <typename T, int WTN, int EPITCH>
-__device__ inline void store_slab(const GemmArgs& p, const float* slab, T* D, const T* C,
-                                  int64_t row0, int64_t col0, int lane) {
-  const bool use_c = C != nullptr && p.beta != 0.f;
+// Calls f(std::integral_constant<int, E>, std::bool_constant<USE_C>) for the
+// call's activation E and C term, so that a kernel's epilogue loop (which
+// calls store_slab_impl<T, E, USE_C, ..> per 32-row slab) is instantiated
+// once per case.  With the choice made inside the loop instead, the bf16
+// loop bodies grew past the unroller's limit and the accumulators, indexed
+// by the slab number, were kept in scratch memory.
+template <typename F>
+__device__ inline void epi_dispatch(const GemmArgs& p, const void* c, F&& f) {
+  const bool use_c = c != nullptr && p.beta != 0.f;
 #define SPH_EPI_CASE(E)                                                            \
   if (use_c)                                                                       \
-    store_slab_impl<T, E, true, WTN, EPITCH>(p, slab, D, C, row0, col0, lane);     \
+    f(std::integral_constant<int, E>{}, std::true_type{});                         \
   else                                                                             \
-    store_slab_impl<T, E, false, WTN, EPITCH>(p, slab, D, C, row0, col0, lane);
+    f(std::integral_constant<int, E>{}, std::false_type{});
   switch (p.epilogue) {
     case SPH_EPI_RELU:
       SPH_EPI_CASE(SPH_EPI_RELU);
@@ -523,18 +529,22 @@ gemm_kernel(const GemmArgs p) {
   float* slab = reinterpret_cast<float*>(lds) + wave * (32 * EPITCH);
   const int64_t row0 = m0 + wm * WTM;
   const int64_t colw = n0 + wn * WTN;
+  epi_dispatch(p, C, [&](auto epi_, auto use_c_) {
+    constexpr int E = decltype(epi_)::value;
+    constexpr bool UC = decltype(use_c_)::value;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
+    for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        slab[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * EPITCH + j * 32 + (lane & 31)] =
-            acc[i][j][r];
-    __syncthreads();
-    store_slab<T, WTN, EPITCH>(p, slab, D, C, row0 + i * 32, colw, lane);
-    __syncthreads();
-  }
+        for (int r = 0; r < 16; ++r)
+          slab[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * EPITCH + j * 32 + (lane & 31)] =
+              acc[i][j][r];
+      __syncthreads();
+      store_slab_impl<T, E, UC, WTN, EPITCH>(p, slab, D, C, row0 + i * 32, colw, lane);
+      __syncthreads();
+    }
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -893,41 +903,46 @@ __global__ void __launch_bounds__((dl::Cfg<BN_, WTN_>::NT)) gemm_dl_kernel(const
   const T* C = p.c ? static_cast<const T*>(p.c) + batch * p.stride_c : nullptr;
   float* slab = reinterpret_cast<float*>(lds) + wave * (32 * EPITCH);
   const int64_t row0 = m0 + wm * WTM;
-  if constexpr (SWIGLU) {
-    // silu(gate) * up per element, 32 output columns per wave
-    static_assert(TN == 4, "gate / up tile pairs");
-    constexpr int SP = 32 + 8;
-    const int64_t colw = n0 + wn * 32;
+  auto chunks = [&](auto epi_, auto use_c_) {
+    constexpr int E = decltype(epi_)::value;
+    constexpr bool UC = decltype(use_c_)::value;
+    if constexpr (SWIGLU) {
+      // silu(gate) * up per element, 32 output columns per wave
+      static_assert(TN == 4, "gate / up tile pairs");
+      constexpr int SP = 32 + 8;
+      const int64_t colw = n0 + wn * 32;
 #pragma unroll
-    for (int i2 = 0; i2 < TM / 2; ++i2) {
+      for (int i2 = 0; i2 < TM / 2; ++i2) {
 #pragma unroll
-      for (int ii = 0; ii < 2; ++ii)
+        for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+          for (int j = 0; j < 2; ++j)
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            slab[(ii * 16 + 4 * g4 + r) * SP + j * 16 + m16] =
-                silu(acc[2 * i2 + ii][j][r]) * acc[2 * i2 + ii][j + 2][r];
-      __syncthreads();
-      store_slab<T, 32, SP>(p, slab, D, C, row0 + i2 * 32, colw, lane);
-      __syncthreads();
+            for (int r = 0; r < 4; ++r)
+              slab[(ii * 16 + 4 * g4 + r) * SP + j * 16 + m16] =
+                  silu(acc[2 * i2 + ii][j][r]) * acc[2 * i2 + ii][j + 2][r];
+        __syncthreads();
+        store_slab_impl<T, E, UC, 32, SP>(p, slab, D, C, row0 + i2 * 32, colw, lane);
+        __syncthreads();
+      }
+    } else {
+      const int64_t colw = n0 + wn * WTN;
+#pragma unroll
+      for (int i2 = 0; i2 < TM / 2; ++i2) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              slab[(ii * 16 + 4 * g4 + r) * EPITCH + j * 16 + m16] = acc[2 * i2 + ii][j][r];
+        __syncthreads();
+        store_slab_impl<T, E, UC, WTN, EPITCH>(p, slab, D, C, row0 + i2 * 32, colw, lane);
+        __syncthreads();
+      }
     }
-  } else {
-    const int64_t colw = n0 + wn * WTN;
-#pragma unroll
-    for (int i2 = 0; i2 < TM / 2; ++i2) {
-#pragma unroll
-      for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            slab[(ii * 16 + 4 * g4 + r) * EPITCH + j * 16 + m16] = acc[2 * i2 + ii][j][r];
-      __syncthreads();
-      store_slab<T, WTN, EPITCH>(p, slab, D, C, row0 + i2 * 32, colw, lane);
-      __syncthreads();
-    }
-  }
+  };
+  epi_dispatch(p, C, chunks);
 }
 
 // Sums the split-K slices of one tail tile and applies the epilogue: one
