@@ -265,6 +265,37 @@ def bench_gemm_cold(steps, warmup, stream, capi, sets=8):
     return out
 
 
+def bench_gemm_bf16(steps, warmup, stream, capi):
+    """c2's 4096^3 A @ B (both row-major) in bf16 through sph_gemm, HIP events
+    after the fp16 headline's warmup count; a sample of rows must agree with
+    torch's fp32 product of the same bf16 operands within 2e-2."""
+    import torch
+
+    lib = capi.lib()
+    s = stream.cuda_stream
+    M = N = K = 4096
+    a = (torch.rand(M, K, generator=_gen(80)) * 2 - 1).to(torch.bfloat16).cuda()
+    b = (torch.rand(K, N, generator=_gen(81)) * 2 - 1).to(torch.bfloat16).cuda()
+    d = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+
+    def step():
+        rc = lib.sph_gemm(capi.BF16, 0, 0, M, N, K, 1.0, a.data_ptr(), K, b.data_ptr(), N, 0.0,
+                          None, 0, 0, d.data_ptr(), N, 0, s)
+        if rc:
+            capi.check(rc, "sph_gemm")
+
+    ms, _ = Timer(stream).run(step, max(steps, 20), max(warmup, 300))
+    rows = torch.arange(0, M, 256, device="cuda")
+    ref = a.index_select(0, rows).float() @ b.float()
+    torch.testing.assert_close(d.index_select(0, rows).float(), ref, rtol=2e-2, atol=2e-2)
+    flop = 2.0 * M * N * K
+    tf = flop / (ms * 1e-3) / 1e12
+    return {"c2_mm_4096_bf16": {"us_per_launch": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                                "roofline_frac": round(tf / PEAK_FP16_TFLOPS, 4), "bound": "mfma",
+                                "note": "bf16 operands and output, fp32 accumulate; "
+                                        "dense bf16 MFMA peak = the fp16 one"}}
+
+
 def bench_extra(steps, warmup, stream, capi):
     """Secondary kernels: bytes / FLOPs per launch and roofline fractions."""
     out = bench_rows(steps, warmup, stream, capi)
@@ -1145,7 +1176,8 @@ def main(argv=None):
         return 0
     if args.kernel == "gemm_cold":
         print(json.dumps({"kernel": "gemm_cold",
-                          **bench_gemm_cold(args.steps, args.warmup, stream, _capi)}))
+                          **bench_gemm_cold(args.steps, args.warmup, stream, _capi),
+                          **bench_gemm_bf16(args.steps, args.warmup, stream, _capi)}))
         return 0
     if args.kernel == "floor":
         print(json.dumps({"kernel": "floor", **bench_launch_floor(max(20, args.steps), _capi)}))
@@ -1182,6 +1214,8 @@ def main(argv=None):
         extra.update(bench_decode_step(max(20, args.steps), stream, _capi))
         _log("GEMMs with operands from HBM")
         extra.update(bench_gemm_cold(max(10, args.steps), sub_w, stream, _capi))
+        _log("bf16 gemm 4096^3")
+        extra.update(bench_gemm_bf16(max(10, args.steps), sub_w, stream, _capi))
     _log("gemm 4096^3")
     g = bench_gemm(args.steps, args.warmup, stream, _capi)
     if not args.no_extra:
