@@ -253,13 +253,39 @@ struct AnyF {
   __device__ static inline float op(float a, float b) { return (a != 0.f || b != 0.f) ? 1.f : 0.f; }
 };
 
+// Lane-to-lane move within a row of 16 lanes (DPP control CTRL: quad
+// permutations, row mirrors), no LDS round trip.
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xf, 0xf, false));
+}
+
+// Reduction over the 64 lanes of a wave; every lane gets the result.  Within
+// each row of 16 lanes: swap neighbours (quad_perm 1,0,3,2), pairs
+// (2,3,0,1), then the mirrored half row and the mirrored row, so every lane
+// holds its row's total; the four row totals are read as scalars (lanes 0,
+// 16, 32, 48) and combined.
+template <typename Op>
+__device__ inline float wave_reduce(float v) {
+  v = Op::op(v, dpp_f<0xb1>(v));
+  v = Op::op(v, dpp_f<0x4e>(v));
+  v = Op::op(v, dpp_f<0x141>(v));
+  v = Op::op(v, dpp_f<0x140>(v));
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return Op::op(Op::op(r0, r1), Op::op(r2, r3));
+}
+
 // Reduction over the BLOCK threads of the workgroup; every thread gets the
 // result.  `lds` holds BLOCK/64 floats; two barriers, so every thread of the
 // workgroup must call it.
 template <typename Op, int BLOCK>
 __device__ inline float block_reduce(float v, float* lds) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = Op::op(v, __shfl_xor(v, off, kWave));
+  v = wave_reduce<Op>(v);
   if constexpr (BLOCK <= kWave) {
     return v;
   } else {
