@@ -48,7 +48,8 @@ DT = {torch.float16: _capi.F16, torch.bfloat16: _capi.BF16, torch.float32: _capi
 # softmax
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("rows,cols", [(512, 4096), (3, 64), (5, 1), (7, 1000), (33, 7),
-                                       (4, 2048), (2, 8192), (2, 12000), (2, 70000)])
+                                       (4, 2048), (2, 8192), (2, 12000), (2, 32768), (3, 40000),
+                                       (2, 70000)])
 def test_softmax_shapes(rows, cols):
     _log(f"softmax {rows}x{cols}")
     x = randn((rows, cols), k=0, scale=4.0)
@@ -137,7 +138,7 @@ def test_softmax_causal(q_len, k_len):
 # norms
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("rows,cols", [(8192, 4096), (3, 64), (17, 100), (4, 4097),
-                                       (2, 70000), (64, 1)])
+                                       (2, 20000), (2, 40000), (2, 70000), (64, 1)])
 @pytest.mark.parametrize("residual", [False, True])
 def test_rmsnorm(rows, cols, residual):
     _log(f"rmsnorm {rows}x{cols} residual={residual}")
@@ -159,7 +160,7 @@ def test_rmsnorm(rows, cols, residual):
         assert torch.equal(hd.cpu(), (x + r))
 
 
-@pytest.mark.parametrize("rows,cols", [(8192, 4096), (5, 300), (3, 8), (2, 70000)])
+@pytest.mark.parametrize("rows,cols", [(8192, 4096), (5, 300), (3, 8), (2, 20000), (2, 70000)])
 @pytest.mark.parametrize("residual", [False, True])
 def test_layernorm(rows, cols, residual):
     _log(f"layernorm {rows}x{cols} residual={residual}")
@@ -208,7 +209,8 @@ def test_norm_fp32_weight_and_bf16():
 # ---------------------------------------------------------------------------
 # GELU chain
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("rows,cols", [(8192, 4096), (3, 100), (2, 70000), (7, 2048), (5, 8192)])
+@pytest.mark.parametrize("rows,cols", [(8192, 4096), (3, 100), (2, 70000), (7, 2048), (5, 8192),
+                                       (2, 16384), (2, 50000)])
 def test_gelu_affine_rowsum(rows, cols):
     _log(f"gelu_rowsum {rows}x{cols}")
     x = randn((rows, cols), k=0)

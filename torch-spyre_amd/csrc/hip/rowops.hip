@@ -19,8 +19,11 @@ struct RowCfg {
   int tpr;
   int vpt;
 };
-constexpr RowCfg kCfgs[] = {{64, 1}, {64, 4}, {256, 2}, {256, 4}, {1024, 8}};
-constexpr int kNumCfgs = 5;
+// ({1024, 4} before {1024, 8}: rows up to 32768 elements then run on the
+// configuration whose registers hold them without spilling; with 8 chunks
+// per thread a 1024-thread workgroup (128 registers per lane) spills.)
+constexpr RowCfg kCfgs[] = {{64, 1}, {64, 4}, {256, 2}, {256, 4}, {1024, 4}, {1024, 8}};
+constexpr int kNumCfgs = 6;
 
 inline int pick_cfg(int64_t cols) {
   for (int i = 0; i < kNumCfgs; ++i)
@@ -674,6 +677,7 @@ int softmax_impl(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
     SPH_SOFTMAX_CASE(2)
     SPH_SOFTMAX_CASE(3)
     SPH_SOFTMAX_CASE(4)
+    SPH_SOFTMAX_CASE(5)
     default:
       softmax_looped<TI, TO><<<static_cast<unsigned>(rows), 256, 0, st>>>(
           xi, ldx, yo, ldy, rows, cols, scale, flags, qlen, qoff);
@@ -715,6 +719,7 @@ int norm_impl(const void* x, const void* res, const void* w, const void* b,
     SPH_NORM_CASE(2)
     SPH_NORM_CASE(3)
     SPH_NORM_CASE(4)
+    SPH_NORM_CASE(5)
     default:
       norm_looped<T, W, LAYER><<<static_cast<unsigned>(rows), 256, 0, st>>>(
           xi, ri, wi, bi, yo, ho, mean_out, rstd_out, rows, cols, eps);
@@ -784,6 +789,7 @@ int gelu_impl(const void* x, const void* s, const void* b, float s0, float b0,
     SPH_GELU_CASE(2)
     SPH_GELU_CASE(3)
     SPH_GELU_CASE(4)
+    SPH_GELU_CASE(5)
     default:
       gelu_rowsum_looped<T><<<static_cast<unsigned>(rows), 256, 0, st>>>(
           xi, si, bi, s0, b0, yo, ro, rows, cols);
