@@ -415,6 +415,44 @@ def test_gemm_whole_tile_epilogue_and_batch(tb):
     assert_close_fp(out, O.gemm(Ab.numpy(), Bb.numpy()), what="direct-load batched")
 
 
+@pytest.mark.parametrize("batch,m,n,k,pad,epi,dtype", [
+    (1, 2048, 6144, 4096, 0, 0, torch.float16),     # c4 QKV: 256 tiles of 256 x 192
+    (1, 4096, 6144, 512, 8, 2, torch.float16),      # 512 tiles, padded rows, GELU
+    (1, 2048, 6144, 1216, 0, 3, torch.bfloat16),    # bf16, SiLU, 19 K tiles
+    (2, 1024, 6144, 256, 0, 0, torch.float16)])     # batched: 2 x 128 tiles
+def test_gemm_192_wide_tiles(batch, m, n, k, pad, epi, dtype):
+    # K-contiguous B whose 256-wide tiles leave a partial round and whose
+    # 192-wide ones fill whole rounds runs 256 x 192 tiles (8 waves of 128 x
+    # 48): alpha, beta * C (a bias row), activation; with and without a
+    # workspace (the 192-wide tiles take precedence over a split-K tail)
+    _log(f"gemm 192-wide {batch}x{m}x{n}x{k} pad={pad} epi={epi} {dtype}")
+    A = uniform((batch, m, k), k=31, dtype=dtype)
+    W = (uniform((batch, n, k), k=32, dtype=dtype).float() * 0.05).to(dtype)
+    bias = uniform((n,), k=33, dtype=dtype)
+    a_buf = torch.zeros(batch, m, k + pad, dtype=dtype)
+    a_buf[:, :, :k] = A
+    w_buf = torch.zeros(batch, n, k + pad, dtype=dtype)
+    w_buf[:, :, :k] = W
+    ad, wd, bd = a_buf.to(DEV), w_buf.to(DEV), bias.to(DEV)
+    want = O.gemm(A.float().numpy(), np.swapaxes(W.float().numpy(), 1, 2), alpha=0.75, beta=0.5,
+                  c=bias.float().numpy()[None, None, :],
+                  epilogue={0: "none", 2: "gelu", 3: "silu"}[epi])
+    tol = dict(rtol=1e-2, atol=1e-2) if dtype == torch.float16 else dict(rtol=2e-2, atol=2e-2)
+    lib = _capi.lib()
+    nws = lib.sph_gemm_workspace_bytes(1, m, n, k) if batch == 1 else 0
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=DEV)
+    outs = []
+    for w_ptr, w_n in ((None, 0), (_p(ws), nws)):
+        d = torch.empty(batch, m, n, dtype=dtype, device=DEV)
+        _capi.call("sph_gemm_ex", DT[dtype], 0, 1, batch, m, n, k, 0.75, _p(ad), k + pad,
+                   a_buf[0].numel(), _p(wd), k + pad, w_buf[0].numel(), 0.5, _p(bd), 0, 1, 0,
+                   _p(d), n, m * n, epi, w_ptr if w_n else None, w_n, _stream())
+        _sync()
+        assert_close_fp(d, want, out_dtype=dtype, what="192-wide gemm", **tol)
+        outs.append(d)
+    assert torch.equal(outs[0], outs[1]), "the workspace changed the 192-wide result"
+
+
 def test_gemm_bf16_and_unaligned_ld():
     _log("gemm bf16 / unaligned")
     A, B = uniform((70, 45), k=7, dtype=torch.bfloat16), uniform((45, 33), k=8, dtype=torch.bfloat16)

@@ -286,10 +286,10 @@ __device__ inline void store_slab_impl(const GemmArgs& p, const float* slab, T* 
                                        const T* C, int64_t row0, int64_t col0,
                                        int lane) {
   constexpr int LPR = WTN / 8;   // lanes per row
-  constexpr int RPP = 64 / LPR;  // rows per pass
+  constexpr int RPP = 64 / LPR;  // rows per pass (48-wide slabs: 10, lanes 60-63 idle)
   const int er = lane / LPR, ec = (lane % LPR) * 8;
   const int64_t col = col0 + ec;
-  if (col >= p.n) return;
+  if (er >= RPP || col >= p.n) return;
   const bool full_cols = p.vec_d && col + 8 <= p.n;
   const int ncols = p.n - col >= 8 ? 8 : static_cast<int>(p.n - col);
   // Lanes whose 8-column group has bit 3 set read the two 16-byte halves
@@ -686,6 +686,7 @@ __global__ void __launch_bounds__((dl::Cfg<BN_, WTN_>::NT)) gemm_dl_kernel(const
   using DC = Cfg<BN_, WTN_>;
   constexpr int WTN = DC::WTN, TN = DC::TN, NMF = DC::NMF, EPITCH = DC::EPITCH;
   static_assert(!SWIGLU || (B_KCONT && BN_ == 256), "SwiGLU tiles: K-contiguous B, 256 wide");
+  static_assert(B_KCONT || (BN_ / 8) % 16 == 0, "row-major B: the swizzle needs 16-chunk row groups");
   constexpr int BN = DC::BN, WN = DC::WN, STAGE = DC::STAGE, LPA = DC::LPA, LPB = DC::LPB;
   constexpr int NBR = B_KCONT ? 1 : 2;           // LDS reads per B fragment
   constexpr int XB = DC::XB;                     // barrier before this MFMA of the last sub-step
@@ -2044,7 +2045,7 @@ int launch_dl(GemmArgs& p, int64_t batch, bool b_kcont, hipStream_t st,
   constexpr int NTH = dl::Cfg<BN, WTN_>::NT;
   if (b_kcont)
     gemm_dl_kernel<T, true, BN, SWIGLU, WTN_><<<grid, dim3(NTH), 0, st>>>(p);
-  else if constexpr (!SWIGLU)
+  else if constexpr (!SWIGLU && (BN / 8) % 16 == 0)
     gemm_dl_kernel<T, false, BN, false, WTN_><<<grid, dim3(NTH), 0, st>>>(p);
   if (split) {
     constexpr int OUTN = SWIGLU ? BN / 2 : BN;
@@ -2147,6 +2148,13 @@ int gemm_dispatch(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
     const int64_t tn = (p.m / dl::BM) * (p.n / 128) * batch;
     const bool w256 = p.n % 256 == 0 && dl_fits(p, b_kcont, 256) && tw < (1LL << 31);
     const bool w128 = dl_fits(p, b_kcont, 128) && tn < (1LL << 31);
+    // 256 x 192 tiles (8 waves of 128 x 48; K-contiguous B) where they fill
+    // whole rounds of the CUs and 256-wide ones do not (QKV at N = 6144:
+    // 256 tiles in one round instead of 192, or 512 in two instead of 384)
+    const int64_t t192 = p.n % 192 == 0 ? (p.m / dl::BM) * (p.n / 192) * batch : 0;
+    if (b_kcont && t192 > 0 && t192 % kNumCUs == 0 && fill(tw) < 1.0 && dl_fits(p, b_kcont, 192) &&
+        t192 < (1LL << 31))
+      return launch_dl<T, 192, false, 48>(p, batch, b_kcont, st);
     // with a workspace, 256-wide tiles whose last round is split along K
     if (w256 && batch == 1 && p.part != nullptr) {
       const SplitPlan pl = splitk_plan(tw, p.k / dl::BKD, 256);
