@@ -548,7 +548,8 @@ gemm_kernel(const GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// Whole 256x256 tiles with A K-contiguous: direct global -> LDS loads.
+// Whole 256-row tiles (256, 192 or 128 columns) with A K-contiguous: direct
+// global -> LDS loads.
 //
 //   * Each 64-deep K tile moves from memory into LDS with
 //     buffer_load_dwordx4 ... lds: no VGPR staging and no LDS write
@@ -591,7 +592,8 @@ gemm_kernel(const GemmArgs p) {
 //     the stages apart), which would serialise load and compute.  Completion
 //     is awaited explicitly (vmcnt) before the barrier.
 //   * 8 waves (2 x 4, two per SIMD), each owning a 128 x 64 block of 16x16
-//     MFMA tiles; epilogue as in the register-staged kernel.
+//     MFMA tiles (128 x 48 on 192-wide tiles; 4 waves on 128-wide ones);
+//     epilogue as in the register-staged kernel.
 // ---------------------------------------------------------------------------
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -640,10 +642,13 @@ __device__ inline int kslot(int r, int c) { return r * CPR + (c ^ ((r >> 1) & 7)
 __device__ inline int bswz(int k) { return 4 * (k & 3) + 2 * ((k >> 3) & 1); }
 
 // BN = 256 (8 waves, 2 x 4) or 128 (4 waves, 2 x 2) with 128 x 64 wave
-// tiles.  (WTN_ = 128, 128 x 128 wave tiles with 256 accumulator registers,
-// one wave per SIMD on a 256-wide tile, reads a third less from LDS per
-// MFMA but measured 2-3 % slower with 32x32x16 MFMAs: one wave per SIMD
-// hides less of the K-tile barrier and the LDS latency.)
+// tiles, or 192 with WTN_ = 48 (8 waves of 128 x 48, K-contiguous B only).
+// (WTN_ = 128, 128 x 128 wave tiles with 256 accumulator registers, one
+// wave per SIMD on a 256-wide tile, reads a third less from LDS per MFMA
+// but measured slower: 2-3 % with 32x32x16 MFMAs, 30 % with 16x16x32 ones,
+// whose accumulators the compiler then moves between register files inside
+// the loop; one wave per SIMD also hides less of the K-tile barrier and the
+// LDS latency.)
 template <int BN_, int WTN_ = WTN>
 struct Cfg {
   static constexpr int WTN = WTN_, TN = WTN / 16, NMF = TM * TN, EPITCH = WTN + 8;
