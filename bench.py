@@ -847,21 +847,23 @@ def bench_decoder(steps, warmup, c5_layers=40, decode_steps=128):
                                  "HIP graph per step; KV over the full cache"})
     # without the graph (the compiled step called from Python), from position
     # S again: the replays above advanced `pos` to the end of the cache
+    # (at most decode_steps of them: the cache holds S + decode_steps positions)
+    n_side = min(8, decode_steps)
     pos.fill_(S)
     torch.spyre.synchronize()
     t0 = time.perf_counter()
-    for t in range(8):
+    for t in range(n_side):
         lg = dec(feed, pos, params, cos, sin, cache, cfg)
         feed = lg.argmax(-1)
     torch.spyre.synchronize()
-    entry["decode_nograph_wall_ms_per_step"] = round((time.perf_counter() - t0) * 1e3 / 8, 3)
+    entry["decode_nograph_wall_ms_per_step"] = round((time.perf_counter() - t0) * 1e3 / n_side, 3)
     # the eager decode step, for comparison (a few steps)
     torch.spyre.synchronize()
     t0 = time.perf_counter()
-    for t in range(8):
+    for t in range(n_side):
         D.decode_step(feed, S + t, params, cos, sin, cache, cfg)
     torch.spyre.synchronize()
-    entry["decode_eager_wall_ms_per_step"] = round((time.perf_counter() - t0) * 1e3 / 8, 3)
+    entry["decode_eager_wall_ms_per_step"] = round((time.perf_counter() - t0) * 1e3 / n_side, 3)
     out["c5_model"] = entry
     del params, cache
     torch._dynamo.reset()
@@ -1139,6 +1141,8 @@ def main(argv=None):
                     help="summarise rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes under DIR "
                          "(pmc_<part>_<COUNTER>/) into profiles/traffic.json and exit")
     args = ap.parse_args(argv)
+    if args.decode_steps < 1 or args.c5_layers < 1:
+        ap.error("--decode-steps and --c5-layers must be at least 1")
     if args.traffic_from:
         print(json.dumps(summarize_traffic(args.traffic_from, ALGORITHMIC_BYTES), indent=1))
         return 0

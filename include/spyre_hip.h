@@ -236,9 +236,10 @@ int64_t sph_gemm_swiglu_workspace_bytes(int64_t m, int64_t n, int64_t k);
 /* sph_gemm_strided_batched with a workspace (device memory, may be NULL):
  * with at least sph_gemm_workspace_bytes(batch, m, n, k) bytes, a product
  * on whole 256 x 256 tiles whose tile count leaves a partial last round on
- * the 256 CUs splits that round's tiles along K into fp32 partial tiles
+ * the 256 CUs may split that round's tiles along K into fp32 partial tiles
  * (summed and finished with the epilogue by a second kernel) instead of
- * running it on a few CUs.  Same results up to fp32 summation order.  No
+ * running it on a few CUs; the size is 0 for shapes where the library's
+ * time model prefers whole rounds of 256- or 128-wide tiles.  Same results up to fp32 summation order.  No
  * counterpart in the reference (its GEMM is one device call,
  * spyre_torch_ops.cpp:214-293); calls sharing a workspace must be ordered
  * on a stream. */

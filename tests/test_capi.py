@@ -54,3 +54,21 @@ def test_host_side_argument_errors():
     assert lib.sph_gemm_f16(0, 4, 4, None, None, None, None) == 0
     assert lib.sph_softmax_rows_f16(None, None, 0, 8, None) == 0
     assert ctypes.c_int(lib.sph_tri(0, 0, 2, None, None, 0, 4, 4, None)).value == 0
+
+
+@pytest.mark.parametrize("batch,m,n,k,split", [
+    (1, 4096, 4096, 4096, False),    # 256 tiles: one whole round
+    (1, 2048, 4096, 4096, True),     # c4 O: a 2-way split beats 128-wide tiles on cold weights
+    (1, 2048, 4096, 2048, False),    # K = 2048: a round of 128-wide tiles beats the split
+    (1, 2048, 4096, 12800, True),    # c4 down: the split tail beats 128-wide tiles
+    (1, 2048, 25600, 4096, True),    # c4 gate/up: 800 tiles, a 32-tile tail in 8 slices
+    (1, 256, 256, 2048, True),       # one tile in 8 slices
+    (2, 2048, 4096, 12800, False),   # batched: never split
+    (1, 2048, 4096, 1024, False)])   # K < 2048: slices too short
+def test_gemm_workspace_bytes(batch, m, n, k, split):
+    # host-side sizing of the split-K workspace (no device call): nonzero
+    # exactly where the GEMM would split its last round along K
+    got = _capi.lib().sph_gemm_workspace_bytes(batch, m, n, k)
+    assert (got > 0) == split, got
+    if split:
+        assert got % (256 * 256 * 4) == 0 and got <= 256 * 256 * 256 * 4

@@ -453,6 +453,73 @@ def test_gemm_192_wide_tiles(batch, m, n, k, pad, epi, dtype):
     assert torch.equal(outs[0], outs[1]), "the workspace changed the 192-wide result"
 
 
+@pytest.mark.parametrize("batch,m,n,k,tb,pad,epi,dtype", [
+    (1, 2048, 4096, 4096, 1, 0, 0, torch.float16),   # c4 O (no workspace): 256 tiles of 256 x 128
+    (1, 2048, 4096, 4096, 0, 0, 3, torch.bfloat16),  # row-major B, bf16, SiLU
+    (2, 1024, 2048, 1024, 1, 8, 2, torch.float16),   # batched, padded rows, GELU
+    (1, 512, 384, 192, 0, 0, 0, torch.float16)])     # N % 256 != 0: 6 tiles, 3 K tiles
+def test_gemm_128_wide_tiles(batch, m, n, k, tb, pad, epi, dtype):
+    # shapes whose 256-wide tiles leave most CUs idle and that have no
+    # split-K workspace run 256 x 128 tiles (8 waves of 128 x 32): alpha,
+    # beta * C (a bias row), activation
+    _log(f"gemm 128-wide {batch}x{m}x{n}x{k} tb={tb} pad={pad} epi={epi} {dtype}")
+    A = uniform((batch, m, k), k=34, dtype=dtype)
+    ld_b = (k if tb else n) + pad
+    W = (uniform((batch, n, k) if tb else (batch, k, n), k=35, dtype=dtype).float() * 0.05).to(dtype)
+    bias = uniform((n,), k=36, dtype=dtype)
+    a_buf = torch.zeros(batch, m, k + pad, dtype=dtype)
+    a_buf[:, :, :k] = A
+    w_buf = torch.zeros(*W.shape[:2], ld_b, dtype=dtype)
+    w_buf[:, :, :W.shape[2]] = W
+    ad, wd, bd = a_buf.to(DEV), w_buf.to(DEV), bias.to(DEV)
+    wf = W.float().numpy()
+    want = O.gemm(A.float().numpy(), np.swapaxes(wf, 1, 2) if tb else wf, alpha=0.75, beta=0.5,
+                  c=bias.float().numpy()[None, None, :],
+                  epilogue={0: "none", 2: "gelu", 3: "silu"}[epi])
+    tol = dict(rtol=1e-2, atol=1e-2) if dtype == torch.float16 else dict(rtol=2e-2, atol=2e-2)
+    d = torch.empty(batch, m, n, dtype=dtype, device=DEV)
+    _capi.call("sph_gemm_ex", DT[dtype], 0, tb, batch, m, n, k, 0.75, _p(ad), k + pad,
+               a_buf[0].numel(), _p(wd), ld_b, w_buf[0].numel(), 0.5, _p(bd), 0, 1, 0,
+               _p(d), n, m * n, epi, None, 0, _stream())
+    _sync()
+    assert_close_fp(d, want, out_dtype=dtype, what="128-wide gemm", **tol)
+
+
+@pytest.mark.parametrize("m,n,k,c_lay,epi,dtype", [
+    (4096, 4096, 1024, "row", 0, torch.float16),       # 256-wide tiles: 16-byte C reads
+    (1024, 2048, 1024, "row", 3, torch.bfloat16),      # 128-wide tiles, bf16
+    (2048, 6144, 512, "row", 2, torch.float16),        # 192-wide tiles
+    (4096, 4096, 1024, "row_off", 0, torch.float16),   # C rows not 16-byte aligned: per element
+    (512, 2048, 1024, "col", 3, torch.float16),        # column-major C: per element
+    (200, 328, 96, "row", 2, torch.bfloat16)])         # register-staged kernel, ragged tiles
+def test_gemm_full_c_epilogue(m, n, k, c_lay, epi, dtype):
+    # D = epi(alpha A B^T + beta C) with a whole matrix C (a residual): the
+    # epilogue reads row-major, 16-byte aligned C rows 16 bytes a lane ahead
+    # of the stores, other layouts element by element
+    _log(f"gemm full C {m}x{n}x{k} {c_lay} epi={epi} {dtype}")
+    A = uniform((m, k), k=37, dtype=dtype)
+    W = (uniform((n, k), k=38, dtype=dtype).float() * 0.05).to(dtype)
+    Cm = uniform((m, n), k=39, dtype=dtype)
+    ad, wd = A.to(DEV), W.to(DEV)
+    if c_lay == "col":
+        cbuf = Cm.t().contiguous().to(DEV)           # C[i, j] at j * m + i
+        c_ptr, ldc_r, ldc_c = _p(cbuf), 1, m
+    else:
+        off = 1 if c_lay == "row_off" else 0
+        cbuf = torch.zeros(m * n + off, dtype=dtype)
+        cbuf[off:] = Cm.reshape(-1)
+        cbuf = cbuf.to(DEV)
+        c_ptr, ldc_r, ldc_c = _p(cbuf) + off * cbuf.element_size(), n, 1
+    want = O.gemm(A.float().numpy(), W.float().numpy().T, alpha=0.75, beta=0.5,
+                  c=Cm.float().numpy(), epilogue={0: "none", 2: "gelu", 3: "silu"}[epi])
+    d = torch.empty(m, n, dtype=dtype, device=DEV)
+    _capi.call("sph_gemm_ex", DT[dtype], 0, 1, 1, m, n, k, 0.75, _p(ad), k, 0, _p(wd), k, 0,
+               0.5, c_ptr, ldc_r, ldc_c, 0, _p(d), n, 0, epi, None, 0, _stream())
+    _sync()
+    tol = dict(rtol=1e-2, atol=1e-2) if dtype == torch.float16 else dict(rtol=2e-2, atol=2e-2)
+    assert_close_fp(d, want, out_dtype=dtype, what=f"gemm full C ({c_lay})", **tol)
+
+
 def test_gemm_bf16_and_unaligned_ld():
     _log("gemm bf16 / unaligned")
     A, B = uniform((70, 45), k=7, dtype=torch.bfloat16), uniform((45, 33), k=8, dtype=torch.bfloat16)
@@ -560,8 +627,8 @@ def test_gemm_swiglu(m, n, k, pad, dtype):
 
 
 @pytest.mark.parametrize("m,n,k,tb,epi,dtype", [
-    (2048, 4096, 4096, True, 0, torch.float16),    # 128 tiles, 2 K slices (O / down shape)
-    (2048, 4096, 4096, False, 3, torch.bfloat16),  # row-major B, bf16
+    (2048, 4096, 12800, True, 0, torch.float16),   # 128 tiles, 2 K slices (c4 down shape)
+    (1024, 4096, 8192, False, 3, torch.bfloat16),  # row-major B, bf16: 64 tiles, 4 slices
     (768, 512, 2048, False, 2, torch.float16),     # 6 tiles, 8 K slices
     (512, 1024, 12800, True, 0, torch.float16),    # 8 tiles, 200 K tiles in 8 slices
     (256, 256, 2048, True, 3, torch.float16),      # one tile

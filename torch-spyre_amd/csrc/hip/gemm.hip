@@ -280,9 +280,13 @@ __device__ inline void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& 
 // Writes one 32 x WTN slab of fp32 results (LDS, row pitch EPITCH floats)
 // to D rows row0.., columns col0.. as D = epi(alpha * slab + beta * C).
 // Lane l handles columns 8*(l % (WTN/8)) .. +7 of rows l / (WTN/8) + k*RPP.
-// The activation and the C term are resolved outside the row loop.
+// The activation and the C term are resolved outside the row loop.  A
+// row-major C with 16-byte aligned rows (a residual, or a bias row with
+// ldc_row 0) is read 16 bytes a lane, every row of the slab before the
+// first store, so the slab waits for one C load latency instead of one per
+// row (2048 x 4096 x 4096 + residual in 128-wide tiles: 76 -> 64 us).
 template <typename T, int EPI, bool USE_C, int WTN, int EPITCH>
-__device__ inline void store_slab_impl(const GemmArgs& p, const float* slab, T* D,
+__device__ __attribute__((always_inline)) inline void store_slab_impl(const GemmArgs& p, const float* slab, T* D,
                                        const T* C, int64_t row0, int64_t col0,
                                        int lane) {
   constexpr int LPR = WTN / 8;   // lanes per row
@@ -295,10 +299,9 @@ __device__ inline void store_slab_impl(const GemmArgs& p, const float* slab, T* 
   // Lanes whose 8-column group has bit 3 set read the two 16-byte halves
   // in the opposite order, so each LDS read cycle touches 64 distinct banks.
   const int sw = (lane >> 3) & 1;
-#pragma unroll 1
-  for (int rr = er; rr < 32; rr += RPP) {
-    const int64_t row = row0 + rr;
-    if (row >= p.m) break;
+  // one row: cv holds the row's 8 C values as 16 bytes when vec_c (else C
+  // is read element by element, when there is a C term)
+  auto row_out = [&](int rr, int64_t row, u32x4 cv, bool vec_c) __attribute__((always_inline)) {
     const u32x4* sp = reinterpret_cast<const u32x4*>(slab + rr * EPITCH + ec);
     const u32x4 h0 = sp[sw], h1 = sp[sw ^ 1];
     float v[8];
@@ -307,12 +310,27 @@ __device__ inline void store_slab_impl(const GemmArgs& p, const float* slab, T* 
       v[e] = __uint_as_float(sw ? h1[e] : h0[e]);
       v[e + 4] = __uint_as_float(sw ? h0[e] : h1[e]);
     }
+    float cf[8];
+    if constexpr (USE_C) {
+      if (vec_c) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t b16 = (cv[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+          if constexpr (__is_same(T, bf16_t))
+            cf[e] = __uint_as_float(b16 << 16);
+          else
+            cf[e] = static_cast<float>(__builtin_bit_cast(half_t, static_cast<uint16_t>(b16)));
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          cf[e] = e < ncols ? Num<T>::to_f(C[row * p.ldc_row + (col + e) * p.ldc_col]) : 0.f;
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float x = p.alpha * v[e];
-      if constexpr (USE_C) {
-        if (e < ncols) x += p.beta * Num<T>::to_f(C[row * p.ldc_row + (col + e) * p.ldc_col]);
-      }
+      if constexpr (USE_C) x += p.beta * cf[e];
       if constexpr (EPI == SPH_EPI_RELU) x = fmaxf(x, 0.f);
       if constexpr (EPI == SPH_EPI_GELU) x = gelu_erf(x);
       if constexpr (EPI == SPH_EPI_SILU) x = silu(x);
@@ -323,6 +341,31 @@ __device__ inline void store_slab_impl(const GemmArgs& p, const float* slab, T* 
       store8<T>(dp, v);
     else
       store8_partial<T>(dp, ncols, v);
+  };
+  if constexpr (USE_C && sizeof(T) == 2) {
+    if (full_cols && p.ldc_col == 1 && (p.ldc_row & 7) == 0 &&
+        (reinterpret_cast<uintptr_t>(C) & 15) == 0) {
+      constexpr int NR = (32 + RPP - 1) / RPP;  // row passes per slab
+      u32x4 cq[NR];
+#pragma unroll
+      for (int i = 0; i < NR; ++i) {
+        const int rr = er + i * RPP;
+        if (rr < 32 && row0 + rr < p.m)
+          cq[i] = *reinterpret_cast<const u32x4*>(C + (row0 + rr) * p.ldc_row + col);
+      }
+#pragma unroll
+      for (int i = 0; i < NR; ++i) {
+        const int rr = er + i * RPP;
+        if (rr < 32 && row0 + rr < p.m) row_out(rr, row0 + rr, cq[i], true);
+      }
+      return;
+    }
+  }
+#pragma unroll 1
+  for (int rr = er; rr < 32; rr += RPP) {
+    const int64_t row = row0 + rr;
+    if (row >= p.m) break;
+    row_out(rr, row, u32x4{0, 0, 0, 0}, false);
   }
 }
 
@@ -592,7 +635,7 @@ gemm_kernel(const GemmArgs p) {
 //     the stages apart), which would serialise load and compute.  Completion
 //     is awaited explicitly (vmcnt) before the barrier.
 //   * 8 waves (2 x 4, two per SIMD), each owning a 128 x 64 block of 16x16
-//     MFMA tiles (128 x 48 on 192-wide tiles; 4 waves on 128-wide ones);
+//     MFMA tiles (128 x 48 on 192-wide tiles, 128 x 32 on 128-wide ones);
 //     epilogue as in the register-staged kernel.
 // ---------------------------------------------------------------------------
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
@@ -641,8 +684,12 @@ __device__ inline int kslot(int r, int c) { return r * CPR + (c ^ ((r >> 1) & 7)
 // bytes of banks, bit 1 moves the second group's rows to the other half.
 __device__ inline int bswz(int k) { return 4 * (k & 3) + 2 * ((k >> 3) & 1); }
 
-// BN = 256 (8 waves, 2 x 4) or 128 (4 waves, 2 x 2) with 128 x 64 wave
-// tiles, or 192 with WTN_ = 48 (8 waves of 128 x 48, K-contiguous B only).
+// BN = 256 with 128 x 64 wave tiles (8 waves, 2 x 4), 192 with WTN_ = 48
+// (8 waves of 128 x 48, K-contiguous B only) or 128 with WTN_ = 32 (8 waves
+// of 128 x 32).  (128-wide tiles on 4 waves of 128 x 64 measured 20-28 %
+// slower than on 8 of 128 x 32, e.g. 869 against 1074 TFLOP/s at 2048 x
+// 4096 x 4096: with one wave per SIMD the compiler keeps the accumulators in
+// AGPRs and copies each through VGPRs on every K tile.)
 // (WTN_ = 128, 128 x 128 wave tiles with 256 accumulator registers, one
 // wave per SIMD on a 256-wide tile, reads a third less from LDS per MFMA
 // but measured slower: 2-3 % with 32x32x16 MFMAs, 30 % with 16x16x32 ones,
@@ -2034,6 +2081,40 @@ inline SplitPlan splitk_plan(int64_t tiles, int64_t ksteps, int bn) {
   return pl;
 }
 
+// Time model of the direct-load kernel, fitted to fp16 runs on one MI355X
+// (us): a round of 256 x 256 tiles (one per CU) takes ~12 us + 22.4 ns per
+// K column (104 us at K = 4096, 299 us at K = 12800); a split-K tail round
+// the time of its K slice plus ~4 us and the fp32 partials' write and
+// reduce at ~4.2 TB/s (~20 us for the 128 tiles x 2 slices of the c4 O and
+// down shapes); a round of 128-wide tiles (8 waves of 128 x 32, half the
+// MFMAs per K tile, so less time to cover each tile's loads) 0.62 of a
+// 256-wide round with its operands in the caches but 0.78 with operands
+// from HBM, as a model layer's weights are (2048 x 4096 x 4096 + residual:
+// 65 us hot, 86 us cold, against 76 / 80 us split along K; a cold 256-wide
+// round at K = 4096: 109 us).  The model takes the cold figure.
+inline double dl_round_us(int64_t k) { return 12.0 + 0.0224 * static_cast<double>(k); }
+inline double dl_est128(int64_t tiles128, int64_t k) {
+  return static_cast<double>(ceil_div(tiles128, kNumCUs)) * 0.78 * dl_round_us(k);
+}
+inline double dl_est256(int64_t tiles256, int64_t k) {
+  return static_cast<double>(ceil_div(tiles256, kNumCUs)) * dl_round_us(k);
+}
+
+// The split plan for `tiles` 256-wide tiles (batch 1, N % 256 == 0) where
+// the model puts it ahead of whole rounds of 256- and of 128-wide tiles;
+// else a plan of one split (no workspace).
+inline SplitPlan splitk_choice(int64_t tiles, int64_t k) {
+  const SplitPlan pl = splitk_plan(tiles, k / dl::BKD, 256);
+  if (pl.splits <= 1) return pl;
+  const double est = static_cast<double>(pl.tail_start / kNumCUs) * dl_round_us(k) +
+                     dl_round_us(static_cast<int64_t>(pl.kslice) * dl::BKD) + 4.0 +
+                     static_cast<double>(pl.bytes) / 4.2e6;
+  if (est < dl_est256(tiles, k) && est < dl_est128(2 * tiles, k)) return pl;
+  SplitPlan none;
+  none.tail_start = tiles;
+  return none;
+}
+
 // Launches the direct-load kernel (and, with a split plan, the reduce).
 template <typename T, int BN, bool SWIGLU = false, int WTN_ = dl::WTN>
 int launch_dl(GemmArgs& p, int64_t batch, bool b_kcont, hipStream_t st,
@@ -2140,10 +2221,8 @@ int gemm_dispatch(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
     return check_launch("sph_gemm (short K)");
   }
   // Whole 256-row tiles with K-contiguous A run the direct-load kernel, 256
-  // or 128 columns wide: the width whose tile count fills the 256 CUs in
-  // the fewest rounds, 128-wide tiles counted at 0.75 (they run 4 waves, one
-  // per SIMD, and move 1.5x the bytes per FLOP: ~800 against ~1000 TFLOP/s
-  // measured per tile-round).
+  // or 128 columns wide, or 256 wide with the last round split along K:
+  // whichever the time model above puts first.
   if (a_kcont && p.m % dl::BM == 0 && p.k % dl::BKD == 0 && p.k > 0 && p.vec_a && p.vec_b &&
       p.n % 128 == 0) {
     auto fill = [](int64_t tiles) {
@@ -2162,11 +2241,12 @@ int gemm_dispatch(GemmArgs& p, int64_t batch, bool a_kcont, bool b_kcont,
       return launch_dl<T, 192, false, 48>(p, batch, b_kcont, st);
     // with a workspace, 256-wide tiles whose last round is split along K
     if (w256 && batch == 1 && p.part != nullptr) {
-      const SplitPlan pl = splitk_plan(tw, p.k / dl::BKD, 256);
+      const SplitPlan pl = splitk_choice(tw, p.k);
       if (pl.splits > 1 && pl.bytes <= p.part_bytes) return launch_dl<T, 256>(p, batch, b_kcont, st, &pl);
     }
-    if (w256 && (!w128 || fill(tw) >= 0.75 * fill(tn))) return launch_dl<T, 256>(p, batch, b_kcont, st);
-    if (w128) return launch_dl<T, 128>(p, batch, b_kcont, st);
+    if (w256 && (!w128 || dl_est256(tw, p.k) <= dl_est128(tn, p.k)))
+      return launch_dl<T, 256>(p, batch, b_kcont, st);
+    if (w128) return launch_dl<T, 128, false, 32>(p, batch, b_kcont, st);
   }
   const int64_t t256 = ceil_div(p.m, 256) * ceil_div(p.n, 256) * batch;
   const int64_t t128 = ceil_div(p.m, 128) * ceil_div(p.n, 128) * batch;
@@ -2255,7 +2335,7 @@ extern "C" int sph_gemm_strided_batched(
 
 extern "C" int64_t sph_gemm_workspace_bytes(int64_t batch, int64_t m, int64_t n, int64_t k) {
   if (batch != 1 || m % dl::BM != 0 || n % 256 != 0 || k % dl::BKD != 0 || k <= 0) return 0;
-  return splitk_plan((m / dl::BM) * (n / 256), k / dl::BKD, 256).bytes;
+  return splitk_choice((m / dl::BM) * (n / 256), k).bytes;
 }
 
 extern "C" int sph_gemm_ex(sph_dtype dtype, int trans_a, int trans_b, int64_t batch, int64_t m,
