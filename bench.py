@@ -509,14 +509,17 @@ def bench_launch_floor(reps, capi):
     return {"launch_floor": out}
 
 
-# (name, M, N, K, B layout): "nn" = B [K, N] row-major (A @ B), "nt" = B given
-# as a weight [N, K] (A @ W^T, nn.Linear)
+# (name, M, N, K, B layout[, split-K workspace]): "nn" = B [K, N] row-major
+# (A @ B), "nt" = B given as a weight [N, K] (A @ W^T, nn.Linear); the
+# workspace is passed unless the entry says False (then a shape whose
+# 256-wide tiles leave CUs idle runs 256 x 128 tiles)
 YARDSTICK_SHAPES = [
     ("c2 4096^3 A@B", 4096, 4096, 4096, "nn"),
     ("4096^3 A@W^T", 4096, 4096, 4096, "nt"),
     ("8192^3 A@B", 8192, 8192, 8192, "nn"),
     ("c4 QKV 2048x6144x4096", 2048, 6144, 4096, "nt"),
     ("c4 O 2048x4096x4096", 2048, 4096, 4096, "nt"),
+    ("c4 O 2048x4096x4096 without workspace", 2048, 4096, 4096, "nt", False),
     ("c4 gate/up 2048x25600x4096", 2048, 25600, 4096, "nt"),
     ("c4 down 2048x4096x12800", 2048, 4096, 12800, "nt"),
     ("c5 prefill gate/up 4096x25600x4096", 4096, 25600, 4096, "nt"),
@@ -539,12 +542,12 @@ def bench_gemm_yardstick(stream, capi, settle_ms=60.0, time_ms=40.0):
     s = stream.cuda_stream
     timer = Timer(stream)
     out = {}
-    for name, M, N, K, lay in YARDSTICK_SHAPES:
+    for name, M, N, K, lay, *opt in YARDSTICK_SHAPES:
         A = (torch.rand(M, K, generator=_gen(70)) * 2 - 1).half().cuda()
         Bm = (torch.rand(*((N, K) if lay == "nt" else (K, N)), generator=_gen(71)) * 2 - 1)
         Bm = Bm.half().cuda()
         D = torch.empty(M, N, dtype=torch.float16, device="cuda")
-        nws = lib.sph_gemm_workspace_bytes(1, M, N, K)
+        nws = lib.sph_gemm_workspace_bytes(1, M, N, K) if not opt or opt[0] else 0
         ws = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
         tb = 1 if lay == "nt" else 0
         ldb = K if lay == "nt" else N
@@ -552,7 +555,8 @@ def bench_gemm_yardstick(stream, capi, settle_ms=60.0, time_ms=40.0):
         def ours():
             capi.check(lib.sph_gemm_ex(capi.F16, 0, tb, 1, M, N, K, 1.0, A.data_ptr(), K, 0,
                                        Bm.data_ptr(), ldb, 0, 0.0, None, 0, 0, 0, D.data_ptr(),
-                                       N, 0, 0, ws.data_ptr(), nws, s), "sph_gemm_ex")
+                                       N, 0, 0, ws.data_ptr() if nws else None, nws, s),
+                       "sph_gemm_ex")
 
         def theirs():
             return torch.mm(A, Bm.t() if lay == "nt" else Bm)
