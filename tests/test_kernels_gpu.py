@@ -457,6 +457,7 @@ def test_gemm_192_wide_tiles(batch, m, n, k, pad, epi, dtype):
     (1, 2048, 4096, 4096, 1, 0, 0, torch.float16),   # c4 O (no workspace): 256 tiles of 256 x 128
     (1, 2048, 4096, 4096, 0, 0, 3, torch.bfloat16),  # row-major B, bf16, SiLU
     (2, 1024, 2048, 1024, 1, 8, 2, torch.float16),   # batched, padded rows, GELU
+    (3, 512, 1024, 512, 0, 8, 3, torch.bfloat16),    # batched row-major B, bf16
     (1, 512, 384, 192, 0, 0, 0, torch.float16)])     # N % 256 != 0: 6 tiles, 3 K tiles
 def test_gemm_128_wide_tiles(batch, m, n, k, tb, pad, epi, dtype):
     # shapes whose 256-wide tiles leave most CUs idle and that have no
@@ -485,18 +486,21 @@ def test_gemm_128_wide_tiles(batch, m, n, k, tb, pad, epi, dtype):
     assert_close_fp(d, want, out_dtype=dtype, what="128-wide gemm", **tol)
 
 
-@pytest.mark.parametrize("m,n,k,c_lay,epi,dtype", [
-    (4096, 4096, 1024, "row", 0, torch.float16),       # 256-wide tiles: 16-byte C reads
-    (1024, 2048, 1024, "row", 3, torch.bfloat16),      # 128-wide tiles, bf16
-    (2048, 6144, 512, "row", 2, torch.float16),        # 192-wide tiles
-    (4096, 4096, 1024, "row_off", 0, torch.float16),   # C rows not 16-byte aligned: per element
-    (512, 2048, 1024, "col", 3, torch.float16),        # column-major C: per element
-    (200, 328, 96, "row", 2, torch.bfloat16)])         # register-staged kernel, ragged tiles
-def test_gemm_full_c_epilogue(m, n, k, c_lay, epi, dtype):
+@pytest.mark.parametrize("m,n,k,c_lay,epi,dtype,split", [
+    (4096, 4096, 1024, "row", 0, torch.float16, False),      # 256-wide tiles: 16-byte C reads
+    (1024, 2048, 1024, "row", 3, torch.bfloat16, False),     # 128-wide tiles, bf16
+    (2048, 6144, 512, "row", 2, torch.float16, False),       # 192-wide tiles
+    (4096, 4096, 1024, "row_off", 0, torch.float16, False),  # C rows not 16-byte aligned
+    (512, 2048, 1024, "col", 3, torch.float16, False),       # column-major C: per element
+    (200, 328, 96, "row", 2, torch.bfloat16, False),         # register-staged kernel, ragged
+    (768, 512, 2048, "row", 3, torch.float16, True),         # split-K tail: C in the reduce
+    (768, 512, 2048, "col", 2, torch.bfloat16, True)])
+def test_gemm_full_c_epilogue(m, n, k, c_lay, epi, dtype, split):
     # D = epi(alpha A B^T + beta C) with a whole matrix C (a residual): the
     # epilogue reads row-major, 16-byte aligned C rows 16 bytes a lane ahead
-    # of the stores, other layouts element by element
-    _log(f"gemm full C {m}x{n}x{k} {c_lay} epi={epi} {dtype}")
+    # of the stores, other layouts element by element; with a workspace the
+    # split-K reduce applies the same epilogue
+    _log(f"gemm full C {m}x{n}x{k} {c_lay} epi={epi} {dtype} split={split}")
     A = uniform((m, k), k=37, dtype=dtype)
     W = (uniform((n, k), k=38, dtype=dtype).float() * 0.05).to(dtype)
     Cm = uniform((m, n), k=39, dtype=dtype)
@@ -512,9 +516,13 @@ def test_gemm_full_c_epilogue(m, n, k, c_lay, epi, dtype):
         c_ptr, ldc_r, ldc_c = _p(cbuf) + off * cbuf.element_size(), n, 1
     want = O.gemm(A.float().numpy(), W.float().numpy().T, alpha=0.75, beta=0.5,
                   c=Cm.float().numpy(), epilogue={0: "none", 2: "gelu", 3: "silu"}[epi])
+    nws = _capi.lib().sph_gemm_workspace_bytes(1, m, n, k) if split else 0
+    assert (nws > 0) == split
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=DEV)
     d = torch.empty(m, n, dtype=dtype, device=DEV)
     _capi.call("sph_gemm_ex", DT[dtype], 0, 1, 1, m, n, k, 0.75, _p(ad), k, 0, _p(wd), k, 0,
-               0.5, c_ptr, ldc_r, ldc_c, 0, _p(d), n, 0, epi, None, 0, _stream())
+               0.5, c_ptr, ldc_r, ldc_c, 0, _p(d), n, 0, epi, _p(ws) if nws else None, nws,
+               _stream())
     _sync()
     tol = dict(rtol=1e-2, atol=1e-2) if dtype == torch.float16 else dict(rtol=2e-2, atol=2e-2)
     assert_close_fp(d, want, out_dtype=dtype, what=f"gemm full C ({c_lay})", **tol)
